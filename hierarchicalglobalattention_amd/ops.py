@@ -1,0 +1,189 @@
+"""Torch-facing wrappers of the libhga entry points.
+
+Each function takes device tensors, checks shapes/dtypes on the host, and launches the HIP
+kernel on torch's current stream through the C ABI.  There is no CPU path: CPU tensors raise.
+"""
+from __future__ import annotations
+
+import ctypes
+import math
+
+import torch
+
+from . import _lib
+from ._lib import HgaConfig, check, lib
+
+_DT = {torch.float32: _lib.HGA_DTYPE_F32, torch.bfloat16: _lib.HGA_DTYPE_BF16}
+
+
+def mixed_cutoff_pair(theta: float, chunk_size: int, head_dim: int, threshold: float = 0.5,
+                      override=None) -> int:
+    """Number of low-index RoPE pairs whose summary is the plain sum of roped keys
+    (``_mixed_cutoff_pair``, KvRouter/vectorized.py:146-155, chunk_router.py:717-726)."""
+    if override is not None:
+        return int(override)
+    half = head_dim // 2
+    cut = 0
+    for i in range(half):
+        if max(1, chunk_size - 1) * (1.0 / (theta ** (i / half))) > threshold:
+            cut = i + 1
+    return cut
+
+
+def make_config(*, batch, heads, kv_heads, head_dim, chunk_size, group_size, topk_chunks,
+                topk_groups, keep_first, keep_last, cutoff_pair, dtype) -> HgaConfig:
+    """hga_config for one layer call.  ``scale``/``group_scale`` are the fp32 roundings of
+    RouterConfig.scale / group_kv_scale (chunk_router.py:83-90), which is what torch multiplies
+    fp32 and bf16 tensors by."""
+    if dtype not in _DT:
+        raise TypeError(f"unsupported activation dtype {dtype}")
+    c = HgaConfig()
+    c.batch, c.heads, c.kv_heads, c.head_dim = batch, heads, kv_heads, head_dim
+    c.chunk_size, c.group_size = chunk_size, group_size
+    c.topk_chunks, c.topk_groups = topk_chunks, topk_groups
+    c.keep_first, c.keep_last = keep_first, keep_last
+    c.cutoff_pair = cutoff_pair
+    c.dtype = _DT[dtype]
+    c.scale = float(torch.tensor(head_dim ** -0.5, dtype=torch.float32))
+    c.group_scale = float(torch.tensor(1.0 / (group_size + math.sqrt(group_size)),
+                                       dtype=torch.float32))
+    return c
+
+
+def _stream() -> int:
+    return torch.cuda.current_stream().cuda_stream
+
+
+def _dev(*ts):
+    for t in ts:
+        if t is not None and not t.is_cuda:
+            raise RuntimeError("hierarchicalglobalattention_amd runs on the GPU only "
+                               "(got a CPU tensor); there is no CPU fallback")
+
+
+def _p(t):
+    return ctypes.c_void_p(t.data_ptr()) if t is not None else ctypes.c_void_p(0)
+
+
+def _s4(t):
+    """(b, x, s) element strides of a [B, X, S, D] view with a contiguous last dim."""
+    if t.dim() != 4 or t.stride(3) != 1:
+        raise ValueError(f"expected a [B, X, S, D] view with contiguous D, got {tuple(t.shape)} "
+                         f"strides {t.stride()}")
+    return t.stride(0), t.stride(1), t.stride(2)
+
+
+def prefill_widths(cfg: HgaConfig, S: int):
+    n, kc, kg = ctypes.c_int32(), ctypes.c_int32(), ctypes.c_int32()
+    check(lib().hga_prefill_widths(ctypes.byref(cfg), S, ctypes.byref(n), ctypes.byref(kc),
+                                   ctypes.byref(kg)), "hga_prefill_widths")
+    return n.value, kc.value, kg.value
+
+
+def rope(cfg: HgaConfig, x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor,
+         out: torch.Tensor | None = None) -> torch.Tensor:
+    """Rotate-half RoPE of x [B, X, S, Dh] with fp32 tables cos/sin [S, Dh] or [B, S, Dh]."""
+    _dev(x, cos, sin)
+    B, X, S, D = x.shape
+    if out is None:
+        out = torch.empty((B, X, S, D), dtype=x.dtype, device=x.device)
+    cos = cos.contiguous().float()
+    sin = sin.contiguous().float()
+    if cos.shape[-2:] != (S, D):
+        raise ValueError(f"rotary table {tuple(cos.shape)} does not cover [{S}, {D}]")
+    cb = 0 if cos.dim() == 2 or cos.shape[0] == 1 else S * D
+    check(lib().hga_rope(ctypes.byref(cfg), X, S, _p(x), *_s4(x), _p(out), *_s4(out), _p(cos),
+                         _p(sin), cb, _stream()), "hga_rope")
+    return out
+
+
+def summarize(cfg: HgaConfig, k_raw: torch.Tensor, k_rope: torch.Tensor, cos_tab: torch.Tensor,
+              sin_tab: torch.Tensor, pos0: int = 0, chunk_k=None, group_k=None, cos_b=None,
+              sin_b=None, chunk_k_b=None, group_k_b=None):
+    """Chunk/group key summaries of the block k_raw/k_rope [B, KVH, S, Dh] (block token 0 at
+    absolute position pos0).  cos_tab/sin_tab: fp32 [*, Dh] indexed by absolute position.
+    Output tensors (optional) are [B, KVH, N', Dh] and [B, KVH, N', M, Dh] views whose first
+    N = ceil(S/C) chunk slots receive the block's summaries."""
+    _dev(k_raw, k_rope, cos_tab, sin_tab)
+    B, KVH, S, D = k_raw.shape
+    C, gs = cfg.chunk_size, cfg.group_size
+    N, M = (S + C - 1) // C, C // gs
+    if chunk_k is None:
+        chunk_k = torch.empty((B, KVH, N, D), dtype=k_raw.dtype, device=k_raw.device)
+    if group_k is None:
+        group_k = torch.empty((B, KVH, N, M, D), dtype=k_raw.dtype, device=k_raw.device)
+    two = cos_b is not None
+    if two and chunk_k_b is None:
+        chunk_k_b = torch.empty_like(chunk_k)
+        group_k_b = torch.empty_like(group_k)
+    for t in (chunk_k, group_k) + ((chunk_k_b, group_k_b) if two else ()):
+        if t.stride(-1) != 1:
+            raise ValueError("summary outputs need a contiguous head dim")
+    if chunk_k.stride(2) != D or group_k.stride(3) != D or group_k.stride(2) != M * D:
+        raise ValueError("summary outputs must be chunk-contiguous")
+    if two and (chunk_k_b.stride() != chunk_k.stride() or group_k_b.stride() != group_k.stride()):
+        raise ValueError("second summary outputs must share the first ones' strides")
+    cos_tab, sin_tab = cos_tab.contiguous().float(), sin_tab.contiguous().float()
+    for tab in (cos_tab, sin_tab) + ((cos_b, sin_b) if two else ()):
+        if tab.dim() != 2 or tab.shape[1] != D or tab.shape[0] < pos0 + S:
+            raise ValueError(f"rotary table {tuple(tab.shape)} must be [>= {pos0 + S}, {D}]")
+    if chunk_k.shape[2] < N or group_k.shape[2] < N:
+        raise ValueError("summary outputs have fewer chunk slots than the block")
+    if two:
+        cos_b, sin_b = cos_b.contiguous().float(), sin_b.contiguous().float()
+    check(lib().hga_summarize(
+        ctypes.byref(cfg), S, pos0, _p(k_raw), *_s4(k_raw), _p(k_rope), *_s4(k_rope),
+        _p(cos_tab), _p(sin_tab), _p(chunk_k), chunk_k.stride(0), chunk_k.stride(1),
+        _p(group_k), group_k.stride(0), group_k.stride(1), _p(cos_b if two else None),
+        _p(sin_b if two else None), _p(chunk_k_b if two else None),
+        _p(group_k_b if two else None), _stream()), "hga_summarize")
+    if two:
+        return chunk_k, group_k, chunk_k_b, group_k_b
+    return chunk_k, group_k
+
+
+def route_prefill(cfg: HgaConfig, q: torch.Tensor, chunk_k: torch.Tensor,
+                  group_k: torch.Tensor, S: int | None = None, canonical: bool = False,
+                  stats: torch.Tensor | None = None) -> dict:
+    """Two-level routing of a fresh prefill block.  Returns int32 tensors
+    sel_chunk/sel_thr [B,H,N,Kc], n_sel [B,H,N], open_grp/open_thr [B,H,N,Kg], n_open [B,H,N]
+    (widths at least 1)."""
+    _dev(q, chunk_k, group_k)
+    B, H, Sq, D = q.shape
+    S = Sq if S is None else S
+    N, Kc, Kg = prefill_widths(cfg, S)
+    dev = q.device
+    r = dict(sel_chunk=torch.empty((B, H, N, max(Kc, 1)), dtype=torch.int32, device=dev),
+             sel_thr=torch.empty((B, H, N, max(Kc, 1)), dtype=torch.int32, device=dev),
+             n_sel=torch.empty((B, H, N), dtype=torch.int32, device=dev),
+             open_grp=torch.empty((B, H, N, max(Kg, 1)), dtype=torch.int32, device=dev),
+             open_thr=torch.empty((B, H, N, max(Kg, 1)), dtype=torch.int32, device=dev),
+             n_open=torch.empty((B, H, N), dtype=torch.int32, device=dev))
+    if chunk_k.stride(-1) != 1 or chunk_k.stride(2) != D or group_k.stride(3) != D or \
+            group_k.stride(2) != group_k.shape[3] * D:
+        raise ValueError("summaries must be chunk-contiguous with a contiguous head dim")
+    flags = _lib.HGA_ROUTE_CANONICAL if canonical else 0
+    check(lib().hga_route_prefill(
+        ctypes.byref(cfg), S, _p(q), *_s4(q), _p(chunk_k), chunk_k.stride(0), chunk_k.stride(1),
+        _p(group_k), group_k.stride(0), group_k.stride(1), _p(r["sel_chunk"]), _p(r["sel_thr"]),
+        _p(r["n_sel"]), _p(r["open_grp"]), _p(r["open_thr"]), _p(r["n_open"]), flags,
+        _p(stats), _stream()), "hga_route_prefill")
+    r["Kc"], r["Kg"] = Kc, Kg
+    return r
+
+
+def attend_prefill(cfg: HgaConfig, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
+                   open_grp: torch.Tensor, open_thr: torch.Tensor, Kg: int,
+                   out: torch.Tensor | None = None) -> torch.Tensor:
+    """Exact attention of q [B,H,S,Dh] over the routed working set (RoPE'd k and v
+    [B,KVH,S,Dh]); returns out [B,H,S,Dh] in q's dtype."""
+    _dev(q, k, v, open_grp, open_thr)
+    B, H, S, D = q.shape
+    if out is None:
+        out = torch.empty((B, H, S, D), dtype=q.dtype, device=q.device)
+    og = open_grp.contiguous()
+    ot = open_thr.contiguous()
+    check(lib().hga_attend_prefill(
+        ctypes.byref(cfg), S, _p(q), *_s4(q), _p(k), *_s4(k), _p(v), *_s4(v), _p(og), _p(ot),
+        Kg, _p(out), *_s4(out), _stream()), "hga_attend_prefill")
+    return out

@@ -1,0 +1,138 @@
+/*
+ * hga.h -- C ABI of the MI355X (gfx950) routed exact-token attention library (libhga.so).
+ *
+ * Each entry point replaces one step of the reference's HierarchicalGlobalAttentionRouted path
+ * (vfedosov77/HierarchicalGlobalAttention, ExistingModelFineTuning/); the reference location is
+ * cited on each declaration.  All data pointers are device memory owned by the caller unless a
+ * comment says otherwise; no entry point allocates device memory.  Activations are laid out as
+ * 4-D views [B, X, S, Dh] with the head dimension contiguous and explicit element strides for
+ * (b, x, s).  Every call is asynchronous on `stream` (a hipStream_t; NULL = default stream) and
+ * returns HGA_OK or a negative code; hga_last_error() then describes the failure (per thread).
+ */
+#ifndef HGA_H
+#define HGA_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum { HGA_DTYPE_F32 = 0, HGA_DTYPE_BF16 = 1 };
+
+enum {
+    HGA_OK = 0,
+    HGA_ERR_ARG = -1,         /* invalid argument / shape */
+    HGA_ERR_UNSUPPORTED = -2, /* valid but outside what the kernels implement */
+    HGA_ERR_LAUNCH = -3,      /* HIP launch / runtime error */
+};
+
+/* Router flags */
+enum {
+    HGA_ROUTE_CANONICAL = 1, /* score every candidate with the canonical fp32 FMA chain
+                                (no MFMA pre-pass); slower, same result */
+};
+
+/* Layer configuration; mirrors RouterConfig + ChunkPlacementPolicy
+ * (KvRouter/chunk_router.py:58-90, KvRouter/chunk_placement_policy.py:12-38). */
+typedef struct hga_config {
+    int32_t batch;       /* B */
+    int32_t heads;       /* H, query heads */
+    int32_t kv_heads;    /* KVH; heads % kv_heads == 0, query head h reads KV head h/(H/KVH) */
+    int32_t head_dim;    /* Dh: 16, 32, 64 or 128 */
+    int32_t chunk_size;  /* C <= 64 */
+    int32_t group_size;  /* gs; C % gs == 0 */
+    int32_t topk_chunks; /* 0 disables routing */
+    int32_t topk_groups; /* 0 disables group opening */
+    int32_t keep_first;  /* sink window, token level (first_token_level=True) */
+    int32_t keep_last;   /* local window */
+    int32_t cutoff_pair; /* mixed-RoPE: pairs [0, cutoff) are summed token-wise */
+    int32_t dtype;       /* HGA_DTYPE_* of q/k/v and summaries */
+    float scale;         /* head_dim ** -0.5 rounded to fp32 */
+    float group_scale;   /* 1 / (gs + sqrt(gs)) rounded to fp32 */
+} hga_config;
+
+/* Library version (major*10000 + minor*100 + patch). */
+int32_t hga_version(void);
+
+/* Text of the last error on this thread ("" if none). */
+const char* hga_last_error(void);
+
+/* Widths of the routing outputs for a prefill block of S tokens at position 0:
+ * N = ceil(S/C), Kc = min(topk_chunks, N) (0 if disabled), Kg = min(topk_groups, Kc*C/gs).
+ * Replaces the size logic of vectorized.py:233-240, 304, 345, 365. */
+int32_t hga_prefill_widths(const hga_config* cfg, int32_t S, int32_t* N, int32_t* Kc,
+                           int32_t* Kg);
+
+/*
+ * Rotate-half RoPE in fp32, rounded to the activation dtype:
+ *   out = x*cos + cat(-x2, x1)*sin    (HierarchicalGlobalAttentionRouted.py:156-157, 219-223)
+ * x/out: [B, nheads, S, Dh] views; cos/sin: fp32 [Bc, S, Dh] rows of the rotary table for the
+ * block's positions, cos_bstride = 0 (shared) or the batch stride in elements.
+ */
+int hga_rope(const hga_config* cfg, int32_t nheads, int32_t S, const void* x, int64_t x_sb,
+             int64_t x_sh, int64_t x_ss, void* out, int64_t o_sb, int64_t o_sh, int64_t o_ss,
+             const float* cos, const float* sin, int64_t cos_bstride, void* stream);
+
+/*
+ * Mixed-RoPE chunk and group key summaries at KV-head granularity
+ * (vectorized._rope_summary, vectorized.py:146-183, as applied at :265-287; the store twin
+ * ChunkRouter._rope_summary_at, chunk_router.py:575-585, 631-652, 693-735).
+ * k_raw/k_rope: [B, KVH, S, Dh] views of the block (block token 0 at absolute position pos0,
+ * a multiple of C).  cos_tab/sin_tab: fp32 [*, Dh] tables indexed by absolute position
+ * (pos0 + local anchor).  Writes chunk n of the block to
+ *   chunk_k + b*ck_sb + h*ck_sh + n*Dh            (dtype, [.., N, Dh])
+ *   group_k + b*gk_sb + h*gk_sh + (n*M + m)*Dh     (dtype, [.., N, M, Dh])
+ * The optional second table/output pair (cos_b, sin_b, chunk_k_b, group_k_b; all NULL or all
+ * set, same strides) receives the same summaries with a second anchor table (the reference
+ * routes with the activation-dtype table and seeds its store with the fp32 one).
+ */
+int hga_summarize(const hga_config* cfg, int32_t S, int64_t pos0, const void* k_raw,
+                  int64_t kr_sb, int64_t kr_sh, int64_t kr_ss, const void* k_rope, int64_t kp_sb,
+                  int64_t kp_sh, int64_t kp_ss, const float* cos_tab, const float* sin_tab,
+                  void* chunk_k, int64_t ck_sb, int64_t ck_sh, void* group_k, int64_t gk_sb,
+                  int64_t gk_sh, const float* cos_b, const float* sin_b, void* chunk_k_b,
+                  void* group_k_b, void* stream);
+
+/*
+ * Two-level prefill routing for a fresh block starting at position 0
+ * (vectorized.py:242-396: windows, stage-1 chunk routing with per-row requests, pooled max,
+ * forced previous chunk, cumsum visibility; stage-2 group routing).  Canonical semantics:
+ * scores are the fp32 FMA chain over Dh times `scale`, ties go to the lower absolute index.
+ * q: [B, H, S, Dh] view (RoPE applied).  chunk_k/group_k: summaries as hga_summarize writes
+ * them.  Outputs (contiguous int32, ascending ids, -1 padded):
+ *   sel_chunk, sel_thr [B, H, N, Kc]   routed chunk id and first query row (chunk-local) that
+ *                                      sees it; n_sel [B, H, N]
+ *   open_grp, open_thr [B, H, N, Kg]   opened group id (chunk*M + group) and first row;
+ *                                      n_open [B, H, N]
+ * Widths from hga_prefill_widths (a zero width still needs 1-element arrays).
+ * stats: NULL or int32[4] device counters, incremented by the number of rows whose MFMA
+ * pre-pass could not certify the selection and were re-ranked canonically
+ * ([0] stage-1 rows, [1] stage-1 pooled, [2] stage-2 rows, [3] stage-2 pooled).
+ */
+int hga_route_prefill(const hga_config* cfg, int32_t S, const void* q, int64_t q_sb,
+                      int64_t q_sh, int64_t q_ss, const void* chunk_k, int64_t ck_sb,
+                      int64_t ck_sh, const void* group_k, int64_t gk_sb, int64_t gk_sh,
+                      int32_t* sel_chunk, int32_t* sel_thr, int32_t* n_sel, int32_t* open_grp,
+                      int32_t* open_thr, int32_t* n_open, int32_t flags, int32_t* stats,
+                      void* stream);
+
+/*
+ * Exact attention over the routed working set of a prefill block (the assembly of
+ * vectorized.py:404-490 and RoutedKV.attend, chunk_router.py:149-158, fused; nothing is
+ * materialised).  Row t of query chunk n attends to: its own chunk's tokens <= t, the
+ * keep_first and keep_last windows, and every opened group with open_thr <= t.
+ * q/out: [B, H, S, Dh]; k/v: [B, KVH, S, Dh] (RoPE'd keys).  open_grp/open_thr as written by
+ * hga_route_prefill (width Kg; Kg = 0 with 1-element arrays when routing is off).
+ */
+int hga_attend_prefill(const hga_config* cfg, int32_t S, const void* q, int64_t q_sb,
+                       int64_t q_sh, int64_t q_ss, const void* k, int64_t k_sb, int64_t k_sh,
+                       int64_t k_ss, const void* v, int64_t v_sb, int64_t v_sh, int64_t v_ss,
+                       const int32_t* open_grp, const int32_t* open_thr, int32_t Kg, void* out,
+                       int64_t o_sb, int64_t o_sh, int64_t o_ss, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* HGA_H */
