@@ -95,9 +95,16 @@ __device__ uint32_t exact_topk(const uint32_t (&kv)[J], int k) {
     if (count_ge<J>(kv, hi) >= k) {
         vstar = hi;
     } else {
-        // invariant: count_ge(lo) > k... >= k, count_ge(hi) < k
+        // invariant: count_ge(lo) > k, count_ge(hi) < k.  The first steps bisect the float
+        // values (fast for smooth score distributions), then the key space (terminates).
+        int it = 0;
         while (hi - lo > 1u) {
-            const uint32_t mid = lo + (hi - lo) / 2u;
+            uint32_t mid = lo + (hi - lo) / 2u;
+            if (it++ < 16) {
+                const float lf = okey_inv(lo), hf = okey_inv(hi);
+                const uint32_t fm = okey(lf + (hf - lf) * 0.5f);
+                if (fm > lo && fm < hi) mid = fm;
+            }
             const int c = count_ge<J>(kv, mid);
             if (c == k) {
 #pragma unroll
@@ -168,24 +175,42 @@ __device__ uint32_t select_certified(const float (&v)[J], int k, float delta, Ca
 // ------------------------------------------------------------------------------------------
 // scores
 // ------------------------------------------------------------------------------------------
+// Canonical score: sequential fp32 FMA chain over d = 0..DH-1, then * scale (-0 -> +0).
+// q comes from LDS, k from global; both are read with 16-byte vector loads, the chain order is
+// unchanged.
 template <int DT, int DH>
-__device__ __forceinline__ float canon_dot(const typename Elem<DT>::T* q,
-                                           const typename Elem<DT>::T* k, float scale) {
+__device__ __noinline__ float canon_dot(const typename Elem<DT>::T* q,
+                                        const typename Elem<DT>::T* k, float scale) {
     float acc = 0.0f;
-#pragma unroll 8
-    for (int d = 0; d < DH; ++d) acc = fmaf(Elem<DT>::ld(q, d), Elem<DT>::ld(k, d), acc);
+    if constexpr (DT == HGA_DTYPE_BF16) {
+        uint4 kr[DH / 8];
+#pragma unroll
+        for (int i = 0; i < DH / 8; ++i) kr[i] = *reinterpret_cast<const uint4*>(k + 8 * i);
+#pragma unroll
+        for (int i = 0; i < DH / 8; ++i) {
+            const uint4 qq = *reinterpret_cast<const uint4*>(q + 8 * i);
+            const uint32_t qw[4] = {qq.x, qq.y, qq.z, qq.w}, kw[4] = {kr[i].x, kr[i].y, kr[i].z, kr[i].w};
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                acc = fmaf(__uint_as_float(qw[e] << 16), __uint_as_float(kw[e] << 16), acc);
+                acc = fmaf(__uint_as_float(qw[e] & 0xffff0000u), __uint_as_float(kw[e] & 0xffff0000u), acc);
+            }
+        }
+    } else {
+        float4 kr[DH / 4];
+#pragma unroll
+        for (int i = 0; i < DH / 4; ++i) kr[i] = *reinterpret_cast<const float4*>(k + 4 * i);
+#pragma unroll
+        for (int i = 0; i < DH / 4; ++i) {
+            const float4 qq = *reinterpret_cast<const float4*>(q + 4 * i);
+            acc = fmaf(qq.x, kr[i].x, acc);
+            acc = fmaf(qq.y, kr[i].y, acc);
+            acc = fmaf(qq.z, kr[i].z, acc);
+            acc = fmaf(qq.w, kr[i].w, acc);
+        }
+    }
     const float s = acc * scale;
     return s == 0.0f ? 0.0f : s;
-}
-
-// Canonical scores of all (row, candidate) pairs.  rowptr(i) -> candidate i's summary row.
-template <int DT, int DH, class RowPtr>
-__device__ void scores_canonical(const typename Elem<DT>::T* sQ, int rows, int ncand,
-                                 RowPtr rowptr, float* sS, int SP, float scale) {
-    for (int idx = threadIdx.x; idx < rows * ncand; idx += kThreads) {
-        const int t = idx / ncand, c = idx % ncand;
-        sS[t * SP + c] = canon_dot<DT, DH>(sQ + t * DH, rowptr(c), scale);
-    }
 }
 
 __device__ __forceinline__ bf16x8 as_bf16x8(uint4 u) { return __builtin_bit_cast(bf16x8, u); }
@@ -204,7 +229,7 @@ __device__ __forceinline__ float sumsq_bf16x8(uint4 u) {
 
 // bf16 MFMA scores (scaled) of all rows against all candidates, plus candidate norms.
 // Wave w handles candidate tiles w, w+8, ... of 32 candidates; both 32-row blocks.
-template <int DH, class RowPtr>
+template <int DH, int QS, class RowPtr>
 __device__ void scores_mfma(const uint16_t* sQ, int rows, int ncand, RowPtr rowptr, float* sS,
                             int SP, float* sKn, float scale) {
     constexpr int KS = DH / 16;
@@ -214,21 +239,25 @@ __device__ void scores_mfma(const uint16_t* sQ, int rows, int ncand, RowPtr rowp
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
         const int col = ks * 16 + 8 * (l / 32);
-        a0[ks] = as_bf16x8(*reinterpret_cast<const uint4*>(sQ + (l % 32) * DH + col));
-        a1[ks] = as_bf16x8(*reinterpret_cast<const uint4*>(sQ + (32 + l % 32) * DH + col));
+        a0[ks] = as_bf16x8(*reinterpret_cast<const uint4*>(sQ + (l % 32) * QS + col));
+        a1[ks] = as_bf16x8(*reinterpret_cast<const uint4*>(sQ + (32 + l % 32) * QS + col));
     }
     for (int ct = w; ct * 32 < ncand; ct += kWaves) {
         const int c = ct * 32 + l % 32;
         const bool cv = c < ncand;
         const uint16_t* kp = cv ? rowptr(c) : nullptr;
+        uint4 u[KS];
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) {
+            u[ks] = make_uint4(0u, 0u, 0u, 0u);
+            if (cv) u[ks] = *reinterpret_cast<const uint4*>(kp + ks * 16 + 8 * (l / 32));
+        }
         floatx16 acc0 = {}, acc1 = {};
         float nsq = 0.0f;
 #pragma unroll
         for (int ks = 0; ks < KS; ++ks) {
-            uint4 u = make_uint4(0u, 0u, 0u, 0u);
-            if (cv) u = *reinterpret_cast<const uint4*>(kp + ks * 16 + 8 * (l / 32));
-            nsq += sumsq_bf16x8(u);
-            const bf16x8 bv = as_bf16x8(u);
+            nsq += sumsq_bf16x8(u[ks]);
+            const bf16x8 bv = as_bf16x8(u[ks]);
             acc0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0[ks], bv, acc0, 0, 0, 0);
             if (nrb > 1) acc1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1[ks], bv, acc1, 0, 0, 0);
         }
@@ -245,17 +274,150 @@ __device__ void scores_mfma(const uint16_t* sQ, int rows, int ncand, RowPtr rowp
     }
 }
 
+template <int J>
+struct JTag {
+    static constexpr int value = J;
+};
+// Calls f(JTag<J>) with the smallest J such that 64*J >= n (wave-uniform n).
+template <class F>
+__device__ __forceinline__ void dispatch_j(int n, F&& f) {
+    if (n <= 64) f(JTag<1>{});
+    else if (n <= 128) f(JTag<2>{});
+    else if (n <= 256) f(JTag<4>{});
+    else f(JTag<8>{});
+}
+
+// Per-row top-k requests for rows w, w+8, ...: every member (row t, candidate i) raises the
+// candidate's pooled key to okey(score), lowers its first row to t, and sets bit (t, i).
+template <int J, class Vis, class Canon>
+__device__ void row_requests(const float* sS, int SP, int rows, int ncand, int k, Vis visible,
+                             const float* sQn, float dscale, Canon canon_row, uint32_t* sPk,
+                             int* sFirst, uint32_t* sBits, int BW, int* amb) {
+    const int w = threadIdx.x / kWave, l = lane_id();
+    for (int t = w; t < rows; t += kWaves) {
+        float v[J];
+#pragma unroll
+        for (int j = 0; j < J; ++j) {
+            const int i = l + 64 * j;
+            v[j] = (i < ncand && visible(t, i)) ? sS[t * SP + i] : -INFINITY;
+        }
+        const float delta = dscale * sQn[t];
+        const uint32_t mem = select_certified<J>(
+            v, k, delta, [&](int i) { return canon_row(t, i); }, amb);
+#pragma unroll
+        for (int j = 0; j < J; ++j) {
+            const bool m = (mem >> j) & 1u;
+            if (m) {
+                const int i = l + 64 * j;
+                atomicMax(&sPk[i], okey(v[j]));
+                atomicMin(&sFirst[i], t);
+            }
+            const uint64_t bal = __ballot(m);
+            if (l == 0 && 64 * j < SP) {
+                sBits[t * BW + 2 * j] = (uint32_t)bal;
+                if (2 * j + 1 < BW) sBits[t * BW + 2 * j + 1] = (uint32_t)(bal >> 32);
+            }
+        }
+    }
+}
+
+// Canonical pooled value of candidate i: max over requesting rows whose approximate score can
+// still be the maximum (within 2*dpool of the approximate pooled max).
+template <class Canon>
+__device__ float pooled_exact(int i, int rows, const float* sS, int SP, const uint32_t* sBits,
+                              int BW, const uint32_t* sPk, float dpool, Canon canon_row) {
+    const float pt = okey_inv(sPk[i]) - 2.0f * dpool;
+    float best = -INFINITY;
+    for (int t = 0; t < rows; ++t) {
+        if (!((sBits[t * BW + i / 32] >> (i % 32)) & 1u)) continue;
+        if (sS[t * SP + i] < pt) continue;
+        best = fmaxf(best, canon_row(t, i));
+    }
+    return best;
+}
+
+// Wave 0: top-k of the requested candidates by pooled score (certified), optional forced
+// candidate `ip` (evicting the last-ranked one when full), written ascending to sSel/sThr with
+// ids base + i; returns the count (wave-uniform).
+template <int J, class Canon>
+__device__ int pooled_select(int ncand, int k, int rows, const float* sS, int SP,
+                             const uint32_t* sBits, int BW, const uint32_t* sPk,
+                             const int* sFirst, float dpool, Canon canon_row, int ip, int base_id,
+                             int* sSel, int* sThr, int* amb) {
+    const int l = lane_id();
+    float v[J];
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+        const int i = l + 64 * j;
+        v[j] = (i < ncand && sFirst[i] < kNoRow) ? okey_inv(sPk[i]) : -INFINITY;
+    }
+    auto canon_pool = [&](int i) {
+        return pooled_exact(i, rows, sS, SP, sBits, BW, sPk, dpool, canon_row);
+    };
+    uint32_t sel = select_certified<J>(v, k, dpool, canon_pool, amb);
+    if (ip >= 0) {
+        const bool have = __ballot(((sel >> (ip / 64)) & 1u) && l == ip % 64) != 0;
+        if (!have) {
+            int nsel = 0;
+#pragma unroll
+            for (int j = 0; j < J; ++j) nsel += __popcll(__ballot((sel >> j) & 1u));
+            if (nsel >= k) {
+                // evict the last-ranked selected candidate: lowest pooled, then highest id
+                float mn = INFINITY;
+#pragma unroll
+                for (int j = 0; j < J; ++j)
+                    if ((sel >> j) & 1u) mn = fminf(mn, v[j]);
+                mn = wave_min(mn);
+                uint32_t ev[J];
+#pragma unroll
+                for (int j = 0; j < J; ++j) {
+                    const bool cand = ((sel >> j) & 1u) && v[j] <= mn + 2.0f * dpool;
+                    const float e = cand ? (dpool > 0.0f ? canon_pool(l + 64 * j) : v[j]) : 0.0f;
+                    ev[j] = cand ? ~okey(e) : 0u;
+                }
+                uint32_t best = 0u;
+#pragma unroll
+                for (int j = 0; j < J; ++j) best = max(best, ev[j]);
+                best = wave_max_u(best);
+                int victim = -1;
+#pragma unroll
+                for (int j = J - 1; j >= 0; --j) {
+                    const uint64_t m = __ballot(ev[j] == best && best != 0u);
+                    if (victim < 0 && m) victim = 64 * j + 63 - __clzll(m);
+                }
+                if (victim >= 0 && l == victim % 64) sel &= ~(1u << (victim / 64));
+            }
+            if (l == ip % 64) sel |= 1u << (ip / 64);
+        }
+    }
+    int base = 0;
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+        const bool m = (sel >> j) & 1u;
+        const uint64_t bal = __ballot(m);
+        if (m) {
+            const int i = l + 64 * j;
+            const int pos = base + lanes_below(bal);
+            sSel[pos] = base_id + i;
+            sThr[pos] = i == ip ? 0 : sFirst[i];
+        }
+        base += __popcll(bal);
+    }
+    return base;
+}
+
 // ------------------------------------------------------------------------------------------
 // the kernel
 // ------------------------------------------------------------------------------------------
 template <int DT, int DH>
 __global__ __launch_bounds__(kThreads) void route_prefill_kernel(RouteArgs A) {
     typedef typename Elem<DT>::T T;
+    constexpr int QS = DH + 8;   // padded LDS row stride of the query tile
     extern __shared__ __align__(16) unsigned char smem_raw[];
     const int SP = A.SP, BW = A.BW;
     float* sS = reinterpret_cast<float*>(smem_raw);                 // [64][SP]
-    T* sQ = reinterpret_cast<T*>(sS + kRows * SP);                   // [64][DH]
-    float* sKn = reinterpret_cast<float*>(sQ + kRows * DH);          // [SP]
+    T* sQ = reinterpret_cast<T*>(sS + kRows * SP);                   // [64][QS]
+    float* sKn = reinterpret_cast<float*>(sQ + kRows * QS);          // [SP]
     float* sQn = sKn + SP;                                           // [64]
     uint32_t* sPk = reinterpret_cast<uint32_t*>(sQn + kRows);        // [SP] pooled key
     int* sFirst = reinterpret_cast<int*>(sPk + SP);                  // [SP]
@@ -263,6 +425,7 @@ __global__ __launch_bounds__(kThreads) void route_prefill_kernel(RouteArgs A) {
     int* sSel = reinterpret_cast<int*>(sBits + kRows * BW);          // [kMaxSel] sorted chunk ids
     int* sThr = sSel + kMaxSel;                                      // [kMaxSel]
     int* sScal = sThr + kMaxSel;                                     // [8] scalars
+    // Stage-2 group selections can be up to Kc*M long; they are emitted straight to global.
 
     const int N = A.N, C = A.C, M = A.M;
     const int n = N - 1 - (int)(blockIdx.x / (A.B * A.H));          // heavy chunks first
@@ -293,11 +456,14 @@ __global__ __launch_bounds__(kThreads) void route_prefill_kernel(RouteArgs A) {
 
     // ---- query rows -> LDS (rows >= `rows` zero), row norms --------------------------------
     {
+        constexpr int VE = 16 / (int)sizeof(T);   // elements per 16-byte vector
         const T* qb = reinterpret_cast<const T*>(A.q) + b * A.q_sb + h * A.q_sh +
                       (int64_t)n * C * A.q_ss;
-        for (int idx = threadIdx.x; idx < kRows * DH; idx += kThreads) {
-            const int t = idx / DH, d = idx % DH;
-            sQ[idx] = t < rows ? qb[(int64_t)t * A.q_ss + d] : (T)0;
+        for (int idx = threadIdx.x; idx < kRows * (DH / VE); idx += kThreads) {
+            const int t = idx / (DH / VE), d = (idx % (DH / VE)) * VE;
+            uint4 u = make_uint4(0u, 0u, 0u, 0u);
+            if (t < rows) u = *reinterpret_cast<const uint4*>(qb + (int64_t)t * A.q_ss + d);
+            *reinterpret_cast<uint4*>(sQ + t * QS + d) = u;
         }
     }
     for (int i = threadIdx.x; i < SP; i += kThreads) {
@@ -309,7 +475,7 @@ __global__ __launch_bounds__(kThreads) void route_prefill_kernel(RouteArgs A) {
     for (int t = w; t < kRows; t += kWaves) {
         float s = 0.0f;
         for (int d = l; d < DH; d += kWave) {
-            const float x = Elem<DT>::ld(sQ, t * DH + d);
+            const float x = Elem<DT>::ld(sQ, t * QS + d);
             s = fmaf(x, x, s);
         }
         s = wave_sum(s);
@@ -319,12 +485,14 @@ __global__ __launch_bounds__(kThreads) void route_prefill_kernel(RouteArgs A) {
     // ---- stage 1 scores ----------------------------------------------------------------------
     const T* ckb = reinterpret_cast<const T*>(A.ck) + b * A.ck_sb + kvh * A.ck_sh;
     auto crow = [&](int i) -> const T* { return ckb + (int64_t)(f_hi + i) * DH; };
+    auto canon1 = [&](int t, int i) { return canon_dot<DT, DH>(sQ + t * QS, crow(i), scale); };
     if (use_mfma)
-        scores_mfma<DH>(reinterpret_cast<const uint16_t*>(sQ), rows, P,
-                        [&](int i) { return reinterpret_cast<const uint16_t*>(crow(i)); }, sS, SP,
-                        sKn, scale);
+        scores_mfma<DH, QS>(reinterpret_cast<const uint16_t*>(sQ), rows, P,
+                            [&](int i) { return reinterpret_cast<const uint16_t*>(crow(i)); },
+                            sS, SP, sKn, scale);
     else
-        scores_canonical<DT, DH>(sQ, rows, P, crow, sS, SP, scale);
+        for (int idx = threadIdx.x; idx < rows * P; idx += kThreads)
+            sS[(idx / P) * SP + idx % P] = canon1(idx / P, idx % P);
     __syncthreads();
     float knmax = 0.0f, qnmax = 0.0f;
     if (use_mfma) {
@@ -333,120 +501,29 @@ __global__ __launch_bounds__(kThreads) void route_prefill_kernel(RouteArgs A) {
         knmax = wave_max(x);
         qnmax = wave_max(l < rows ? sQn[l] : 0.0f);
     }
+    const float ds1 = use_mfma ? kDeltaRel * knmax * scale * 1.01f : 0.0f;
 
-    // ---- stage 1 per-row requests ----------------------------------------------------------
+    // ---- stage 1 per-row requests ------------------------------------------------------------
     const int kreq = A.Kc < P ? A.Kc : P;
-    for (int t = w; t < rows; t += kWaves) {
-        float v[kJ];
-#pragma unroll
-        for (int j = 0; j < kJ; ++j) {
-            const int i = l + 64 * j;
-            v[j] = i < P ? sS[t * SP + i] : -INFINITY;
-        }
-        const float delta = use_mfma ? kDeltaRel * sQn[t] * knmax * scale * 1.01f : 0.0f;
-        const T* qr = sQ + t * DH;
-        const uint32_t mem = select_certified<kJ>(
-            v, kreq, delta, [&](int i) { return canon_dot<DT, DH>(qr, crow(i), scale); }, &amb1);
-#pragma unroll
-        for (int j = 0; j < kJ; ++j) {
-            const bool m = (mem >> j) & 1u;
-            if (m) {
-                const int i = l + 64 * j;
-                atomicMax(&sPk[i], okey(v[j]));
-                atomicMin(&sFirst[i], t);
-            }
-            const uint64_t bal = __ballot(m);
-            if (l == 0 && 64 * j < SP) {
-                sBits[t * BW + 2 * j] = (uint32_t)bal;
-                if (2 * j + 1 < BW) sBits[t * BW + 2 * j + 1] = (uint32_t)(bal >> 32);
-            }
-        }
-    }
+    dispatch_j(P, [&](auto jt) {
+        constexpr int J = decltype(jt)::value;
+        row_requests<J>(sS, SP, rows, P, kreq, [](int, int) { return true; }, sQn, ds1, canon1,
+                        sPk, sFirst, sBits, BW, &amb1);
+    });
     __syncthreads();
 
-    // ---- stage 1 pooled selection, forced previous chunk, sorted output (wave 0) ------------
-    const float dpool = use_mfma ? kDeltaRel * qnmax * knmax * scale * 1.01f : 0.0f;
-    auto pooled_exact = [&](int i, const float* S_, const uint32_t* bits_, auto rowfn) {
-        // canonical max over requesting rows whose approximate score can still be the max
-        const float pt = okey_inv(sPk[i]) - 2.0f * dpool;
-        float best = -INFINITY;
-        for (int t = 0; t < rows; ++t) {
-            if (!((bits_[t * BW + i / 32] >> (i % 32)) & 1u)) continue;
-            if (S_[t * SP + i] < pt) continue;
-            best = fmaxf(best, rowfn(t, i));
-        }
-        return best;
-    };
+    // ---- stage 1 pooled selection + forced previous chunk (wave 0) -------------------------
+    const float dpool = ds1 * qnmax;
     if (w == 0) {
-        float v[kJ];
-#pragma unroll
-        for (int j = 0; j < kJ; ++j) {
-            const int i = l + 64 * j;
-            v[j] = (i < P && sFirst[i] < kNoRow) ? okey_inv(sPk[i]) : -INFINITY;
-        }
-        auto canon_pool = [&](int i) {
-            return pooled_exact(i, sS, sBits, [&](int t, int c) {
-                return canon_dot<DT, DH>(sQ + t * DH, crow(c), scale);
-            });
-        };
-        uint32_t sel = select_certified<kJ>(v, A.Kc, dpool, canon_pool, &amb1p);
-        // forced previous chunk (vectorized.py:314-337): n-1 in the pool and not selected
         const int prev = n - 1;
-        const bool prev_in = n > 0 && prev >= f_hi && prev < l_lo;
-        const int ip = prev - f_hi;
-        if (prev_in) {
-            const bool have = __ballot(ip < P && ((sel >> (ip / 64)) & 1u) && l == ip % 64) != 0;
-            if (!have) {
-                int nsel = 0;
-#pragma unroll
-                for (int j = 0; j < kJ; ++j) nsel += __popcll(__ballot((sel >> j) & 1u));
-                if (nsel >= A.Kc) {
-                    // evict the last-ranked selected chunk: lowest pooled, then highest id
-                    float mn = INFINITY;
-#pragma unroll
-                    for (int j = 0; j < kJ; ++j)
-                        if ((sel >> j) & 1u) mn = fminf(mn, v[j]);
-                    mn = wave_min(mn);
-                    uint32_t ev[kJ];
-#pragma unroll
-                    for (int j = 0; j < kJ; ++j) {
-                        // candidates for eviction: within 2*dpool of the minimum; ranked by
-                        // (exact pooled ascending, id descending) -> key = ~okey(value)
-                        const bool cand = ((sel >> j) & 1u) && v[j] <= mn + 2.0f * dpool;
-                        float e = cand ? (dpool > 0.0f ? canon_pool(l + 64 * j) : v[j]) : 0.0f;
-                        ev[j] = cand ? (~okey(e)) : 0u;
-                    }
-                    // largest key = lowest value; among equal keys the HIGHEST index must win:
-                    // scan from the highest index down
-                    uint32_t best = 0u;
-#pragma unroll
-                    for (int j = 0; j < kJ; ++j) best = max(best, ev[j]);
-                    best = wave_max_u(best);
-                    int victim = -1;
-                    for (int j = kJ - 1; j >= 0 && victim < 0; --j) {
-                        const uint64_t m = __ballot(ev[j] == best && best != 0u);
-                        if (m) victim = 64 * j + 63 - __clzll(m);
-                    }
-                    if (victim >= 0 && l == victim % 64) sel &= ~(1u << (victim / 64));
-                }
-                if (l == ip % 64) sel |= 1u << (ip / 64);
-            }
-        }
-        // sorted list of selected chunks with first visible rows
-        int base = 0;
-#pragma unroll
-        for (int j = 0; j < kJ; ++j) {
-            const bool m = (sel >> j) & 1u;
-            const uint64_t bal = __ballot(m);
-            if (m) {
-                const int i = l + 64 * j;
-                const int pos = base + lanes_below(bal);
-                sSel[pos] = f_hi + i;
-                sThr[pos] = (prev_in && i == ip) ? 0 : sFirst[i];
-            }
-            base += __popcll(bal);
-        }
-        if (l == 0) sScal[0] = base;
+        const int ip = (n > 0 && prev >= f_hi && prev < l_lo) ? prev - f_hi : -1;
+        int cnt = 0;
+        dispatch_j(P, [&](auto jt) {
+            constexpr int J = decltype(jt)::value;
+            cnt = pooled_select<J>(P, A.Kc, rows, sS, SP, sBits, BW, sPk, sFirst, dpool, canon1,
+                                   ip, f_hi, sSel, sThr, &amb1p);
+        });
+        if (l == 0) sScal[0] = cnt;
     }
     __syncthreads();
     const int nsel = sScal[0];
@@ -471,12 +548,14 @@ __global__ __launch_bounds__(kThreads) void route_prefill_kernel(RouteArgs A) {
         auto grow = [&](int i) -> const T* {
             return gkb + ((int64_t)sSel[i / M] * M + (i % M)) * DH;
         };
+        auto canon2 = [&](int t, int i) { return canon_dot<DT, DH>(sQ + t * QS, grow(i), scale); };
         if (use_mfma)
-            scores_mfma<DH>(reinterpret_cast<const uint16_t*>(sQ), rows, T2,
-                            [&](int i) { return reinterpret_cast<const uint16_t*>(grow(i)); },
-                            sS, SP, sKn, scale);
+            scores_mfma<DH, QS>(reinterpret_cast<const uint16_t*>(sQ), rows, T2,
+                                [&](int i) { return reinterpret_cast<const uint16_t*>(grow(i)); },
+                                sS, SP, sKn, scale);
         else
-            scores_canonical<DT, DH>(sQ, rows, T2, grow, sS, SP, scale);
+            for (int idx = threadIdx.x; idx < rows * T2; idx += kThreads)
+                sS[(idx / T2) * SP + idx % T2] = canon2(idx / T2, idx % T2);
         __syncthreads();
         float kn2 = 0.0f;
         if (use_mfma) {
@@ -484,70 +563,49 @@ __global__ __launch_bounds__(kThreads) void route_prefill_kernel(RouteArgs A) {
             for (int i = l; i < T2; i += kWave) x = fmaxf(x, sKn[i]);
             kn2 = wave_max(x);
         }
-        for (int t = w; t < rows; t += kWaves) {
-            float v[kJ];
-#pragma unroll
-            for (int j = 0; j < kJ; ++j) {
-                const int i = l + 64 * j;
-                v[j] = (i < T2 && sThr[i / M] <= t) ? sS[t * SP + i] : -INFINITY;
-            }
-            const float delta = use_mfma ? kDeltaRel * sQn[t] * kn2 * scale * 1.01f : 0.0f;
-            const T* qr = sQ + t * DH;
-            const uint32_t mem = select_certified<kJ>(
-                v, A.Kgr, delta, [&](int i) { return canon_dot<DT, DH>(qr, grow(i), scale); },
-                &amb2);
-#pragma unroll
-            for (int j = 0; j < kJ; ++j) {
-                const bool m = (mem >> j) & 1u;
-                if (m) {
-                    const int i = l + 64 * j;
-                    atomicMax(&sPk[i], okey(v[j]));
-                    atomicMin(&sFirst[i], t);
-                }
-                const uint64_t bal = __ballot(m);
-                if (l == 0 && 64 * j < SP) {
-                    sBits[t * BW + 2 * j] = (uint32_t)bal;
-                    if (2 * j + 1 < BW) sBits[t * BW + 2 * j + 1] = (uint32_t)(bal >> 32);
-                }
-            }
-        }
+        const float ds2 = use_mfma ? kDeltaRel * kn2 * scale * 1.01f : 0.0f;
+        dispatch_j(T2, [&](auto jt) {
+            constexpr int J = decltype(jt)::value;
+            row_requests<J>(sS, SP, rows, T2, A.Kgr,
+                            [&](int t, int i) { return sThr[i / M] <= t; }, sQn, ds2, canon2, sPk,
+                            sFirst, sBits, BW, &amb2);
+        });
         __syncthreads();
-        const float dpool2 = use_mfma ? kDeltaRel * qnmax * kn2 * scale * 1.01f : 0.0f;
         if (w == 0) {
-            float v[kJ];
+            int cnt = 0;
+            const float dpool2 = ds2 * qnmax;
+            dispatch_j(T2, [&](auto jt) {
+                constexpr int J = decltype(jt)::value;
+                const int l2 = lane_id();
+                float v[J];
 #pragma unroll
-            for (int j = 0; j < kJ; ++j) {
-                const int i = l + 64 * j;
-                v[j] = (i < T2 && sFirst[i] < kNoRow) ? okey_inv(sPk[i]) : -INFINITY;
-            }
-            auto canon_pool2 = [&](int i) {
-                const float pt = okey_inv(sPk[i]) - 2.0f * dpool2;
-                float best = -INFINITY;
-                for (int t = 0; t < rows; ++t) {
-                    if (!((sBits[t * BW + i / 32] >> (i % 32)) & 1u)) continue;
-                    if (sS[t * SP + i] < pt) continue;
-                    best = fmaxf(best, canon_dot<DT, DH>(sQ + t * DH, grow(i), scale));
+                for (int j = 0; j < J; ++j) {
+                    const int i = l2 + 64 * j;
+                    v[j] = (i < T2 && sFirst[i] < kNoRow) ? okey_inv(sPk[i]) : -INFINITY;
                 }
-                return best;
-            };
-            const uint32_t op = select_certified<kJ>(v, A.Kg, dpool2, canon_pool2, &amb2p);
-            int base = 0;
+                auto canon_pool2 = [&](int i) {
+                    return pooled_exact(i, rows, sS, SP, sBits, BW, sPk, dpool2, canon2);
+                };
+                const uint32_t op = select_certified<J>(v, A.Kg, dpool2, canon_pool2, &amb2p);
+                int base = 0;
 #pragma unroll
-            for (int j = 0; j < kJ; ++j) {
-                const bool m = (op >> j) & 1u;
-                const uint64_t bal = __ballot(m);
-                if (m) {
-                    const int i = l + 64 * j;
-                    const int pos = base + lanes_below(bal);
-                    if (pos < Kgw) {
-                        out_og[pos] = sSel[i / M] * M + (i % M);
-                        out_ot[pos] = sFirst[i];
+                for (int j = 0; j < J; ++j) {
+                    const bool m = (op >> j) & 1u;
+                    const uint64_t bal = __ballot(m);
+                    if (m) {
+                        const int i = l2 + 64 * j;
+                        const int pos = base + lanes_below(bal);
+                        if (pos < Kgw) {
+                            out_og[pos] = sSel[i / M] * M + (i % M);
+                            out_ot[pos] = sFirst[i];
+                        }
                     }
+                    base += __popcll(bal);
                 }
-                base += __popcll(bal);
-            }
-            for (int i = base + l; i < Kgw; i += kWave) out_og[i] = out_ot[i] = -1;
-            if (l == 0) A.n_open[o] = base;
+                cnt = base;
+            });
+            for (int i = cnt + l; i < Kgw; i += kWave) out_og[i] = out_ot[i] = -1;
+            if (l == 0) A.n_open[o] = cnt;
         }
     }
     if (A.stats && l == 0) {
@@ -622,16 +680,17 @@ extern "C" int hga_route_prefill(const hga_config* cfg, int32_t S, const void* q
     a.BW = (SP + 31) / 32;
     const int D = cfg->head_dim;
     const size_t esz = cfg->dtype == HGA_DTYPE_BF16 ? 2 : 4;
-    const size_t lds = sizeof(float) * (size_t)kRows * SP + esz * kRows * D +
+    const size_t lds = sizeof(float) * (size_t)kRows * SP + esz * kRows * (D + 8) +
                        sizeof(float) * (SP + kRows) + sizeof(uint32_t) * SP + sizeof(int) * SP +
                        sizeof(uint32_t) * (size_t)kRows * a.BW + sizeof(int) * 2 * kMaxSel +
                        sizeof(int) * 8 + sizeof(float) * 8;
     HGA_REQUIRE(lds <= 163840, HGA_ERR_UNSUPPORTED,
                 "hga_route_prefill: %zu bytes of LDS needed (pool %d, head_dim %d)", lds, Pmax, D);
-    if (cfg->dtype == HGA_DTYPE_BF16) {
-        const uintptr_t al = (uintptr_t)chunk_k | (uintptr_t)group_k;
-        HGA_REQUIRE(al % 16 == 0 && ((ck_sb | ck_sh | gk_sb | gk_sh) % 8) == 0, HGA_ERR_ARG,
-                    "hga_route_prefill: summaries must be 16-byte aligned");
+    {
+        const int64_t ve = cfg->dtype == HGA_DTYPE_BF16 ? 8 : 4;   // elements per 16 bytes
+        const uintptr_t al = (uintptr_t)chunk_k | (uintptr_t)group_k | (uintptr_t)q;
+        HGA_REQUIRE(al % 16 == 0 && ((ck_sb | ck_sh | gk_sb | gk_sh | q_sb | q_sh | q_ss) % ve) == 0,
+                    HGA_ERR_ARG, "hga_route_prefill: q and summaries need 16-byte aligned rows");
     }
     hipStream_t st = (hipStream_t)stream;
 #define HGA_ROUTE_CASE(DTV, DHV) \

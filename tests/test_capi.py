@@ -1,0 +1,76 @@
+"""CPU checks of the C ABI: the library loads, exports every function include/hga.h declares,
+and its host-side validation and size logic behave (no kernel is launched)."""
+import ctypes
+import os
+import re
+
+import pytest
+
+import oracle
+from hierarchicalglobalattention_amd import _lib, ops
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def declared_functions():
+    text = open(os.path.join(ROOT, "include", "hga.h")).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(hga_[a-z_0-9]+)\s*\(", text)))
+
+
+def test_exports_every_declared_symbol():
+    lib = _lib.lib()
+    names = declared_functions()
+    assert "hga_route_prefill" in names and len(names) >= 7
+    for n in names:
+        assert hasattr(lib, n), f"{n} declared in include/hga.h but not exported"
+        assert n in _lib.SIGNATURES, f"{n} has no ctypes signature"
+
+
+def test_version_and_widths():
+    lib = _lib.lib()
+    assert lib.hga_version() >= 100
+    for S, C, gs, tc, tg in [(2048, 64, 16, 4, 8), (32768, 64, 16, 16, 64), (37, 8, 4, 3, 4),
+                             (100, 64, 16, 0, 8), (64, 64, 16, 20, 32)]:
+        cfg = ops.make_config(batch=1, heads=8, kv_heads=2, head_dim=64, chunk_size=C,
+                              group_size=gs, topk_chunks=tc, topk_groups=tg, keep_first=1,
+                              keep_last=2, cutoff_pair=3, dtype=__import__("torch").bfloat16)
+        N, Kc, Kg = ops.prefill_widths(cfg, S)
+        assert (N, Kc, Kg) == tuple(oracle.sizes(S, C, gs, tc, tg)[i] for i in (0, 2, 3))
+
+
+def test_errors_reported_without_launch():
+    import torch
+    lib = _lib.lib()
+    cfg = ops.make_config(batch=1, heads=6, kv_heads=4, head_dim=64, chunk_size=64,
+                          group_size=16, topk_chunks=4, topk_groups=8, keep_first=1, keep_last=2,
+                          cutoff_pair=3, dtype=torch.float32)
+    rc = lib.hga_prefill_widths(ctypes.byref(cfg), 100, None, None, None)
+    assert rc == -1 and b"kv_heads" in lib.hga_last_error()
+    cfg.kv_heads = 2
+    cfg.head_dim = 96
+    assert lib.hga_prefill_widths(ctypes.byref(cfg), 100, None, None, None) == -2
+    cfg.head_dim = 64
+    z = ctypes.c_void_p(0)
+    rc = lib.hga_rope(ctypes.byref(cfg), 2, 10, z, 0, 0, 0, z, 0, 0, 0, z, z, 0, z)
+    assert rc == -1 and b"NULL" in lib.hga_last_error()
+    with pytest.raises(_lib.HgaError):
+        _lib.check(lib.hga_rope(ctypes.byref(cfg), 2, 10, z, 0, 0, 0, z, 0, 0, 0, z, z, 0, z),
+                   "hga_rope")
+
+
+def test_cpu_tensors_are_rejected():
+    import torch
+    cfg = ops.make_config(batch=1, heads=2, kv_heads=1, head_dim=64, chunk_size=64,
+                          group_size=16, topk_chunks=4, topk_groups=8, keep_first=1, keep_last=2,
+                          cutoff_pair=3, dtype=torch.float32)
+    x = torch.zeros(1, 2, 8, 64)
+    with pytest.raises(RuntimeError, match="GPU only"):
+        ops.rope(cfg, x, torch.zeros(8, 64), torch.zeros(8, 64))
+
+
+def test_cutoff_pair_closed_forms():
+    """Closed-form values of the mixed-RoPE cutoff (chunk_router.py:717-726)."""
+    for theta, C, Dh, want in [(1e4, 64, 64, 17), (1e6, 64, 128, 23), (1e4, 8, 16, 3)]:
+        assert ops.mixed_cutoff_pair(theta, C, Dh) == want
+        assert oracle.cutoff_pair(theta, C, Dh) == want
