@@ -1,26 +1,28 @@
 // Two-level prefill router (vectorized.py:242-396) for gfx950.
 //
-// One 512-thread workgroup per (batch, query head, query chunk n); nothing is materialised in
-// HBM except the routing lists.
+// One 512-thread workgroup per (batch, query head, query chunk n); at most ~80 KB of LDS so that
+// two workgroups share a CU.  Nothing is materialised in HBM except the routing lists.
 //
-//   1. The chunk's query rows go to LDS.  Scores of every row against every candidate of the
-//      routing pool P(n) = [f_hi, l_lo) are produced into LDS: by bf16 MFMA
-//      (v_mfma_f32_32x32x16_bf16, fp32 accumulate) for bf16 inputs, or by the canonical fp32
-//      FMA chain for fp32 inputs / HGA_ROUTE_CANONICAL.
-//   2. Each wave selects, per query row, the row's top-min(Kc,|P|) candidates with an exact
-//      wave-wide bisection over order-preserving score keys (ballot counts), ties to the lower
-//      chunk id.  MFMA scores differ from the canonical chain by at most
+//   1. Stage 1, per 32-row block of the chunk: the block's query rows go to LDS; scores of the
+//      rows against every candidate of the routing pool P(n) = [f_hi, l_lo) are produced into LDS
+//      by bf16 MFMA (v_mfma_f32_32x32x16_bf16, fp32 accumulate), or by the canonical fp32 FMA
+//      chain for fp32 inputs / HGA_ROUTE_CANONICAL.
+//   2. Each wave selects, for one query row at a time, the row's top-min(Kc,|P|) candidates:
+//      an interpolation search for a separating threshold (seeded from the row's mean and
+//      standard deviation, secant steps on the ballot counts, then key-space bisection), ties to
+//      the lower chunk id.  MFMA scores differ from the canonical chain by at most
 //      delta = 2^-16 * |q| * |k| * scale (both are fp32 accumulations of the same exact bf16
-//      products); when the k-th and (k+1)-th scores are closer than 2*delta the row is
-//      re-ranked: the candidates inside the uncertainty band are re-scored with the canonical
-//      chain and the remaining slots are filled from them exactly.  Selections are therefore
-//      identical to the canonical oracle.
+//      products); when the k-th and (k+1)-th scores are closer than 2*delta the candidates
+//      inside the band are re-scored with the canonical chain and the remaining slots filled
+//      exactly, so selections equal the canonical oracle's.
 //   3. Requests are pooled per chunk (max score, first requesting row) with LDS atomics; one
-//      wave takes the top-Kc pooled chunks (same certification, with the pooled maxima
-//      recomputed canonically when ambiguous), forces in chunk n-1 when it lies in the pool,
-//      and writes the sorted (chunk, first row) list.
-//   4. Stage 2 repeats 1-3 over the M groups of each selected chunk, with a group visible to a
-//      row only from its parent's first row on, top-Kgr requests per row and top-Kg opened.
+//      wave takes the top-Kc pooled chunks (same certification; ambiguous pooled maxima are
+//      recomputed canonically over the requesting rows), forces in chunk n-1 when it lies in the
+//      pool, and writes the sorted (chunk, first row) list.
+//   4. Stage 2 repeats 1-3 for all rows at once over the M groups of each selected chunk, a
+//      group being visible to a row from its parent's first row on; top-Kgr requests per row,
+//      top-Kg opened.
+// Wave-wide reductions use DPP row operations and lane reads (no LDS round trips).
 #include "hga_common.h"
 
 namespace hga {
@@ -31,9 +33,10 @@ typedef float floatx16 __attribute__((ext_vector_type(16)));
 
 constexpr int kThreads = 512;
 constexpr int kWaves = kThreads / kWave;
-constexpr int kRows = 64;   // query rows per chunk (C <= 64)
-constexpr int kJ = 8;       // candidates per lane in a wave selection: <= 512 candidates
-constexpr int kMaxSel = 64; // Kc bound
+constexpr int kRows = 64;     // query rows per chunk (C <= 64)
+constexpr int kBlk = 32;      // stage-1 row block
+constexpr int kJ = 8;         // candidates per lane in a selection: <= 512 candidates
+constexpr int kMaxSel = 64;   // Kc bound
 constexpr float kDeltaRel = 1.0f / 65536.0f;
 constexpr int kNoRow = 1 << 20;
 
@@ -46,24 +49,47 @@ struct RouteArgs {
     int64_t gk_sb, gk_sh;
     int32_t *sel_chunk, *sel_thr, *n_sel, *open_grp, *open_thr, *n_open;
     int32_t* stats;
-    int B, H, KVH, S, N, C, M, kf, kl, Kc, Kg, Kgr, SP, BW, canonical;
+    int B, H, KVH, S, N, C, M, kf, kl, Kc, Kg, Kgr;
+    int SP, SP2, SSZ, SPP, BW, canonical;
     float scale;
 };
 
 // ------------------------------------------------------------------------------------------
-// wave-level exact top-k over order-preserving keys (0 = not a candidate)
+// wave-wide reductions: DPP within rows of 16 lanes, then the four row results by lane reads
 // ------------------------------------------------------------------------------------------
-__device__ __forceinline__ uint32_t wave_max_u(uint32_t v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v = max(v, (uint32_t)__shfl_xor((int)v, o, kWave));
-    return v;
+template <int CTRL>
+__device__ __forceinline__ int dpp(int x) {
+    return __builtin_amdgcn_update_dpp(x, x, CTRL, 0xf, 0xf, false);
 }
-__device__ __forceinline__ uint32_t wave_min_u(uint32_t v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v = min(v, (uint32_t)__shfl_xor((int)v, o, kWave));
-    return v;
+template <class Op>
+__device__ __forceinline__ int wave_reduce_bits(int x, Op op) {
+    x = op(x, dpp<0xB1>(x));    // quad_perm [1,0,3,2]
+    x = op(x, dpp<0x4E>(x));    // quad_perm [2,3,0,1]
+    x = op(x, dpp<0x124>(x));   // row_ror:4
+    x = op(x, dpp<0x128>(x));   // row_ror:8
+    const int a = __builtin_amdgcn_readlane(x, 0), b = __builtin_amdgcn_readlane(x, 16);
+    const int c = __builtin_amdgcn_readlane(x, 32), d = __builtin_amdgcn_readlane(x, 48);
+    return op(op(a, b), op(c, d));
+}
+__device__ __forceinline__ float wmax(float v) {
+    return __int_as_float(wave_reduce_bits(__float_as_int(v), [](int a, int b) {
+        return __float_as_int(fmaxf(__int_as_float(a), __int_as_float(b)));
+    }));
+}
+__device__ __forceinline__ float wmin(float v) {
+    return __int_as_float(wave_reduce_bits(__float_as_int(v), [](int a, int b) {
+        return __float_as_int(fminf(__int_as_float(a), __int_as_float(b)));
+    }));
+}
+__device__ __forceinline__ float wsum(float v) {
+    return __int_as_float(wave_reduce_bits(__float_as_int(v), [](int a, int b) {
+        return __float_as_int(__int_as_float(a) + __int_as_float(b));
+    }));
 }
 
+// ------------------------------------------------------------------------------------------
+// wave-level exact top-k over order-preserving keys (0 = not a candidate)
+// ------------------------------------------------------------------------------------------
 template <int J>
 __device__ __forceinline__ int count_ge(const uint32_t (&kv)[J], uint32_t x) {
     int c = 0;
@@ -72,10 +98,22 @@ __device__ __forceinline__ int count_ge(const uint32_t (&kv)[J], uint32_t x) {
     return c;
 }
 
+// Upper-tail standard normal quantile, Abramowitz & Stegun 26.2.23 (|error| < 4.5e-4); only
+// seeds the threshold search.
+__device__ __forceinline__ float z_upper(float p) {
+    p = fminf(fmaxf(p, 1e-6f), 1.0f - 1e-6f);
+    const bool lower = p > 0.5f;
+    const float pp = lower ? 1.0f - p : p;
+    const float t = sqrtf(-2.0f * logf(pp));
+    const float z = t - (2.515517f + 0.802853f * t + 0.010328f * t * t) /
+                            (1.0f + 1.432788f * t + 0.189269f * t * t + 0.001308f * t * t * t);
+    return lower ? -z : z;
+}
+
 // Members of the top-k (largest keys; equal keys -> lower candidate index lane + 64*j).
-// Returns bit j set for member candidate lane + 64*j.
+// v holds the float values of the keys (only used to steer the search).
 template <int J>
-__device__ uint32_t exact_topk(const uint32_t (&kv)[J], int k) {
+__device__ uint32_t exact_topk(const uint32_t (&kv)[J], const float (&v)[J], int k) {
     const int nvalid = count_ge<J>(kv, 1u);
     uint32_t bits = 0;
     if (nvalid <= k) {
@@ -84,35 +122,53 @@ __device__ uint32_t exact_topk(const uint32_t (&kv)[J], int k) {
         return bits;
     }
     if (k <= 0) return 0u;
-    uint32_t lmin = 0xffffffffu, lmax = 0u;
+    float s1 = 0.0f, s2 = 0.0f, mn = INFINITY, mx = -INFINITY;
 #pragma unroll
-    for (int j = 0; j < J; ++j) {
-        if (kv[j] != 0u) lmin = min(lmin, kv[j]);
-        lmax = max(lmax, kv[j]);
-    }
-    uint32_t lo = wave_min_u(lmin), hi = wave_max_u(lmax);
+    for (int j = 0; j < J; ++j)
+        if (kv[j] != 0u) {
+            s1 += v[j];
+            s2 = fmaf(v[j], v[j], s2);
+            mn = fminf(mn, v[j]);
+            mx = fmaxf(mx, v[j]);
+        }
+    s1 = wsum(s1);
+    s2 = wsum(s2);
+    uint32_t lo = okey(wmin(mn)), hi = okey(wmax(mx));
+    int clo = nvalid, chi = count_ge<J>(kv, hi);
     uint32_t vstar;
-    if (count_ge<J>(kv, hi) >= k) {
+    if (chi >= k) {
         vstar = hi;
     } else {
-        // invariant: count_ge(lo) > k, count_ge(hi) < k.  The first steps bisect the float
-        // values (fast for smooth score distributions), then the key space (terminates).
+        // invariant: count_ge(lo) = clo > k > chi = count_ge(hi)
+        const float mu = s1 / nvalid;
+        const float sd = sqrtf(fmaxf(s2 / nvalid - mu * mu, 0.0f));
+        const float guess = mu + z_upper((k + 0.5f) / nvalid) * sd;
         int it = 0;
         while (hi - lo > 1u) {
             uint32_t mid = lo + (hi - lo) / 2u;
-            if (it++ < 16) {
-                const float lf = okey_inv(lo), hf = okey_inv(hi);
-                const uint32_t fm = okey(lf + (hf - lf) * 0.5f);
-                if (fm > lo && fm < hi) mid = fm;
+            if (it < 8) {
+                const float lf = okey_inv(lo), hf = okey_inv(hi), span = hf - lf;
+                float x = it == 0 ? guess : lf + span * (float)(clo - k) / (float)(clo - chi);
+                x = fminf(fmaxf(x, lf + span * 0.0625f), hf - span * 0.0625f);
+                if (x == x && span < INFINITY) {
+                    const uint32_t xm = okey(x);
+                    if (xm > lo && xm < hi) mid = xm;
+                }
             }
+            ++it;
             const int c = count_ge<J>(kv, mid);
             if (c == k) {
 #pragma unroll
                 for (int j = 0; j < J; ++j) bits |= (kv[j] >= mid ? 1u : 0u) << j;
                 return bits;
             }
-            if (c > k) lo = mid;
-            else hi = mid;
+            if (c > k) {
+                lo = mid;
+                clo = c;
+            } else {
+                hi = mid;
+                chi = c;
+            }
         }
         vstar = lo;
     }
@@ -143,7 +199,7 @@ __device__ uint32_t select_certified(const float (&v)[J], int k, float delta, Ca
     uint32_t kv[J];
 #pragma unroll
     for (int j = 0; j < J; ++j) kv[j] = (v[j] == -INFINITY) ? 0u : okey(v[j]);
-    const uint32_t bits = exact_topk<J>(kv, k);
+    const uint32_t bits = exact_topk<J>(kv, v, k);
     if (!(delta > 0.0f)) return bits;
     if (count_ge<J>(kv, 1u) <= k) return bits;
     float ak = INFINITY, ak1 = -INFINITY;
@@ -153,12 +209,13 @@ __device__ uint32_t select_certified(const float (&v)[J], int k, float delta, Ca
         if ((bits >> j) & 1u) ak = fminf(ak, v[j]);
         else ak1 = fmaxf(ak1, v[j]);
     }
-    ak = wave_min(ak);
-    ak1 = wave_max(ak1);
+    ak = wmin(ak);
+    ak1 = wmax(ak1);
     if (ak - 2.0f * delta > ak1) return bits;
     *amb += 1;
     const float band_lo = ak - 2.0f * delta, band_hi = ak1 + 2.0f * delta;
     uint32_t cin = 0, ck[J];
+    float cv[J];
     int cc = 0;
 #pragma unroll
     for (int j = 0; j < J; ++j) {
@@ -166,47 +223,81 @@ __device__ uint32_t select_certified(const float (&v)[J], int k, float delta, Ca
         const bool certain = mem && v[j] > band_hi;
         const bool inA = valid && !certain && v[j] >= band_lo;
         cin |= (certain ? 1u : 0u) << j;
-        ck[j] = inA ? okey(canon(lane_id() + 64 * j)) : 0u;
+        cv[j] = inA ? canon(lane_id() + 64 * j) : -INFINITY;
+        ck[j] = inA ? okey(cv[j]) : 0u;
         cc += __popcll(__ballot(certain));
     }
-    return cin | exact_topk<J>(ck, k - cc);
+    return cin | exact_topk<J>(ck, cv, k - cc);
+}
+
+template <int J>
+struct JTag {
+    static constexpr int value = J;
+};
+// Calls f(JTag<J>) with the smallest J such that 64*J >= n (wave-uniform n).
+template <class F>
+__device__ __forceinline__ void dispatch_j(int n, F&& f) {
+    if (n <= 64) f(JTag<1>{});
+    else if (n <= 128) f(JTag<2>{});
+    else if (n <= 256) f(JTag<4>{});
+    else f(JTag<8>{});
 }
 
 // ------------------------------------------------------------------------------------------
 // scores
 // ------------------------------------------------------------------------------------------
 // Canonical score: sequential fp32 FMA chain over d = 0..DH-1, then * scale (-0 -> +0).
-// q comes from LDS, k from global; both are read with 16-byte vector loads, the chain order is
-// unchanged.
+// q and k are read with 16-byte vector loads (LDS or global); the chain order is unchanged.
 template <int DT, int DH>
-__device__ __noinline__ float canon_dot(const typename Elem<DT>::T* q,
-                                        const typename Elem<DT>::T* k, float scale) {
+__device__ __forceinline__ float canon_dot(const typename Elem<DT>::T* q,
+                                           const typename Elem<DT>::T* k, float scale) {
     float acc = 0.0f;
     if constexpr (DT == HGA_DTYPE_BF16) {
-        uint4 kr[DH / 8];
+        for (int p = 0; p < DH / 32; ++p) {          // 32 dims per step, 16-byte loads
+            uint4 kr[4], qr[4];
 #pragma unroll
-        for (int i = 0; i < DH / 8; ++i) kr[i] = *reinterpret_cast<const uint4*>(k + 8 * i);
+            for (int i = 0; i < 4; ++i) {
+                kr[i] = *reinterpret_cast<const uint4*>(k + 32 * p + 8 * i);
+                qr[i] = *reinterpret_cast<const uint4*>(q + 32 * p + 8 * i);
+            }
 #pragma unroll
-        for (int i = 0; i < DH / 8; ++i) {
-            const uint4 qq = *reinterpret_cast<const uint4*>(q + 8 * i);
-            const uint32_t qw[4] = {qq.x, qq.y, qq.z, qq.w}, kw[4] = {kr[i].x, kr[i].y, kr[i].z, kr[i].w};
+            for (int i = 0; i < 4; ++i) {
+                const uint32_t qw[4] = {qr[i].x, qr[i].y, qr[i].z, qr[i].w};
+                const uint32_t kw[4] = {kr[i].x, kr[i].y, kr[i].z, kr[i].w};
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
+                for (int e = 0; e < 4; ++e) {
+                    acc = fmaf(__uint_as_float(qw[e] << 16), __uint_as_float(kw[e] << 16), acc);
+                    acc = fmaf(__uint_as_float(qw[e] & 0xffff0000u),
+                               __uint_as_float(kw[e] & 0xffff0000u), acc);
+                }
+            }
+        }
+        if constexpr (DH % 32 != 0) {                 // DH == 16
+            const uint4 kr0 = *reinterpret_cast<const uint4*>(k), kr1 = *reinterpret_cast<const uint4*>(k + 8);
+            const uint4 qr0 = *reinterpret_cast<const uint4*>(q), qr1 = *reinterpret_cast<const uint4*>(q + 8);
+            const uint32_t qw[8] = {qr0.x, qr0.y, qr0.z, qr0.w, qr1.x, qr1.y, qr1.z, qr1.w};
+            const uint32_t kw[8] = {kr0.x, kr0.y, kr0.z, kr0.w, kr1.x, kr1.y, kr1.z, kr1.w};
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
                 acc = fmaf(__uint_as_float(qw[e] << 16), __uint_as_float(kw[e] << 16), acc);
                 acc = fmaf(__uint_as_float(qw[e] & 0xffff0000u), __uint_as_float(kw[e] & 0xffff0000u), acc);
             }
         }
     } else {
-        float4 kr[DH / 4];
+        for (int p = 0; p < DH / 16; ++p) {
+            float4 kr[4], qr[4];
 #pragma unroll
-        for (int i = 0; i < DH / 4; ++i) kr[i] = *reinterpret_cast<const float4*>(k + 4 * i);
+            for (int i = 0; i < 4; ++i) {
+                kr[i] = *reinterpret_cast<const float4*>(k + 16 * p + 4 * i);
+                qr[i] = *reinterpret_cast<const float4*>(q + 16 * p + 4 * i);
+            }
 #pragma unroll
-        for (int i = 0; i < DH / 4; ++i) {
-            const float4 qq = *reinterpret_cast<const float4*>(q + 4 * i);
-            acc = fmaf(qq.x, kr[i].x, acc);
-            acc = fmaf(qq.y, kr[i].y, acc);
-            acc = fmaf(qq.z, kr[i].z, acc);
-            acc = fmaf(qq.w, kr[i].w, acc);
+            for (int i = 0; i < 4; ++i) {
+                acc = fmaf(qr[i].x, kr[i].x, acc);
+                acc = fmaf(qr[i].y, kr[i].y, acc);
+                acc = fmaf(qr[i].z, kr[i].z, acc);
+                acc = fmaf(qr[i].w, kr[i].w, acc);
+            }
         }
     }
     const float s = acc * scale;
@@ -227,21 +318,19 @@ __device__ __forceinline__ float sumsq_bf16x8(uint4 u) {
     return s;
 }
 
-// bf16 MFMA scores (scaled) of all rows against all candidates, plus candidate norms.
-// Wave w handles candidate tiles w, w+8, ... of 32 candidates; both 32-row blocks.
-template <int DH, int QS, class RowPtr>
-__device__ void scores_mfma(const uint16_t* sQ, int rows, int ncand, RowPtr rowptr, float* sS,
-                            int SP, float* sKn, float scale) {
+// bf16 MFMA scores (scaled) of one 32-row block (query rows in sQ, stride DH) against all
+// candidates, written to sRows[row * stride + c]; the largest candidate norm is folded into
+// *knmax (uint bits of a non-negative float) when knmax is not NULL.  Wave w handles candidate
+// tiles w, w+8, ... of 32 candidates.
+template <int DH, class RowPtr>
+__device__ void scores_block_mfma(const uint16_t* sQ, int ncand, RowPtr rowptr, float* sRows,
+                                  int stride, float scale, uint32_t* knmax) {
     constexpr int KS = DH / 16;
     const int w = threadIdx.x / kWave, l = lane_id();
-    const int nrb = rows > 32 ? 2 : 1;
-    bf16x8 a0[KS], a1[KS];
+    bf16x8 a[KS];
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks) {
-        const int col = ks * 16 + 8 * (l / 32);
-        a0[ks] = as_bf16x8(*reinterpret_cast<const uint4*>(sQ + (l % 32) * QS + col));
-        a1[ks] = as_bf16x8(*reinterpret_cast<const uint4*>(sQ + (32 + l % 32) * QS + col));
-    }
+    for (int ks = 0; ks < KS; ++ks)
+        a[ks] = as_bf16x8(*reinterpret_cast<const uint4*>(sQ + (l % 32) * DH + ks * 16 + 8 * (l / 32)));
     for (int ct = w; ct * 32 < ncand; ct += kWaves) {
         const int c = ct * 32 + l % 32;
         const bool cv = c < ncand;
@@ -252,98 +341,67 @@ __device__ void scores_mfma(const uint16_t* sQ, int rows, int ncand, RowPtr rowp
             u[ks] = make_uint4(0u, 0u, 0u, 0u);
             if (cv) u[ks] = *reinterpret_cast<const uint4*>(kp + ks * 16 + 8 * (l / 32));
         }
-        floatx16 acc0 = {}, acc1 = {};
+        floatx16 acc = {};
         float nsq = 0.0f;
 #pragma unroll
         for (int ks = 0; ks < KS; ++ks) {
             nsq += sumsq_bf16x8(u[ks]);
-            const bf16x8 bv = as_bf16x8(u[ks]);
-            acc0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0[ks], bv, acc0, 0, 0, 0);
-            if (nrb > 1) acc1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1[ks], bv, acc1, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[ks], as_bf16x8(u[ks]), acc, 0, 0, 0);
         }
         nsq += __shfl_xor(nsq, 32, kWave);
         if (cv) {
-            if (l < 32) sKn[c] = sqrtf(nsq);
+            if (knmax && l < 32) atomicMax(knmax, __float_as_uint(sqrtf(nsq)));
 #pragma unroll
             for (int i = 0; i < 16; ++i) {
                 const int row = 8 * (i / 4) + 4 * (l / 32) + (i % 4);
-                sS[row * SP + c] = acc0[i] * scale;
-                if (nrb > 1) sS[(32 + row) * SP + c] = acc1[i] * scale;
+                sRows[row * stride + c] = acc[i] * scale;
             }
         }
     }
 }
 
-template <int J>
-struct JTag {
-    static constexpr int value = J;
-};
-// Calls f(JTag<J>) with the smallest J such that 64*J >= n (wave-uniform n).
-template <class F>
-__device__ __forceinline__ void dispatch_j(int n, F&& f) {
-    if (n <= 64) f(JTag<1>{});
-    else if (n <= 128) f(JTag<2>{});
-    else if (n <= 256) f(JTag<4>{});
-    else f(JTag<8>{});
-}
-
-// Per-row top-k requests for rows w, w+8, ...: every member (row t, candidate i) raises the
-// candidate's pooled key to okey(score), lowers its first row to t, and sets bit (t, i).
-template <int J, class Vis, class Canon>
-__device__ void row_requests(const float* sS, int SP, int rows, int ncand, int k, Vis visible,
-                             const float* sQn, float dscale, Canon canon_row, uint32_t* sPk,
-                             int* sFirst, uint32_t* sBits, int BW, int* amb) {
-    const int w = threadIdx.x / kWave, l = lane_id();
-    for (int t = w; t < rows; t += kWaves) {
-        float v[J];
+// One query row's requests: members raise the candidate's pooled key to okey(score), lower its
+// first row to t, and set bit (t, i).  v: the row's approximate scores (-inf = not visible).
+template <int J, class Canon>
+__device__ __forceinline__ void row_request(int t, const float (&v)[J], int k, float delta,
+                                            Canon canon, uint32_t* sPk, int* sFirst,
+                                            uint32_t* sBits, int BW, int* amb) {
+    const int l = lane_id();
+    const uint32_t mem = select_certified<J>(v, k, delta, canon, amb);
 #pragma unroll
-        for (int j = 0; j < J; ++j) {
+    for (int j = 0; j < J; ++j) {
+        const bool m = (mem >> j) & 1u;
+        if (m) {
             const int i = l + 64 * j;
-            v[j] = (i < ncand && visible(t, i)) ? sS[t * SP + i] : -INFINITY;
+            atomicMax(&sPk[i], okey(v[j]));
+            atomicMin(&sFirst[i], t);
         }
-        const float delta = dscale * sQn[t];
-        const uint32_t mem = select_certified<J>(
-            v, k, delta, [&](int i) { return canon_row(t, i); }, amb);
-#pragma unroll
-        for (int j = 0; j < J; ++j) {
-            const bool m = (mem >> j) & 1u;
-            if (m) {
-                const int i = l + 64 * j;
-                atomicMax(&sPk[i], okey(v[j]));
-                atomicMin(&sFirst[i], t);
-            }
-            const uint64_t bal = __ballot(m);
-            if (l == 0 && 64 * j < SP) {
-                sBits[t * BW + 2 * j] = (uint32_t)bal;
-                if (2 * j + 1 < BW) sBits[t * BW + 2 * j + 1] = (uint32_t)(bal >> 32);
-            }
+        const uint64_t bal = __ballot(m);
+        if (l == 0) {
+            if (2 * j < BW) sBits[t * BW + 2 * j] = (uint32_t)bal;
+            if (2 * j + 1 < BW) sBits[t * BW + 2 * j + 1] = (uint32_t)(bal >> 32);
         }
     }
 }
 
-// Canonical pooled value of candidate i: max over requesting rows whose approximate score can
-// still be the maximum (within 2*dpool of the approximate pooled max).
+// Canonical pooled value of candidate i: max of the canonical scores over the rows that
+// requested it.
 template <class Canon>
-__device__ float pooled_exact(int i, int rows, const float* sS, int SP, const uint32_t* sBits,
-                              int BW, const uint32_t* sPk, float dpool, Canon canon_row) {
-    const float pt = okey_inv(sPk[i]) - 2.0f * dpool;
+__device__ float pooled_exact(int i, int rows, const uint32_t* sBits, int BW, Canon canon_row) {
     float best = -INFINITY;
-    for (int t = 0; t < rows; ++t) {
-        if (!((sBits[t * BW + i / 32] >> (i % 32)) & 1u)) continue;
-        if (sS[t * SP + i] < pt) continue;
-        best = fmaxf(best, canon_row(t, i));
-    }
+    for (int t = 0; t < rows; ++t)
+        if ((sBits[t * BW + i / 32] >> (i % 32)) & 1u) best = fmaxf(best, canon_row(t, i));
     return best;
 }
 
 // Wave 0: top-k of the requested candidates by pooled score (certified), optional forced
 // candidate `ip` (evicting the last-ranked one when full), written ascending to sSel/sThr with
-// ids base + i; returns the count (wave-uniform).
+// ids base_id + i; returns the count (wave-uniform).
 template <int J, class Canon>
-__device__ int pooled_select(int ncand, int k, int rows, const float* sS, int SP,
-                             const uint32_t* sBits, int BW, const uint32_t* sPk,
-                             const int* sFirst, float dpool, Canon canon_row, int ip, int base_id,
-                             int* sSel, int* sThr, int* amb) {
+__device__ int pooled_select(int ncand, int k, int rows, const uint32_t* sBits, int BW,
+                             const uint32_t* sPk, const int* sFirst, float dpool,
+                             Canon canon_row, int ip, int base_id, int* sSel, int* sThr,
+                             int* amb) {
     const int l = lane_id();
     float v[J];
 #pragma unroll
@@ -351,9 +409,7 @@ __device__ int pooled_select(int ncand, int k, int rows, const float* sS, int SP
         const int i = l + 64 * j;
         v[j] = (i < ncand && sFirst[i] < kNoRow) ? okey_inv(sPk[i]) : -INFINITY;
     }
-    auto canon_pool = [&](int i) {
-        return pooled_exact(i, rows, sS, SP, sBits, BW, sPk, dpool, canon_row);
-    };
+    auto canon_pool = [&](int i) { return pooled_exact(i, rows, sBits, BW, canon_row); };
     uint32_t sel = select_certified<J>(v, k, dpool, canon_pool, amb);
     if (ip >= 0) {
         const bool have = __ballot(((sel >> (ip / 64)) & 1u) && l == ip % 64) != 0;
@@ -367,18 +423,19 @@ __device__ int pooled_select(int ncand, int k, int rows, const float* sS, int SP
 #pragma unroll
                 for (int j = 0; j < J; ++j)
                     if ((sel >> j) & 1u) mn = fminf(mn, v[j]);
-                mn = wave_min(mn);
+                mn = wmin(mn);
                 uint32_t ev[J];
+                uint32_t best = 0u;
 #pragma unroll
                 for (int j = 0; j < J; ++j) {
                     const bool cand = ((sel >> j) & 1u) && v[j] <= mn + 2.0f * dpool;
                     const float e = cand ? (dpool > 0.0f ? canon_pool(l + 64 * j) : v[j]) : 0.0f;
                     ev[j] = cand ? ~okey(e) : 0u;
+                    best = max(best, ev[j]);
                 }
-                uint32_t best = 0u;
-#pragma unroll
-                for (int j = 0; j < J; ++j) best = max(best, ev[j]);
-                best = wave_max_u(best);
+                best = (uint32_t)wave_reduce_bits((int)best, [](int a, int b) {
+                    return (int)max((uint32_t)a, (uint32_t)b);
+                });
                 int victim = -1;
 #pragma unroll
                 for (int j = J - 1; j >= 0; --j) {
@@ -406,26 +463,36 @@ __device__ int pooled_select(int ncand, int k, int rows, const float* sS, int SP
     return base;
 }
 
+// Query rows [r0, r0+32) of the chunk into sQ (stride DH), zero beyond `rows`.
+template <class T, int DH>
+__device__ __forceinline__ void load_block(T* sQ, const T* qg, int64_t q_ss, int r0, int rows) {
+    constexpr int VE = 16 / (int)sizeof(T);
+    for (int idx = threadIdx.x; idx < kBlk * (DH / VE); idx += kThreads) {
+        const int r = idx / (DH / VE), d = (idx % (DH / VE)) * VE;
+        uint4 u = make_uint4(0u, 0u, 0u, 0u);
+        if (r0 + r < rows) u = *reinterpret_cast<const uint4*>(qg + (int64_t)(r0 + r) * q_ss + d);
+        *reinterpret_cast<uint4*>(sQ + r * DH + d) = u;
+    }
+}
+
 // ------------------------------------------------------------------------------------------
 // the kernel
 // ------------------------------------------------------------------------------------------
 template <int DT, int DH>
-__global__ __launch_bounds__(kThreads) void route_prefill_kernel(RouteArgs A) {
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4)))
+void route_prefill_kernel(RouteArgs A) {
     typedef typename Elem<DT>::T T;
-    constexpr int QS = DH + 8;   // padded LDS row stride of the query tile
     extern __shared__ __align__(16) unsigned char smem_raw[];
-    const int SP = A.SP, BW = A.BW;
-    float* sS = reinterpret_cast<float*>(smem_raw);                 // [64][SP]
-    T* sQ = reinterpret_cast<T*>(sS + kRows * SP);                   // [64][QS]
-    float* sKn = reinterpret_cast<float*>(sQ + kRows * QS);          // [SP]
-    float* sQn = sKn + SP;                                           // [64]
-    uint32_t* sPk = reinterpret_cast<uint32_t*>(sQn + kRows);        // [SP] pooled key
-    int* sFirst = reinterpret_cast<int*>(sPk + SP);                  // [SP]
-    uint32_t* sBits = reinterpret_cast<uint32_t*>(sFirst + SP);      // [64][BW]
+    const int SP = A.SP, SP2 = A.SP2, BW = A.BW;
+    float* sS = reinterpret_cast<float*>(smem_raw);                 // [32][SP] | [64][SP2]
+    T* sQ = reinterpret_cast<T*>(sS + A.SSZ);                        // [32][DH]
+    float* sQn = reinterpret_cast<float*>(sQ + kBlk * DH);           // [64]
+    uint32_t* sPk = reinterpret_cast<uint32_t*>(sQn + kRows);        // [SPP] pooled key
+    int* sFirst = reinterpret_cast<int*>(sPk + A.SPP);               // [SPP]
+    uint32_t* sBits = reinterpret_cast<uint32_t*>(sFirst + A.SPP);   // [64][BW]
     int* sSel = reinterpret_cast<int*>(sBits + kRows * BW);          // [kMaxSel] sorted chunk ids
     int* sThr = sSel + kMaxSel;                                      // [kMaxSel]
     int* sScal = sThr + kMaxSel;                                     // [8] scalars
-    // Stage-2 group selections can be up to Kc*M long; they are emitted straight to global.
 
     const int N = A.N, C = A.C, M = A.M;
     const int n = N - 1 - (int)(blockIdx.x / (A.B * A.H));          // heavy chunks first
@@ -453,75 +520,78 @@ __global__ __launch_bounds__(kThreads) void route_prefill_kernel(RouteArgs A) {
     const bool use_mfma = (DT == HGA_DTYPE_BF16) && !A.canonical;
     const float scale = A.scale;
     int amb1 = 0, amb1p = 0, amb2 = 0, amb2p = 0;
+    const T* qg = reinterpret_cast<const T*>(A.q) + b * A.q_sb + h * A.q_sh + (int64_t)n * C * A.q_ss;
+    const T* ckb = reinterpret_cast<const T*>(A.ck) + b * A.ck_sb + kvh * A.ck_sh;
+    auto crow = [&](int i) -> const T* { return ckb + (int64_t)(f_hi + i) * DH; };
+    auto canonG1 = [&](int t, int i) { return canon_dot<DT, DH>(qg + t * A.q_ss, crow(i), scale); };
 
-    // ---- query rows -> LDS (rows >= `rows` zero), row norms --------------------------------
-    {
-        constexpr int VE = 16 / (int)sizeof(T);   // elements per 16-byte vector
-        const T* qb = reinterpret_cast<const T*>(A.q) + b * A.q_sb + h * A.q_sh +
-                      (int64_t)n * C * A.q_ss;
-        for (int idx = threadIdx.x; idx < kRows * (DH / VE); idx += kThreads) {
-            const int t = idx / (DH / VE), d = (idx % (DH / VE)) * VE;
-            uint4 u = make_uint4(0u, 0u, 0u, 0u);
-            if (t < rows) u = *reinterpret_cast<const uint4*>(qb + (int64_t)t * A.q_ss + d);
-            *reinterpret_cast<uint4*>(sQ + t * QS + d) = u;
-        }
-    }
-    for (int i = threadIdx.x; i < SP; i += kThreads) {
+    for (int i = threadIdx.x; i < A.SPP; i += kThreads) {
         sPk[i] = 0u;
         sFirst[i] = kNoRow;
     }
     for (int i = threadIdx.x; i < kRows * BW; i += kThreads) sBits[i] = 0u;
-    __syncthreads();
-    for (int t = w; t < kRows; t += kWaves) {
-        float s = 0.0f;
-        for (int d = l; d < DH; d += kWave) {
-            const float x = Elem<DT>::ld(sQ, t * QS + d);
-            s = fmaf(x, x, s);
+    if (threadIdx.x < 8) sScal[threadIdx.x] = 0;
+
+    // ---- stage 1, per 32-row block -----------------------------------------------------------
+    for (int r0 = 0; r0 < rows; r0 += kBlk) {
+        const int brows = rows - r0 < kBlk ? rows - r0 : kBlk;
+        load_block<T, DH>(sQ, qg, A.q_ss, r0, rows);
+        __syncthreads();
+        for (int r = w; r < kBlk; r += kWaves) {
+            float x = 0.0f;
+            for (int d = l; d < DH; d += kWave) {
+                const float e = Elem<DT>::ld(sQ, r * DH + d);
+                x = fmaf(e, e, x);
+            }
+            x = wsum(x);
+            if (l == 0 && r0 + r < kRows) sQn[r0 + r] = sqrtf(x);
         }
-        s = wave_sum(s);
-        if (l == 0) sQn[t] = sqrtf(s);
+        if (use_mfma)
+            scores_block_mfma<DH>(reinterpret_cast<const uint16_t*>(sQ), P,
+                                  [&](int i) { return reinterpret_cast<const uint16_t*>(crow(i)); },
+                                  sS, SP, scale,
+                                  r0 == 0 ? reinterpret_cast<uint32_t*>(&sScal[1]) : nullptr);
+        else
+            for (int idx = threadIdx.x; idx < brows * P; idx += kThreads)
+                sS[(idx / P) * SP + idx % P] = canon_dot<DT, DH>(sQ + (idx / P) * DH, crow(idx % P), scale);
+        __syncthreads();
+        const float ds1 = use_mfma ? kDeltaRel * __uint_as_float((uint32_t)sScal[1]) * scale * 1.01f : 0.0f;
+        const int kreq = A.Kc < P ? A.Kc : P;
+        dispatch_j(P, [&](auto jt) {
+            constexpr int J = decltype(jt)::value;
+            for (int r = w; r < brows; r += kWaves) {
+                const int t = r0 + r;
+                float v[J];
+#pragma unroll
+                for (int j = 0; j < J; ++j) {
+                    const int i = l + 64 * j;
+                    v[j] = i < P ? sS[r * SP + i] : -INFINITY;
+                }
+                const T* qr = sQ + r * DH;
+                row_request<J>(t, v, kreq, ds1 * sQn[t],
+                               [&](int i) { return canon_dot<DT, DH>(qr, crow(i), scale); }, sPk,
+                               sFirst, sBits, BW, &amb1);
+            }
+        });
+        __syncthreads();
     }
-
-    // ---- stage 1 scores ----------------------------------------------------------------------
-    const T* ckb = reinterpret_cast<const T*>(A.ck) + b * A.ck_sb + kvh * A.ck_sh;
-    auto crow = [&](int i) -> const T* { return ckb + (int64_t)(f_hi + i) * DH; };
-    auto canon1 = [&](int t, int i) { return canon_dot<DT, DH>(sQ + t * QS, crow(i), scale); };
-    if (use_mfma)
-        scores_mfma<DH, QS>(reinterpret_cast<const uint16_t*>(sQ), rows, P,
-                            [&](int i) { return reinterpret_cast<const uint16_t*>(crow(i)); },
-                            sS, SP, sKn, scale);
-    else
-        for (int idx = threadIdx.x; idx < rows * P; idx += kThreads)
-            sS[(idx / P) * SP + idx % P] = canon1(idx / P, idx % P);
-    __syncthreads();
-    float knmax = 0.0f, qnmax = 0.0f;
-    if (use_mfma) {
+    float qnmax = 0.0f;
+    {
         float x = 0.0f;
-        for (int i = l; i < P; i += kWave) x = fmaxf(x, sKn[i]);
-        knmax = wave_max(x);
-        qnmax = wave_max(l < rows ? sQn[l] : 0.0f);
+        if (l < rows) x = sQn[l];
+        qnmax = wmax(x);
     }
-    const float ds1 = use_mfma ? kDeltaRel * knmax * scale * 1.01f : 0.0f;
-
-    // ---- stage 1 per-row requests ------------------------------------------------------------
-    const int kreq = A.Kc < P ? A.Kc : P;
-    dispatch_j(P, [&](auto jt) {
-        constexpr int J = decltype(jt)::value;
-        row_requests<J>(sS, SP, rows, P, kreq, [](int, int) { return true; }, sQn, ds1, canon1,
-                        sPk, sFirst, sBits, BW, &amb1);
-    });
-    __syncthreads();
 
     // ---- stage 1 pooled selection + forced previous chunk (wave 0) -------------------------
-    const float dpool = ds1 * qnmax;
     if (w == 0) {
+        const float dpool = use_mfma ? kDeltaRel * __uint_as_float((uint32_t)sScal[1]) * qnmax * scale * 1.01f : 0.0f;
         const int prev = n - 1;
         const int ip = (n > 0 && prev >= f_hi && prev < l_lo) ? prev - f_hi : -1;
         int cnt = 0;
         dispatch_j(P, [&](auto jt) {
             constexpr int J = decltype(jt)::value;
-            cnt = pooled_select<J>(P, A.Kc, rows, sS, SP, sBits, BW, sPk, sFirst, dpool, canon1,
-                                   ip, f_hi, sSel, sThr, &amb1p);
+            cnt = pooled_select<J>(P, A.Kc, rows, sBits, BW, sPk, sFirst, dpool, canonG1, ip,
+                                   f_hi, sSel, sThr, &amb1p);
         });
         if (l == 0) sScal[0] = cnt;
     }
@@ -533,13 +603,13 @@ __global__ __launch_bounds__(kThreads) void route_prefill_kernel(RouteArgs A) {
     }
     if (threadIdx.x == 0) A.n_sel[o] = nsel;
 
-    // ---- stage 2: groups of the selected chunks ---------------------------------------------
+    // ---- stage 2: groups of the selected chunks, all rows ----------------------------------
     const int T2 = nsel * M;
     if (A.Kg == 0 || A.Kgr == 0 || nsel == 0) {
         for (int i = threadIdx.x; i < Kgw; i += kThreads) out_og[i] = out_ot[i] = -1;
         if (threadIdx.x == 0) A.n_open[o] = 0;
     } else {
-        for (int i = threadIdx.x; i < SP; i += kThreads) {
+        for (int i = threadIdx.x; i < A.SPP; i += kThreads) {
             sPk[i] = 0u;
             sFirst[i] = kNoRow;
         }
@@ -548,44 +618,49 @@ __global__ __launch_bounds__(kThreads) void route_prefill_kernel(RouteArgs A) {
         auto grow = [&](int i) -> const T* {
             return gkb + ((int64_t)sSel[i / M] * M + (i % M)) * DH;
         };
-        auto canon2 = [&](int t, int i) { return canon_dot<DT, DH>(sQ + t * QS, grow(i), scale); };
-        if (use_mfma)
-            scores_mfma<DH, QS>(reinterpret_cast<const uint16_t*>(sQ), rows, T2,
-                                [&](int i) { return reinterpret_cast<const uint16_t*>(grow(i)); },
-                                sS, SP, sKn, scale);
-        else
-            for (int idx = threadIdx.x; idx < rows * T2; idx += kThreads)
-                sS[(idx / T2) * SP + idx % T2] = canon2(idx / T2, idx % T2);
-        __syncthreads();
-        float kn2 = 0.0f;
-        if (use_mfma) {
-            float x = 0.0f;
-            for (int i = l; i < T2; i += kWave) x = fmaxf(x, sKn[i]);
-            kn2 = wave_max(x);
+        auto canonG2 = [&](int t, int i) { return canon_dot<DT, DH>(qg + t * A.q_ss, grow(i), scale); };
+        for (int r0 = 0; r0 < rows; r0 += kBlk) {
+            const int brows = rows - r0 < kBlk ? rows - r0 : kBlk;
+            load_block<T, DH>(sQ, qg, A.q_ss, r0, rows);
+            __syncthreads();
+            if (use_mfma)
+                scores_block_mfma<DH>(reinterpret_cast<const uint16_t*>(sQ), T2,
+                                      [&](int i) { return reinterpret_cast<const uint16_t*>(grow(i)); },
+                                      sS + r0 * SP2, SP2, scale,
+                                      r0 == 0 ? reinterpret_cast<uint32_t*>(&sScal[2]) : nullptr);
+            else
+                for (int idx = threadIdx.x; idx < brows * T2; idx += kThreads)
+                    sS[(r0 + idx / T2) * SP2 + idx % T2] =
+                        canon_dot<DT, DH>(sQ + (idx / T2) * DH, grow(idx % T2), scale);
+            __syncthreads();
         }
-        const float ds2 = use_mfma ? kDeltaRel * kn2 * scale * 1.01f : 0.0f;
+        const float ds2 = use_mfma ? kDeltaRel * __uint_as_float((uint32_t)sScal[2]) * scale * 1.01f : 0.0f;
         dispatch_j(T2, [&](auto jt) {
             constexpr int J = decltype(jt)::value;
-            row_requests<J>(sS, SP, rows, T2, A.Kgr,
-                            [&](int t, int i) { return sThr[i / M] <= t; }, sQn, ds2, canon2, sPk,
-                            sFirst, sBits, BW, &amb2);
-        });
-        __syncthreads();
-        if (w == 0) {
-            int cnt = 0;
-            const float dpool2 = ds2 * qnmax;
-            dispatch_j(T2, [&](auto jt) {
-                constexpr int J = decltype(jt)::value;
-                const int l2 = lane_id();
+            for (int t = w; t < rows; t += kWaves) {
                 float v[J];
 #pragma unroll
                 for (int j = 0; j < J; ++j) {
-                    const int i = l2 + 64 * j;
+                    const int i = l + 64 * j;
+                    v[j] = (i < T2 && sThr[i / M] <= t) ? sS[t * SP2 + i] : -INFINITY;
+                }
+                row_request<J>(t, v, A.Kgr, ds2 * sQn[t], [&](int i) { return canonG2(t, i); },
+                               sPk, sFirst, sBits, BW, &amb2);
+            }
+        });
+        __syncthreads();
+        if (w == 0) {
+            const float dpool2 = ds2 * qnmax;
+            int cnt = 0;
+            dispatch_j(T2, [&](auto jt) {
+                constexpr int J = decltype(jt)::value;
+                float v[J];
+#pragma unroll
+                for (int j = 0; j < J; ++j) {
+                    const int i = l + 64 * j;
                     v[j] = (i < T2 && sFirst[i] < kNoRow) ? okey_inv(sPk[i]) : -INFINITY;
                 }
-                auto canon_pool2 = [&](int i) {
-                    return pooled_exact(i, rows, sS, SP, sBits, BW, sPk, dpool2, canon2);
-                };
+                auto canon_pool2 = [&](int i) { return pooled_exact(i, rows, sBits, BW, canonG2); };
                 const uint32_t op = select_certified<J>(v, A.Kg, dpool2, canon_pool2, &amb2p);
                 int base = 0;
 #pragma unroll
@@ -593,7 +668,7 @@ __global__ __launch_bounds__(kThreads) void route_prefill_kernel(RouteArgs A) {
                     const bool m = (op >> j) & 1u;
                     const uint64_t bal = __ballot(m);
                     if (m) {
-                        const int i = l2 + 64 * j;
+                        const int i = l + 64 * j;
                         const int pos = base + lanes_below(bal);
                         if (pos < Kgw) {
                             out_og[pos] = sSel[i / M] * M + (i % M);
@@ -674,16 +749,17 @@ extern "C" int hga_route_prefill(const hga_config* cfg, int32_t S, const void* q
     HGA_REQUIRE(Pmax <= kJ * 64 && T2max <= kJ * 64, HGA_ERR_UNSUPPORTED,
                 "hga_route_prefill: routing pool %d / group candidates %d exceed %d", Pmax,
                 T2max, kJ * 64);
-    int SP = (Pmax > T2max ? Pmax : T2max) + 1;
-    if (SP % 2 == 0) ++SP;
-    a.SP = SP;
-    a.BW = (SP + 31) / 32;
+    auto odd_above = [](int x) { return (x + 1) | 1; };   // smallest odd stride > x
+    a.SP = odd_above(Pmax);
+    a.SP2 = odd_above(T2max);
+    a.SSZ = ((kBlk * a.SP > kRows * a.SP2 ? kBlk * a.SP : kRows * a.SP2) + 3) / 4 * 4;
+    a.SPP = (Pmax > T2max ? Pmax : T2max) + 1;
+    a.BW = (a.SPP + 31) / 32;
     const int D = cfg->head_dim;
     const size_t esz = cfg->dtype == HGA_DTYPE_BF16 ? 2 : 4;
-    const size_t lds = sizeof(float) * (size_t)kRows * SP + esz * kRows * (D + 8) +
-                       sizeof(float) * (SP + kRows) + sizeof(uint32_t) * SP + sizeof(int) * SP +
-                       sizeof(uint32_t) * (size_t)kRows * a.BW + sizeof(int) * 2 * kMaxSel +
-                       sizeof(int) * 8 + sizeof(float) * 8;
+    const size_t lds = sizeof(float) * (size_t)a.SSZ + esz * kBlk * D + sizeof(float) * kRows +
+                       2 * sizeof(int) * (size_t)a.SPP + sizeof(uint32_t) * (size_t)kRows * a.BW +
+                       sizeof(int) * (2 * kMaxSel + 8);
     HGA_REQUIRE(lds <= 163840, HGA_ERR_UNSUPPORTED,
                 "hga_route_prefill: %zu bytes of LDS needed (pool %d, head_dim %d)", lds, Pmax, D);
     {
