@@ -2,9 +2,10 @@
 the reference's HierarchicalGlobalAttentionRouted / ChunkRouter interfaces."""
 from ._lib import HgaError, build, lib
 from .routed_attention import HierarchicalGlobalAttentionRouted, RMSNorm
-from .router import ChunkPlacementPolicy, ChunkRouter, RoutedKV, RouterConfig, VramKVCacheStore
+from .router import (ChunkPlacementPolicy, ChunkRouter, RamKVCacheStore, RoutedKV, RouterConfig,
+                     VramKVCacheStore)
 
 __all__ = [
     "HierarchicalGlobalAttentionRouted", "RMSNorm", "ChunkPlacementPolicy", "ChunkRouter",
-    "RoutedKV", "RouterConfig", "VramKVCacheStore", "HgaError", "build", "lib",
+    "RoutedKV", "RouterConfig", "VramKVCacheStore", "RamKVCacheStore", "HgaError", "build", "lib",
 ]

@@ -46,6 +46,12 @@ SIGNATURES = {
     "hga_attend_prefill": ([_CFG, _i32, _vp, _i64, _i64, _i64, _vp, _i64, _i64, _i64, _vp,
                             _i64, _i64, _i64, _vp, _vp, _i32, _vp, _i64, _i64, _i64, _vp],
                            ctypes.c_int),
+    "hga_decode_widths": ([_CFG, _i32, _I32P, _I32P], _i32),
+    "hga_route_decode": ([_CFG, _i32, _i32, _vp, _i64, _i64, _i64, _vp, _i64, _i64, _vp, _i64,
+                          _i64, _vp, _vp, _vp, _vp, _vp, _vp, _vp], ctypes.c_int),
+    "hga_attend_decode": ([_CFG, _i32, _i32, _i64, _vp, _i64, _i64, _i64, _vp, _vp, _i64, _i64,
+                           _i64, _i32, _vp, _vp, _i64, _i64, _i64, _vp, _vp, _i64, _i64, _i64,
+                           _i32, _vp, _vp, _i32, _vp, _i64, _i64, _i64, _vp], ctypes.c_int),
 }
 
 _lib = None

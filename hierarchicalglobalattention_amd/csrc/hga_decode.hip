@@ -1,0 +1,590 @@
+// Decode path: routing of an L-token block inside the active chunk (ChunkRouter._route_decision,
+// chunk_router.py:187-277) and the attention over its working set (decode_block,
+// chunk_router.py:279-407).
+//
+// Router: one 256-thread workgroup per (batch, query head).  Decode scores are few (L rows x
+// pool), so they are computed directly with the canonical fp32 FMA chain (no MFMA pre-pass, no
+// certification needed); the wave selections of hga_select.h handle up to 2048 pool chunks
+// (128K-token contexts at C = 64).
+//
+// Attention: one 256-thread workgroup per (batch, query head); the key sequence [first window |
+// last window | opened groups | active chunk] is split over the 4 waves, lanes score one key
+// each (16-byte loads of the key row), the online softmax runs per wave, values are
+// accumulated with lanes over the head dim, and the 4 partial states are merged in LDS.  Opened
+// groups can be read straight from a pinned host record (zero copy over PCIe), so only the
+// routed groups cross the link.
+#include "hga_common.h"
+#include "hga_select.h"
+
+namespace hga {
+namespace {
+
+constexpr int kDT = 256;            // threads
+constexpr int kDW = kDT / kWave;     // waves
+constexpr int kMaxL = 64;
+constexpr int kDecJ = 32;            // <= 2048 pool candidates
+
+struct DecRouteArgs {
+    const void* q;
+    int64_t q_sb, q_sh, q_ss;
+    const void* ck;
+    int64_t ck_sb, ck_sh;
+    const void* gk;
+    int64_t gk_sb, gk_sh;
+    int32_t *mid, *mid_thr, *n_mid, *open_grp, *open_thr, *n_open;
+    int B, H, KVH, L, n_closed, M, kf, kl, Kc, Kg, Kgr, SPD;
+    float scale;
+};
+
+template <int DT, int DH>
+__device__ __forceinline__ float cdot(const typename Elem<DT>::T* q, const typename Elem<DT>::T* k,
+                                      float scale) {
+    // canonical chain: sequential fp32 FMA over d, then * scale, -0 -> +0
+    float acc = 0.0f;
+    if constexpr (DT == HGA_DTYPE_BF16) {
+#pragma unroll 4
+        for (int i = 0; i < DH / 8; ++i) {
+            const uint4 qq = *reinterpret_cast<const uint4*>(q + 8 * i);
+            const uint4 kk = *reinterpret_cast<const uint4*>(k + 8 * i);
+            const uint32_t qw[4] = {qq.x, qq.y, qq.z, qq.w}, kw[4] = {kk.x, kk.y, kk.z, kk.w};
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                acc = fmaf(__uint_as_float(qw[e] << 16), __uint_as_float(kw[e] << 16), acc);
+                acc = fmaf(__uint_as_float(qw[e] & 0xffff0000u), __uint_as_float(kw[e] & 0xffff0000u), acc);
+            }
+        }
+    } else {
+#pragma unroll 4
+        for (int i = 0; i < DH / 4; ++i) {
+            const float4 qq = *reinterpret_cast<const float4*>(q + 4 * i);
+            const float4 kk = *reinterpret_cast<const float4*>(k + 4 * i);
+            acc = fmaf(qq.x, kk.x, acc);
+            acc = fmaf(qq.y, kk.y, acc);
+            acc = fmaf(qq.z, kk.z, acc);
+            acc = fmaf(qq.w, kk.w, acc);
+        }
+    }
+    const float s = acc * scale;
+    return s == 0.0f ? 0.0f : s;
+}
+
+// Wave-wide exact top-k of LDS values vals[0..n) (-inf excluded); returns member bits.
+template <int J>
+__device__ __forceinline__ uint32_t topk_lds(const float* vals, int n, int k) {
+    const int l = lane_id();
+    float v[J];
+    uint32_t kv[J];
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+        const int i = l + 64 * j;
+        v[j] = i < n ? vals[i] : -INFINITY;
+        kv[j] = v[j] == -INFINITY ? 0u : okey(v[j]);
+    }
+    return exact_topk<J>(kv, v, k);
+}
+
+template <int DT, int DH>
+__global__ __launch_bounds__(kDT) void route_decode_kernel(DecRouteArgs A) {
+    typedef typename Elem<DT>::T T;
+    extern __shared__ __align__(16) unsigned char smem_raw[];
+    const int SPD = A.SPD, M = A.M, L = A.L;
+    T* sQ = reinterpret_cast<T*>(smem_raw);                     // [L][DH]
+    float* sS = reinterpret_cast<float*>(sQ + L * DH);          // [L][SPD]
+    float* sPool = sS + L * SPD;                                // [SPD]
+    int* sFirst = reinterpret_cast<int*>(sPool + SPD);          // [SPD]
+    int* sSel = sFirst + SPD;                                   // [64] sorted chunk ids
+    int* sThr = sSel + 64;                                      // [64] -1 = never visible
+    int* sScal = sThr + 64;                                     // [8]
+
+    const int bh = blockIdx.x, b = bh / A.H, h = bh % A.H, kvh = h / (A.H / A.KVH);
+    const int w = threadIdx.x / kWave, l = lane_id();
+    int f_hi, l_lo;
+    windows(A.n_closed, A.kf, A.kl, &f_hi, &l_lo);
+    const int nmid = l_lo > f_hi ? l_lo - f_hi : 0;
+    const int Kcw = A.Kc > 0 ? A.Kc : 1, Kgw = A.Kg > 0 ? A.Kg : 1;
+    int32_t* o_mid = A.mid + (int64_t)bh * Kcw;
+    int32_t* o_mth = A.mid_thr + (int64_t)bh * Kcw;
+    int32_t* o_og = A.open_grp + (int64_t)bh * Kgw;
+    int32_t* o_ot = A.open_thr + (int64_t)bh * Kgw;
+    if (A.Kc == 0) {
+        for (int i = threadIdx.x; i < Kcw; i += kDT) o_mid[i] = o_mth[i] = -1;
+        for (int i = threadIdx.x; i < Kgw; i += kDT) o_og[i] = o_ot[i] = -1;
+        if (threadIdx.x == 0) A.n_mid[bh] = A.n_open[bh] = 0;
+        return;
+    }
+    const float scale = A.scale;
+    {
+        constexpr int VE = 16 / (int)sizeof(T);
+        const T* qg = reinterpret_cast<const T*>(A.q) + b * A.q_sb + h * A.q_sh;
+        for (int idx = threadIdx.x; idx < L * (DH / VE); idx += kDT) {
+            const int r = idx / (DH / VE), d = (idx % (DH / VE)) * VE;
+            *reinterpret_cast<uint4*>(sQ + r * DH + d) =
+                *reinterpret_cast<const uint4*>(qg + (int64_t)r * A.q_ss + d);
+        }
+    }
+    for (int i = threadIdx.x; i < SPD; i += kDT) sFirst[i] = kNoRow;
+    __syncthreads();
+    const T* ckb = reinterpret_cast<const T*>(A.ck) + b * A.ck_sb + kvh * A.ck_sh;
+    for (int idx = threadIdx.x; idx < L * nmid; idx += kDT) {
+        const int r = idx / nmid, i = idx % nmid;
+        sS[r * SPD + i] = cdot<DT, DH>(sQ + r * DH, ckb + (int64_t)(f_hi + i) * DH, scale);
+    }
+    __syncthreads();
+    for (int i = threadIdx.x; i < nmid; i += kDT) {       // pooled over all rows (:227)
+        float m = -INFINITY;
+        for (int r = 0; r < L; ++r) m = fmaxf(m, sS[r * SPD + i]);
+        sPool[i] = m;
+    }
+    __syncthreads();
+    // per-row requests (:230) -> first requesting row
+    dispatch_j<kDecJ>(nmid, [&](auto jt) {
+        constexpr int J = decltype(jt)::value;
+        for (int r = w; r < L; r += kDW) {
+            const uint32_t mem = topk_lds<J>(sS + r * SPD, nmid, A.Kc);
+#pragma unroll
+            for (int j = 0; j < J; ++j)
+                if ((mem >> j) & 1u) atomicMin(&sFirst[l + 64 * j], r);
+        }
+    });
+    __syncthreads();
+    if (w == 0) {
+        dispatch_j<kDecJ>(nmid, [&](auto jt) {
+            constexpr int J = decltype(jt)::value;
+            uint32_t sel = topk_lds<J>(sPool, nmid, A.Kc);
+            const int prev = A.n_closed - 1;
+            const int ip = (prev >= f_hi && prev < l_lo) ? prev - f_hi : -1;   // (:232-241)
+            if (ip >= 0 && __ballot(((sel >> (ip / 64)) & 1u) && l == ip % 64) == 0) {
+                // evict the last-ranked selected chunk (lowest pooled score, highest id)
+                uint32_t worst = 0xffffffffu;
+#pragma unroll
+                for (int j = 0; j < J; ++j)
+                    if ((sel >> j) & 1u) worst = min(worst, okey(sPool[l + 64 * j]));
+                worst = (uint32_t)wave_reduce_bits((int)worst, [](int a, int c) {
+                    return (int)min((uint32_t)a, (uint32_t)c);
+                });
+                int victim = -1;
+#pragma unroll
+                for (int j = J - 1; j >= 0; --j) {
+                    const uint64_t m = __ballot(((sel >> j) & 1u) && okey(sPool[l + 64 * j]) == worst);
+                    if (victim < 0 && m) victim = 64 * j + 63 - __clzll(m);
+                }
+                if (victim >= 0 && l == victim % 64) sel &= ~(1u << (victim / 64));
+                if (l == ip % 64) sel |= 1u << (ip / 64);
+            }
+            int base = 0, nvis = 0;
+#pragma unroll
+            for (int j = 0; j < J; ++j) {
+                const int i = l + 64 * j;
+                const bool m = (sel >> j) & 1u;
+                const int thr = i == ip ? 0 : (i < nmid && sFirst[i] < kNoRow ? sFirst[i] : -1);
+                const uint64_t bal = __ballot(m);
+                if (m) {
+                    sSel[base + lanes_below(bal)] = f_hi + i;
+                    sThr[base + lanes_below(bal)] = thr;
+                }
+                base += __popcll(bal);
+                const uint64_t vb = __ballot(m && thr >= 0);
+                if (m && thr >= 0 && nvis + lanes_below(vb) < Kcw) {
+                    o_mid[nvis + lanes_below(vb)] = f_hi + i;
+                    o_mth[nvis + lanes_below(vb)] = thr;
+                }
+                nvis += __popcll(vb);
+            }
+            for (int i = nvis + l; i < Kcw; i += kWave) o_mid[i] = o_mth[i] = -1;
+            if (l == 0) {
+                A.n_mid[bh] = nvis;
+                sScal[0] = base;
+            }
+        });
+    }
+    __syncthreads();
+    const int nsel = sScal[0];
+    const int T2 = nsel * M;
+    if (A.Kg == 0 || T2 == 0) {
+        for (int i = threadIdx.x; i < Kgw; i += kDT) o_og[i] = o_ot[i] = -1;
+        if (threadIdx.x == 0) A.n_open[bh] = 0;
+        return;
+    }
+    // ---- groups of the selected chunks (:256-276) --------------------------------------------
+    const T* gkb = reinterpret_cast<const T*>(A.gk) + b * A.gk_sb + kvh * A.gk_sh;
+    for (int idx = threadIdx.x; idx < L * T2; idx += kDT) {
+        const int r = idx / T2, i = idx % T2;
+        sS[r * SPD + i] = cdot<DT, DH>(sQ + r * DH, gkb + ((int64_t)sSel[i / M] * M + i % M) * DH, scale);
+    }
+    for (int i = threadIdx.x; i < T2; i += kDT) sFirst[i] = kNoRow;
+    __syncthreads();
+    for (int i = threadIdx.x; i < T2; i += kDT) {
+        float m = -INFINITY;
+        for (int r = 0; r < L; ++r) m = fmaxf(m, sS[r * SPD + i]);
+        sPool[i] = m;
+    }
+    __syncthreads();
+    dispatch_j<kDecJ>(T2, [&](auto jt) {
+        constexpr int J = decltype(jt)::value;
+        for (int r = w; r < L; r += kDW) {
+            const uint32_t mem = topk_lds<J>(sS + r * SPD, T2, A.Kgr);
+#pragma unroll
+            for (int j = 0; j < J; ++j)
+                if ((mem >> j) & 1u) atomicMin(&sFirst[l + 64 * j], r);
+        }
+    });
+    __syncthreads();
+    if (w == 0) {
+        dispatch_j<kDecJ>(T2, [&](auto jt) {
+            constexpr int J = decltype(jt)::value;
+            const uint32_t op = topk_lds<J>(sPool, T2, A.Kg);
+            int base = 0;
+#pragma unroll
+            for (int j = 0; j < J; ++j) {
+                const int i = l + 64 * j;
+                int thr = -1;
+                if (((op >> j) & 1u) && sFirst[i] < kNoRow && sThr[i / M] >= 0)
+                    thr = sFirst[i] > sThr[i / M] ? sFirst[i] : sThr[i / M];
+                const uint64_t bal = __ballot(thr >= 0);
+                if (thr >= 0 && base + lanes_below(bal) < Kgw) {
+                    o_og[base + lanes_below(bal)] = sSel[i / M] * M + i % M;
+                    o_ot[base + lanes_below(bal)] = thr;
+                }
+                base += __popcll(bal);
+            }
+            for (int i = base + l; i < Kgw; i += kWave) o_og[i] = o_ot[i] = -1;
+            if (l == 0) A.n_open[bh] = base;
+        });
+    }
+}
+
+// ------------------------------------------------------------------------------------------
+// decode attention
+// ------------------------------------------------------------------------------------------
+struct DecAttnArgs {
+    const void* q;
+    int64_t q_sb, q_sh, q_ss;
+    const void *kr, *vr;
+    int64_t r_sb, r_sh, r_ss;
+    const void *kfst, *vfst;
+    int64_t f_sb, f_sh, f_ss;
+    const void *kd, *vd;
+    int64_t d_sb, d_sh, d_ss;
+    const int32_t* open_grp;
+    const int32_t* open_thr;
+    void* out;
+    int64_t o_sb, o_sh, o_ss;
+    int64_t start_pos;
+    int B, H, KVH, L, n_closed, C, gs, M, kf, kl, Kg, ring;
+    float scale;
+};
+
+template <int DT, int DH>
+__global__ __launch_bounds__(kDT) void attend_decode_kernel(DecAttnArgs A) {
+    typedef typename Elem<DT>::T T;
+    constexpr int DPL = DH / kWave > 0 ? DH / kWave : 1;   // dims per lane
+    __shared__ float sQ[DH];
+    __shared__ float sM[kDW], sLs[kDW];
+    __shared__ float sAcc[kDW][DH];
+    __shared__ int sOG[256], sOT[256];
+    const int bh = blockIdx.x, b = bh / A.H, h = bh % A.H, kvh = h / (A.H / A.KVH);
+    const int w = threadIdx.x / kWave, l = lane_id();
+    const int C = A.C, gs = A.gs, M = A.M;
+    int f_hi, l_lo;
+    windows(A.n_closed, A.kf, A.kl, &f_hi, &l_lo);
+    const int Kgw = A.Kg > 0 ? A.Kg : 1;
+    for (int i = threadIdx.x; i < A.Kg; i += kDT) {
+        sOG[i] = A.open_grp[(int64_t)bh * Kgw + i];
+        sOT[i] = A.open_thr[(int64_t)bh * Kgw + i];
+    }
+    __syncthreads();
+    int nopen = 0;
+    for (int i = 0; i < A.Kg; ++i)
+        if (sOG[i] >= 0 && sOT[i] >= 0) nopen = i + 1;
+    const int64_t c0 = A.start_pos - (int64_t)A.n_closed * C;
+    const int a1 = f_hi * C, a2 = a1 + (A.n_closed - l_lo) * C, a3 = a2 + nopen * gs;
+    const int a4 = a3 + (int)c0 + A.L;
+    const T* kr = reinterpret_cast<const T*>(A.kr) + b * A.r_sb + kvh * A.r_sh;
+    const T* vr = reinterpret_cast<const T*>(A.vr) + b * A.r_sb + kvh * A.r_sh;
+    const T* kf = reinterpret_cast<const T*>(A.kfst) + b * A.f_sb + kvh * A.f_sh;
+    const T* vf = reinterpret_cast<const T*>(A.vfst) + b * A.f_sb + kvh * A.f_sh;
+    const T* kd = reinterpret_cast<const T*>(A.kd) + b * A.d_sb + kvh * A.d_sh;
+    const T* vd = reinterpret_cast<const T*>(A.vd) + b * A.d_sb + kvh * A.d_sh;
+    // key k -> (key row, value row, first visible query row)
+    auto key = [&](int k, const T*& kp, const T*& vp, int& thr) {
+        if (k < a1) {
+            kp = kf + (int64_t)k * A.f_ss;
+            vp = vf + (int64_t)k * A.f_ss;
+            thr = 0;
+            return;
+        }
+        int64_t pos;
+        if (k < a2) {
+            pos = (int64_t)l_lo * C + (k - a1);
+            thr = 0;
+        } else if (k < a3) {
+            const int g = (k - a2) / gs, e = (k - a2) % gs, grp = sOG[g];
+            if (grp < 0 || grp >= A.n_closed * M || sOT[g] < 0) {   // padding / invalid id
+                kp = vp = nullptr;
+                thr = kNoRow;
+                return;
+            }
+            const int64_t p = (int64_t)(grp / M) * C + (grp % M) * gs + e;
+            kp = kd + p * A.d_ss;
+            vp = vd + p * A.d_ss;
+            thr = sOT[g];
+            return;
+        } else {
+            pos = (int64_t)A.n_closed * C + (k - a3);
+            thr = (int)((k - a3) - c0);
+            if (thr < 0) thr = 0;
+        }
+        const int64_t slot = A.ring > 0 ? ((pos / C) % A.ring) * C + pos % C : pos;
+        kp = kr + slot * A.r_ss;
+        vp = vr + slot * A.r_ss;
+    };
+    const int per = (a4 + kDW - 1) / kDW;
+    const int k_lo = w * per, k_hi = (w + 1) * per < a4 ? (w + 1) * per : a4;
+    const T* qg = reinterpret_cast<const T*>(A.q) + b * A.q_sb + h * A.q_sh;
+    T* og = reinterpret_cast<T*>(A.out) + b * A.o_sb + h * A.o_sh;
+    for (int row = 0; row < A.L; ++row) {
+        for (int d = threadIdx.x; d < DH; d += kDT) sQ[d] = Elem<DT>::ld(qg, (int64_t)row * A.q_ss + d);
+        __syncthreads();
+        float m_run = -INFINITY, l_run = 0.0f, acc[DPL];
+#pragma unroll
+        for (int e = 0; e < DPL; ++e) acc[e] = 0.0f;
+        for (int base = k_lo; base < k_hi; base += kWave) {
+            const int k = base + l;
+            const T* kp = nullptr;
+            const T* vp = nullptr;
+            int thr = kNoRow;
+            if (k < k_hi) key(k, kp, vp, thr);
+            float s = -INFINITY;
+            if (k < k_hi && row >= thr) {
+                float d0 = 0.0f;
+                for (int d = 0; d < DH; d += 8) {
+                    if constexpr (DT == HGA_DTYPE_BF16) {
+                        const uint4 u = *reinterpret_cast<const uint4*>(kp + d);
+                        const uint32_t wv[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) {
+                            d0 = fmaf(sQ[d + 2 * e], __uint_as_float(wv[e] << 16), d0);
+                            d0 = fmaf(sQ[d + 2 * e + 1], __uint_as_float(wv[e] & 0xffff0000u), d0);
+                        }
+                    } else {
+                        const float4 u0 = *reinterpret_cast<const float4*>(kp + d);
+                        const float4 u1 = *reinterpret_cast<const float4*>(kp + d + 4);
+                        d0 = fmaf(sQ[d], u0.x, d0); d0 = fmaf(sQ[d + 1], u0.y, d0);
+                        d0 = fmaf(sQ[d + 2], u0.z, d0); d0 = fmaf(sQ[d + 3], u0.w, d0);
+                        d0 = fmaf(sQ[d + 4], u1.x, d0); d0 = fmaf(sQ[d + 5], u1.y, d0);
+                        d0 = fmaf(sQ[d + 6], u1.z, d0); d0 = fmaf(sQ[d + 7], u1.w, d0);
+                    }
+                }
+                s = d0 * A.scale;
+            }
+            const float mx = wave_max(s);
+            const float m_new = fmaxf(m_run, mx);
+            const float m_use = m_new == -INFINITY ? 0.0f : m_new;
+            const float alpha = expf(m_run - m_use);
+            const float p = expf(s - m_use);
+            l_run = l_run * alpha + wave_sum(p);
+            m_run = m_new;
+#pragma unroll
+            for (int e = 0; e < DPL; ++e) acc[e] *= alpha;
+            const int lim = k_hi - base < kWave ? k_hi - base : kWave;
+            const uint64_t vaddr = (uint64_t)vp;
+            for (int kk = 0; kk < lim; ++kk) {
+                const float pk = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(p), kk));
+                if (pk == 0.0f) continue;
+                const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)vaddr, kk);
+                const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(vaddr >> 32), kk);
+                const T* vrow = reinterpret_cast<const T*>(((uint64_t)hi << 32) | lo);
+#pragma unroll
+                for (int e = 0; e < DPL; ++e) {
+                    const int d = l + kWave * e;
+                    if (d < DH) acc[e] = fmaf(pk, Elem<DT>::ld(vrow, d), acc[e]);
+                }
+            }
+        }
+        if (l == 0) {
+            sM[w] = m_run;
+            sLs[w] = l_run;
+        }
+#pragma unroll
+        for (int e = 0; e < DPL; ++e)
+            if (l + kWave * e < DH) sAcc[w][l + kWave * e] = acc[e];
+        __syncthreads();
+        if (w == 0) {
+            float mt = -INFINITY;
+            for (int i = 0; i < kDW; ++i) mt = fmaxf(mt, sM[i]);
+            const float mu = mt == -INFINITY ? 0.0f : mt;
+            float lt = 0.0f;
+            for (int i = 0; i < kDW; ++i) lt += sLs[i] * expf(sM[i] - mu);
+            const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
+            for (int d = l; d < DH; d += kWave) {
+                float o = 0.0f;
+                for (int i = 0; i < kDW; ++i) o += sAcc[i][d] * expf(sM[i] - mu);
+                Elem<DT>::st(og, (int64_t)row * A.o_ss + d, o * inv);
+            }
+        }
+        __syncthreads();
+    }
+}
+
+}  // namespace
+}  // namespace hga
+
+extern "C" int32_t hga_decode_widths(const hga_config* cfg, int32_t n_closed, int32_t* Kc,
+                                     int32_t* Kg) {
+    using namespace hga;
+    int rc = check_config(cfg);
+    if (rc) return rc;
+    HGA_REQUIRE(n_closed >= 0, HGA_ERR_ARG, "negative n_closed");
+    int f_hi, l_lo;
+    windows(n_closed, cfg->keep_first, cfg->keep_last, &f_hi, &l_lo);
+    const int nmid = l_lo > f_hi ? l_lo - f_hi : 0;
+    const int M = cfg->chunk_size / cfg->group_size;
+    const int kc = (nmid > 0 && cfg->topk_chunks > 0) ? (cfg->topk_chunks < nmid ? cfg->topk_chunks : nmid) : 0;
+    const int kg = cfg->topk_groups > 0 ? (cfg->topk_groups < kc * M ? cfg->topk_groups : kc * M) : 0;
+    if (Kc) *Kc = kc;
+    if (Kg) *Kg = kg;
+    return HGA_OK;
+}
+
+extern "C" int hga_route_decode(const hga_config* cfg, int32_t L, int32_t n_closed, const void* q,
+                                int64_t q_sb, int64_t q_sh, int64_t q_ss, const void* chunk_k,
+                                int64_t ck_sb, int64_t ck_sh, const void* group_k, int64_t gk_sb,
+                                int64_t gk_sh, int32_t* mid, int32_t* mid_thr, int32_t* n_mid,
+                                int32_t* open_grp, int32_t* open_thr, int32_t* n_open,
+                                void* stream) {
+    using namespace hga;
+    int rc = check_config(cfg);
+    if (rc) return rc;
+    HGA_REQUIRE(q && mid && mid_thr && n_mid && open_grp && open_thr && n_open, HGA_ERR_ARG,
+                "hga_route_decode: NULL pointer");
+    HGA_REQUIRE(L >= 1 && L <= kMaxL, HGA_ERR_UNSUPPORTED, "hga_route_decode: L=%d outside [1, 64]", L);
+    HGA_REQUIRE(n_closed >= 0, HGA_ERR_ARG, "hga_route_decode: negative n_closed");
+    DecRouteArgs a{};
+    a.q = q; a.q_sb = q_sb; a.q_sh = q_sh; a.q_ss = q_ss;
+    a.ck = chunk_k; a.ck_sb = ck_sb; a.ck_sh = ck_sh;
+    a.gk = group_k; a.gk_sb = gk_sb; a.gk_sh = gk_sh;
+    a.mid = mid; a.mid_thr = mid_thr; a.n_mid = n_mid;
+    a.open_grp = open_grp; a.open_thr = open_thr; a.n_open = n_open;
+    a.B = cfg->batch; a.H = cfg->heads; a.KVH = cfg->kv_heads; a.L = L; a.n_closed = n_closed;
+    a.M = cfg->chunk_size / cfg->group_size; a.kf = cfg->keep_first; a.kl = cfg->keep_last;
+    hga_decode_widths(cfg, n_closed, &a.Kc, &a.Kg);
+    a.Kgr = cfg->topk_groups > 0 ? (cfg->topk_groups / 2 < a.Kc * a.M ? cfg->topk_groups / 2 : a.Kc * a.M) : 0;
+    a.scale = cfg->scale;
+    int f_hi, l_lo;
+    windows(n_closed, a.kf, a.kl, &f_hi, &l_lo);
+    const int nmid = l_lo > f_hi ? l_lo - f_hi : 0;
+    HGA_REQUIRE(a.Kc <= 64, HGA_ERR_UNSUPPORTED, "hga_route_decode: top-k chunks %d > 64", a.Kc);
+    HGA_REQUIRE(nmid <= kDecJ * 64 && a.Kc * a.M <= kDecJ * 64, HGA_ERR_UNSUPPORTED,
+                "hga_route_decode: pool %d exceeds %d chunks", nmid, kDecJ * 64);
+    const int W = (nmid > a.Kc * a.M ? nmid : a.Kc * a.M) + 1;
+    a.SPD = W | 1;
+    const int D = cfg->head_dim;
+    const size_t esz = cfg->dtype == HGA_DTYPE_BF16 ? 2 : 4;
+    const size_t lds = sizeof(float) * ((size_t)L * a.SPD + a.SPD) + sizeof(int) * (a.SPD + 128 + 8) +
+                       esz * (size_t)L * D + 16;
+    HGA_REQUIRE(lds <= 163840, HGA_ERR_UNSUPPORTED,
+                "hga_route_decode: %zu bytes of LDS for L=%d x pool %d", lds, L, nmid);
+    if (a.Kc > 0) {
+        const int64_t ve = esz == 2 ? 8 : 4;
+        HGA_REQUIRE(chunk_k && group_k, HGA_ERR_ARG, "hga_route_decode: NULL summaries");
+        const uintptr_t al = (uintptr_t)chunk_k | (uintptr_t)group_k | (uintptr_t)q;
+        HGA_REQUIRE(al % 16 == 0 && ((ck_sb | ck_sh | gk_sb | gk_sh | q_sb | q_sh | q_ss) % ve) == 0,
+                    HGA_ERR_ARG, "hga_route_decode: 16-byte aligned rows required");
+    }
+    hipStream_t st = (hipStream_t)stream;
+    const unsigned grid = (unsigned)(a.B * a.H);
+#define HGA_DEC_CASE(DTV, DHV)                                                                  \
+    if (cfg->dtype == DTV && D == DHV) {                                                        \
+        static bool attr = false;                                                               \
+        if (!attr) {                                                                            \
+            (void)hipFuncSetAttribute((const void*)route_decode_kernel<DTV, DHV>,                   \
+                                hipFuncAttributeMaxDynamicSharedMemorySize, 163840);            \
+            attr = true;                                                                        \
+        }                                                                                       \
+        route_decode_kernel<DTV, DHV><<<grid, kDT, lds, st>>>(a);                               \
+        return launch_status("hga_route_decode");                                               \
+    }
+    HGA_DEC_CASE(HGA_DTYPE_BF16, 128)
+    HGA_DEC_CASE(HGA_DTYPE_BF16, 64)
+    HGA_DEC_CASE(HGA_DTYPE_BF16, 32)
+    HGA_DEC_CASE(HGA_DTYPE_BF16, 16)
+    HGA_DEC_CASE(HGA_DTYPE_F32, 128)
+    HGA_DEC_CASE(HGA_DTYPE_F32, 64)
+    HGA_DEC_CASE(HGA_DTYPE_F32, 32)
+    HGA_DEC_CASE(HGA_DTYPE_F32, 16)
+#undef HGA_DEC_CASE
+    set_error("hga_route_decode: unsupported dtype/head_dim");
+    return HGA_ERR_UNSUPPORTED;
+}
+
+extern "C" int hga_attend_decode(const hga_config* cfg, int32_t L, int32_t n_closed,
+                                 int64_t start_pos, const void* q, int64_t q_sb, int64_t q_sh,
+                                 int64_t q_ss, const void* k_recent, const void* v_recent,
+                                 int64_t r_sb, int64_t r_sh, int64_t r_ss, int32_t ring_chunks,
+                                 const void* k_first, const void* v_first, int64_t f_sb,
+                                 int64_t f_sh, int64_t f_ss, const void* k_record,
+                                 const void* v_record, int64_t d_sb, int64_t d_sh, int64_t d_ss,
+                                 int32_t record_on_host, const int32_t* open_grp,
+                                 const int32_t* open_thr, int32_t Kg, void* out, int64_t o_sb,
+                                 int64_t o_sh, int64_t o_ss, void* stream) {
+    using namespace hga;
+    int rc = check_config(cfg);
+    if (rc) return rc;
+    HGA_REQUIRE(q && k_recent && v_recent && out && open_grp && open_thr, HGA_ERR_ARG,
+                "hga_attend_decode: NULL pointer");
+    HGA_REQUIRE(L >= 1 && L <= kMaxL && n_closed >= 0 && Kg >= 0 && Kg <= 256 && ring_chunks >= 0,
+                HGA_ERR_ARG, "hga_attend_decode: bad L/n_closed/Kg/ring");
+    const int C = cfg->chunk_size;
+    const int64_t c0 = start_pos - (int64_t)n_closed * C;
+    HGA_REQUIRE(c0 >= 0 && c0 + L <= C, HGA_ERR_ARG,
+                "hga_attend_decode: block [%lld, +%d) is not inside active chunk %d",
+                (long long)start_pos, L, n_closed);
+    int f_hi, l_lo;
+    windows(n_closed, cfg->keep_first, cfg->keep_last, &f_hi, &l_lo);
+    HGA_REQUIRE(f_hi == 0 || (k_first && v_first), HGA_ERR_ARG, "hga_attend_decode: first window source missing");
+    HGA_REQUIRE(ring_chunks == 0 || ring_chunks >= n_closed - l_lo + 1, HGA_ERR_ARG,
+                "hga_attend_decode: ring of %d chunks cannot hold the last window + active chunk",
+                ring_chunks);
+    DecAttnArgs a{};
+    a.q = q; a.q_sb = q_sb; a.q_sh = q_sh; a.q_ss = q_ss;
+    a.kr = k_recent; a.vr = v_recent; a.r_sb = r_sb; a.r_sh = r_sh; a.r_ss = r_ss;
+    a.kfst = k_first ? k_first : k_recent; a.vfst = v_first ? v_first : v_recent;
+    a.f_sb = f_sb; a.f_sh = f_sh; a.f_ss = f_ss;
+    a.kd = k_record ? k_record : k_recent; a.vd = v_record ? v_record : v_recent;
+    a.d_sb = d_sb; a.d_sh = d_sh; a.d_ss = d_ss;
+    if (record_on_host && k_record) {
+        void *dk = nullptr, *dv = nullptr;
+        hipError_t e1 = hipHostGetDevicePointer(&dk, const_cast<void*>(k_record), 0);
+        hipError_t e2 = hipHostGetDevicePointer(&dv, const_cast<void*>(v_record), 0);
+        HGA_REQUIRE(e1 == hipSuccess && e2 == hipSuccess, HGA_ERR_ARG,
+                    "hga_attend_decode: the host record is not pinned device-accessible memory");
+        a.kd = dk;
+        a.vd = dv;
+    }
+    a.open_grp = open_grp; a.open_thr = open_thr;
+    a.out = out; a.o_sb = o_sb; a.o_sh = o_sh; a.o_ss = o_ss;
+    a.start_pos = start_pos;
+    a.B = cfg->batch; a.H = cfg->heads; a.KVH = cfg->kv_heads; a.L = L; a.n_closed = n_closed;
+    a.C = C; a.gs = cfg->group_size; a.M = C / cfg->group_size; a.kf = cfg->keep_first;
+    a.kl = cfg->keep_last; a.Kg = Kg; a.ring = ring_chunks; a.scale = cfg->scale;
+    const int D = cfg->head_dim;
+    const int64_t ve = cfg->dtype == HGA_DTYPE_BF16 ? 8 : 4;
+    const uintptr_t al = (uintptr_t)a.kr | (uintptr_t)a.kfst | (uintptr_t)a.kd;
+    HGA_REQUIRE(al % 16 == 0 && ((r_sb | r_sh | r_ss | f_sb | f_sh | f_ss | d_sb | d_sh | d_ss) % ve) == 0,
+                HGA_ERR_ARG, "hga_attend_decode: 16-byte aligned key rows required");
+    hipStream_t st = (hipStream_t)stream;
+    const unsigned grid = (unsigned)(a.B * a.H);
+#define HGA_DA_CASE(DTV, DHV) \
+    if (cfg->dtype == DTV && D == DHV) { attend_decode_kernel<DTV, DHV><<<grid, kDT, 0, st>>>(a); return launch_status("hga_attend_decode"); }
+    HGA_DA_CASE(HGA_DTYPE_BF16, 128)
+    HGA_DA_CASE(HGA_DTYPE_BF16, 64)
+    HGA_DA_CASE(HGA_DTYPE_BF16, 32)
+    HGA_DA_CASE(HGA_DTYPE_BF16, 16)
+    HGA_DA_CASE(HGA_DTYPE_F32, 128)
+    HGA_DA_CASE(HGA_DTYPE_F32, 64)
+    HGA_DA_CASE(HGA_DTYPE_F32, 32)
+    HGA_DA_CASE(HGA_DTYPE_F32, 16)
+#undef HGA_DA_CASE
+    set_error("hga_attend_decode: unsupported dtype/head_dim");
+    return HGA_ERR_UNSUPPORTED;
+}

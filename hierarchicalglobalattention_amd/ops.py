@@ -187,3 +187,71 @@ def attend_prefill(cfg: HgaConfig, q: torch.Tensor, k: torch.Tensor, v: torch.Te
         ctypes.byref(cfg), S, _p(q), *_s4(q), _p(k), *_s4(k), _p(v), *_s4(v), _p(og), _p(ot),
         Kg, _p(out), *_s4(out), _stream()), "hga_attend_prefill")
     return out
+
+
+def decode_widths(cfg: HgaConfig, n_closed: int):
+    kc, kg = ctypes.c_int32(), ctypes.c_int32()
+    check(lib().hga_decode_widths(ctypes.byref(cfg), n_closed, ctypes.byref(kc), ctypes.byref(kg)),
+          "hga_decode_widths")
+    return kc.value, kg.value
+
+
+def route_decode(cfg: HgaConfig, q: torch.Tensor, chunk_k: torch.Tensor, group_k: torch.Tensor,
+                 n_closed: int) -> dict:
+    """Decode routing of q [B,H,L,Dh] against the store tables chunk_k [B,KVH,cap,Dh] and
+    group_k [B,KVH,cap,M,Dh] (first n_closed chunks valid).  Returns int32 tensors mid/mid_thr
+    [B,H,Kc], n_mid [B,H], open_grp/open_thr [B,H,Kg], n_open [B,H] (widths >= 1)."""
+    _dev(q, chunk_k, group_k)
+    B, H, L, D = q.shape
+    Kc, Kg = decode_widths(cfg, n_closed)
+    dev = q.device
+    r = dict(mid=torch.empty((B, H, max(Kc, 1)), dtype=torch.int32, device=dev),
+             mid_thr=torch.empty((B, H, max(Kc, 1)), dtype=torch.int32, device=dev),
+             n_mid=torch.empty((B, H), dtype=torch.int32, device=dev),
+             open_grp=torch.empty((B, H, max(Kg, 1)), dtype=torch.int32, device=dev),
+             open_thr=torch.empty((B, H, max(Kg, 1)), dtype=torch.int32, device=dev),
+             n_open=torch.empty((B, H), dtype=torch.int32, device=dev))
+    if chunk_k.stride(-1) != 1 or chunk_k.stride(2) != D or group_k.stride(3) != D or \
+            group_k.stride(2) != group_k.shape[3] * D:
+        raise ValueError("store tables must be chunk-contiguous with a contiguous head dim")
+    check(lib().hga_route_decode(
+        ctypes.byref(cfg), L, n_closed, _p(q), *_s4(q), _p(chunk_k), chunk_k.stride(0),
+        chunk_k.stride(1), _p(group_k), group_k.stride(0), group_k.stride(1), _p(r["mid"]),
+        _p(r["mid_thr"]), _p(r["n_mid"]), _p(r["open_grp"]), _p(r["open_thr"]), _p(r["n_open"]),
+        _stream()), "hga_route_decode")
+    r["Kc"], r["Kg"] = Kc, Kg
+    return r
+
+
+def attend_decode(cfg: HgaConfig, q: torch.Tensor, n_closed: int, start_pos: int,
+                  recent_k: torch.Tensor, recent_v: torch.Tensor, ring_chunks: int,
+                  first_k, first_v, record_k, record_v, record_on_host: bool,
+                  open_grp: torch.Tensor, open_thr: torch.Tensor, Kg: int,
+                  out: torch.Tensor | None = None) -> torch.Tensor:
+    """Decode attention of q [B,H,L,Dh] (rows at start_pos..start_pos+L-1).  Token sources are
+    [B,KVH,T,Dh] views: ``recent`` (positions >= the last window, optionally a ring of
+    ring_chunks chunks), ``first`` (the first window) and ``record`` (the closed-token record
+    read for opened groups; a pinned host tensor when record_on_host)."""
+    _dev(q, recent_k, recent_v, open_grp, open_thr)
+    B, H, L, D = q.shape
+    if out is None:
+        out = torch.empty((B, H, L, D), dtype=q.dtype, device=q.device)
+    if first_k is None:
+        first_k, first_v = recent_k, recent_v
+    if record_k is None:
+        record_k, record_v = recent_k, recent_v
+    if record_on_host and not record_k.is_pinned():
+        raise ValueError("a host record must be pinned memory")
+    if not record_on_host:
+        _dev(first_k, first_v, record_k, record_v)
+    for a_, b_ in ((recent_k, recent_v), (first_k, first_v), (record_k, record_v)):
+        if a_.stride() != b_.stride():
+            raise ValueError("K and V of a source must share strides")
+    og = open_grp.contiguous()
+    ot = open_thr.contiguous()
+    check(lib().hga_attend_decode(
+        ctypes.byref(cfg), L, n_closed, start_pos, _p(q), *_s4(q), _p(recent_k), _p(recent_v),
+        *_s4(recent_k), ring_chunks, _p(first_k), _p(first_v), *_s4(first_k), _p(record_k),
+        _p(record_v), *_s4(record_k), 1 if record_on_host else 0, _p(og), _p(ot), Kg, _p(out),
+        *_s4(out), _stream()), "hga_attend_decode")
+    return out

@@ -15,7 +15,8 @@ import torch
 import torch.nn as nn
 
 from . import ops
-from .router import ChunkPlacementPolicy, ChunkRouter, RouterConfig, VramKVCacheStore
+from .router import (ChunkPlacementPolicy, ChunkRouter, RamKVCacheStore, RouterConfig,
+                     VramKVCacheStore)
 
 
 class RMSNorm(nn.Module):
@@ -128,13 +129,13 @@ class HierarchicalGlobalAttentionRouted(nn.Module):
         return emb.cos(), emb.sin()
 
     def _make_store(self, B: int, dtype, device):
+        """VRAM or pinned-RAM token record (HierarchicalGlobalAttentionRouted.py:223-240)."""
         if self.cache_location not in ("vram", "ram"):
             raise ValueError(f"unknown cache_location {self.cache_location!r}")
-        return VramKVCacheStore(compute_device=device, policy=self._policy,
-                                kv_heads=self.kv_heads, head_dim=self.head_dim,
-                                chunk_size=self.chunk_size,
-                                groups_per_chunk=self._cfg.groups_per_chunk, batch_size=B,
-                                dtype=dtype)
+        cls = VramKVCacheStore if self.cache_location == "vram" else RamKVCacheStore
+        return cls(compute_device=device, policy=self._policy, kv_heads=self.kv_heads,
+                   head_dim=self.head_dim, chunk_size=self.chunk_size,
+                   groups_per_chunk=self._cfg.groups_per_chunk, batch_size=B, dtype=dtype)
 
     def _get_router(self, pkv: Any, B: int, dtype, device) -> ChunkRouter:
         holder = pkv if pkv is not None else self

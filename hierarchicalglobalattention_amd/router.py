@@ -85,25 +85,27 @@ def rotary_for_positions(theta: float, head_dim: int, start: int, length: int,
 
 
 class _LayerRecord:
-    """Closed-chunk record of one layer on the compute device: store summaries (fp32-table
-    anchors, chunk_router.py:552-598) and the RoPE'd token K / V history, capacity-doubling
-    like RamKVCacheStore._ensure_capacity (ram_kv_cache_store.py:138-157)."""
+    """Per-layer store state: closed-chunk summary tables on the compute device (store anchors,
+    fp32 table, chunk_router.py:552-598, 631-657), the token record, and the active chunk's raw
+    keys (needed for its summaries when it closes).  Capacities double like
+    RamKVCacheStore._ensure_capacity (ram_kv_cache_store.py:138-157)."""
 
     def __init__(self):
-        self.chunk_k = None   # [B, KVH, cap, Dh]
-        self.group_k = None   # [B, KVH, cap, M, Dh]
-        self.tok_k = None     # [B, KVH, cap*C, Dh]
+        self.cap = 0
+        self.chunk_k = None      # [B, KVH, cap, Dh]
+        self.group_k = None      # [B, KVH, cap, M, Dh]
+        self.tok_k = None        # record [B, KVH, cap*C, Dh]: device (VRAM) or pinned host (RAM)
         self.tok_v = None
+        self.first_k = None      # RAM tier: first window [B, KVH, kf*C, Dh] on device
+        self.first_v = None
+        self.ring_k = None       # RAM tier: last window + active chunk, ring of kl+1 chunks
+        self.ring_v = None
+        self.ring_R = 0
+        self.act_kraw = None     # [B, KVH, C, Dh] raw keys of the active chunk
         self.n_closed = 0
-        self.active_krope = None   # [B, KVH, cur, Dh] partial chunk
-        self.active_kraw = None
-        self.active_v = None
 
 
-class VramKVCacheStore:
-    """All-VRAM store (vram_kv_cache_store.py:15-50 semantics): chunk summaries and the full
-    token record stay on the compute device."""
-
+class _StoreBase:
     def __init__(self, *, compute_device, policy: ChunkPlacementPolicy, kv_heads: int,
                  head_dim: int, chunk_size: int, groups_per_chunk: int, batch_size: int,
                  dtype=torch.float32, initial_capacity: int = 64):
@@ -128,54 +130,203 @@ class VramKVCacheStore:
     def num_closed_chunks(self, layer: int) -> int:
         return self.layer(layer).n_closed
 
-    def ensure_capacity(self, layer: int, need: int) -> _LayerRecord:
-        st = self.layer(layer)
-        cur = 0 if st.chunk_k is None else st.chunk_k.shape[2]
-        if need <= cur:
-            return st
-        cap = max(self._init_cap, cur * 2, need)
-        B, KVH, D, C, M, dev, dt = self.B, self.kvh, self.dh, self.C, self.M, \
-            self.compute_device, self.dtype
-        ck = torch.zeros(B, KVH, cap, D, device=dev, dtype=dt)
-        gk = torch.zeros(B, KVH, cap, M, D, device=dev, dtype=dt)
-        tk = torch.zeros(B, KVH, cap * C, D, device=dev, dtype=dt)
-        tv = torch.zeros(B, KVH, cap * C, D, device=dev, dtype=dt)
-        if st.chunk_k is not None and st.n_closed:
-            n = st.n_closed
-            ck[:, :, :n] = st.chunk_k[:, :, :n]
-            gk[:, :, :n] = st.group_k[:, :, :n]
-            tk[:, :, :n * C] = st.tok_k[:, :, :n * C]
-            tv[:, :, :n * C] = st.tok_v[:, :, :n * C]
-        st.chunk_k, st.group_k, st.tok_k, st.tok_v = ck, gk, tk, tv
-        return st
-
     def chunk_summaries(self, layer: int):
         st = self.layer(layer)
         return None if st.n_closed == 0 else st.chunk_k[:, :, :st.n_closed]
+
+    def prepare_block(self, layer: int, first_chunk: int, last_chunk: int) -> None:
+        """Reserve room for every chunk a block touches before any of its segments is routed,
+        so routed segments keep reading the buffers they were routed against."""
+        self.ensure_capacity(layer, last_chunk + 1)
+
+    def _dev_zeros(self, *shape):
+        return torch.zeros(*shape, device=self.compute_device, dtype=self.dtype)
+
+    def ensure_capacity(self, layer: int, need: int) -> _LayerRecord:
+        """Room for `need` chunks (closed + active) in the summary tables and the record."""
+        st = self.layer(layer)
+        if need <= st.cap:
+            return st
+        cap = max(self._init_cap, st.cap * 2, need)
+        B, KVH, D, C, M = self.B, self.kvh, self.dh, self.C, self.M
+        ck, gk = self._dev_zeros(B, KVH, cap, D), self._dev_zeros(B, KVH, cap, M, D)
+        tk, tv = self._new_record(B, KVH, cap * C, D), self._new_record(B, KVH, cap * C, D)
+        if st.cap:
+            if not st.tok_k.is_cuda:   # pending async D2H copies into the old host record
+                torch.cuda.current_stream(self.compute_device).synchronize()
+            n = st.n_closed
+            ck[:, :, :n] = st.chunk_k[:, :, :n]
+            gk[:, :, :n] = st.group_k[:, :, :n]
+            keep = self._record_len(st)
+            tk[:, :, :keep].copy_(st.tok_k[:, :, :keep])
+            tv[:, :, :keep].copy_(st.tok_v[:, :, :keep])
+        st.chunk_k, st.group_k, st.tok_k, st.tok_v, st.cap = ck, gk, tk, tv, cap
+        if st.act_kraw is None:
+            st.act_kraw = self._dev_zeros(B, KVH, C, D)
+        return st
+
+
+class VramKVCacheStore(_StoreBase):
+    """All-VRAM tier (vram_kv_cache_store.py:15-50): summaries and every token, closed and
+    active, live on the compute device in one record addressed by absolute position."""
+
+    def _new_record(self, *shape):
+        return self._dev_zeros(*shape)
+
+    def _record_len(self, st):
+        return st.cap * self.C
+
+    def write_tokens(self, layer: int, pos: int, k_rope, v) -> None:
+        st = self.layer(layer)
+        L = k_rope.shape[2]
+        st.tok_k[:, :, pos:pos + L] = k_rope
+        st.tok_v[:, :, pos:pos + L] = v
+
+    def close_chunk(self, layer: int, n: int) -> None:
+        pass
+
+    def seed(self, layer: int, k_rope, v, n_closed: int) -> None:
+        st = self.layer(layer)
+        S = k_rope.shape[2]
+        st.tok_k[:, :, :S] = k_rope
+        st.tok_v[:, :, :S] = v
+
+    def sources(self, layer: int):
+        st = self.layer(layer)
+        return dict(recent_k=st.tok_k, recent_v=st.tok_v, ring_chunks=0, first_k=st.tok_k,
+                    first_v=st.tok_v, record_k=st.tok_k, record_v=st.tok_v, record_on_host=False)
+
+
+class RamKVCacheStore(_StoreBase):
+    """RAM tier (ram_kv_cache_store.py:29-619 semantics): the closed-token record lives in pinned
+    host memory; only the summary tables, the first window and a ring holding the last window
+    plus the active chunk live on the GPU.  Opened groups are read from the host record by the
+    decode attention kernel directly over PCIe (zero copy), so only routed groups cross the link.
+    The record must be pinned for that (the reference's module uses pageable memory,
+    HierarchicalGlobalAttentionRouted.py:239); ``pin_memory`` is accepted for signature
+    compatibility.  The reference's optional LRU VRAM banks (``vram_cache_chunks``,
+    ``vram_summary_chunks``) are not needed: summaries stay resident and opened groups are read
+    in place."""
+
+    def __init__(self, *, pin_memory: bool = True, num_layers: int = 0, **kw):
+        kw = {k: v for k, v in kw.items() if k in ("compute_device", "policy", "kv_heads",
+                                                     "head_dim", "chunk_size",
+                                                     "groups_per_chunk", "batch_size", "dtype",
+                                                     "initial_capacity")}
+        super().__init__(**kw)
+
+    def _new_record(self, *shape):
+        return torch.zeros(*shape, dtype=self.dtype, pin_memory=True)
+
+    def _record_len(self, st):
+        return st.n_closed * self.C
+
+    def _ring_slot(self, st, c: int) -> int:
+        return c % st.ring_R
+
+    def _ensure_hot(self, st, span: int = 1):
+        """Device first-window buffer and a ring of keep_last + span chunk slots: the last window
+        plus every chunk a block of `span` chunks writes, so that no segment of the block
+        overwrites a chunk an earlier segment still attends to.  Growing re-lays the live chunks
+        out for the new ring size."""
+        B, KVH, D, C = self.B, self.kvh, self.dh, self.C
+        R = max(self.policy.keep_last, 0) + max(span, 1)
+        if st.ring_k is not None and st.ring_R >= R:
+            return
+        rk, rv = self._dev_zeros(B, KVH, R * C, D), self._dev_zeros(B, KVH, R * C, D)
+        if st.ring_k is not None:
+            lo = self.policy.hot_last_range(st.n_closed)[0]
+            for c in range(lo, st.n_closed + 1):
+                a, b = (c % st.ring_R) * C, (c % R) * C
+                rk[:, :, b:b + C] = st.ring_k[:, :, a:a + C]
+                rv[:, :, b:b + C] = st.ring_v[:, :, a:a + C]
+        st.ring_k, st.ring_v, st.ring_R = rk, rv, R
+        kf = max(self.policy.keep_first, 0)
+        if kf and st.first_k is None:
+            st.first_k = self._dev_zeros(B, KVH, kf * C, D)
+            st.first_v = self._dev_zeros(B, KVH, kf * C, D)
+
+    def prepare_block(self, layer: int, first_chunk: int, last_chunk: int) -> None:
+        super().prepare_block(layer, first_chunk, last_chunk)
+        self._ensure_hot(self.layer(layer), last_chunk - first_chunk + 1)
+
+    def write_tokens(self, layer: int, pos: int, k_rope, v) -> None:
+        st = self.layer(layer)
+        self._ensure_hot(st)
+        C = self.C
+        s = self._ring_slot(st, pos // C) * C + pos % C
+        L = k_rope.shape[2]
+        st.ring_k[:, :, s:s + L] = k_rope
+        st.ring_v[:, :, s:s + L] = v
+
+    def close_chunk(self, layer: int, n: int) -> None:
+        """Chunk n left the active slot: copy it to the host record (async D2H into pinned
+        memory) and, inside the first window, to the device first-window buffer."""
+        st = self.layer(layer)
+        C = self.C
+        s = self._ring_slot(st, n) * C
+        st.tok_k[:, :, n * C:(n + 1) * C].copy_(st.ring_k[:, :, s:s + C], non_blocking=True)
+        st.tok_v[:, :, n * C:(n + 1) * C].copy_(st.ring_v[:, :, s:s + C], non_blocking=True)
+        if n < self.policy.keep_first:
+            st.first_k[:, :, n * C:(n + 1) * C] = st.ring_k[:, :, s:s + C]
+            st.first_v[:, :, n * C:(n + 1) * C] = st.ring_v[:, :, s:s + C]
+
+    def seed(self, layer: int, k_rope, v, n_closed: int) -> None:
+        st = self.layer(layer)
+        self._ensure_hot(st)
+        C = self.C
+        S = k_rope.shape[2]
+        e = n_closed * C
+        if e:
+            st.tok_k[:, :, :e].copy_(k_rope[:, :, :e], non_blocking=True)
+            st.tok_v[:, :, :e].copy_(v[:, :, :e], non_blocking=True)
+        kf = min(self.policy.keep_first, n_closed)
+        if kf:
+            st.first_k[:, :, :kf * C] = k_rope[:, :, :kf * C]
+            st.first_v[:, :, :kf * C] = v[:, :, :kf * C]
+        lo = self.policy.hot_last_range(n_closed)[0]
+        for c in range(lo, (S + C - 1) // C):
+            a, b = c * C, min(S, (c + 1) * C)
+            s = self._ring_slot(st, c) * C
+            st.ring_k[:, :, s:s + b - a] = k_rope[:, :, a:b]
+            st.ring_v[:, :, s:s + b - a] = v[:, :, a:b]
+
+    def sources(self, layer: int):
+        st = self.layer(layer)
+        return dict(recent_k=st.ring_k, recent_v=st.ring_v, ring_chunks=st.ring_R,
+                    first_k=st.first_k, first_v=st.first_v, record_k=st.tok_k,
+                    record_v=st.tok_v, record_on_host=True)
 
 
 class RoutedKV:
     """Routing result of one block: the index lists the attention kernel reads -- no
     materialised K/V (compare RoutedKV, chunk_router.py:93-162).  ``attend`` computes the exact
     softmax attention over real tokens (``use_summaries=False``, the only mode of the exact
-    routed path, HierarchicalGlobalAttentionRouted.py:172-174)."""
+    routed path, HierarchicalGlobalAttentionRouted.py:172-174).  ``chunked`` results come from
+    the vectorized prefill, the others from ``decode_block``."""
 
-    def __init__(self, hcfg, k_rope, v, routing: dict, scale: float, chunk_size: int):
+    def __init__(self, hcfg, routing: dict, scale: float, chunk_size: int, *, chunked: bool,
+                 k_rope=None, v=None, sources=None, n_closed: int = 0, start_pos: int = 0):
         self.hcfg = hcfg
-        self.k_rope = k_rope
-        self.v = v
         self.routing = routing
         self.scale = scale
-        self.chunked = True
+        self.chunked = chunked
         self.chunk_size = chunk_size
+        self.k_rope, self.v = k_rope, v
+        self.sources = sources
+        self.n_closed, self.start_pos = n_closed, start_pos
 
     def attend(self, q: torch.Tensor, use_summaries: bool = False) -> torch.Tensor:
         if use_summaries:
             raise NotImplementedError("summary-attending routed attention is not part of the "
                                       "exact-token path")
         r = self.routing
-        return ops.attend_prefill(self.hcfg, q, self.k_rope, self.v, r["open_grp"],
-                                  r["open_thr"], r["Kg"])
+        if self.chunked:
+            return ops.attend_prefill(self.hcfg, q, self.k_rope, self.v, r["open_grp"],
+                                      r["open_thr"], r["Kg"])
+        return ops.attend_decode(self.hcfg, q, self.n_closed, self.start_pos,
+                                 open_grp=r["open_grp"], open_thr=r["open_thr"], Kg=r["Kg"],
+                                 **self.sources)
 
 
 class ChunkRouter:
@@ -212,17 +363,76 @@ class ChunkRouter:
                           return_positions: bool = False) -> List[Tuple[RoutedKV, int, int]]:
         """Route a block of new queries (chunk_router.py:463-516): q [B,H,S,Dh] RoPE'd,
         k_rope/k_raw/v [B,KVH,S,Dh]; cos/sin the block's rotary rows in the activation dtype
-        ([1,1,S,Dh] or [S,Dh]).  Returns [(routed, lo, hi)] segments."""
+        ([1,1,S,Dh] or [S,Dh]).  Returns [(routed, lo, hi)] segments: one decode segment for a
+        block inside one chunk, one chunk-parallel segment for a fresh multi-chunk block, else
+        one decode segment per chunk."""
         if return_positions:
             raise NotImplementedError("token positions are only used by the DCA attend variant")
         C = self.cfg.chunk_size
         S = q.shape[2]
         first_chunk, last_chunk = start_pos // C, (start_pos + S - 1) // C
+        if start_pos > 0 or first_chunk == last_chunk:
+            self.store.prepare_block(layer, first_chunk, last_chunk)
         if first_chunk == last_chunk:
-            raise NotImplementedError("decode blocks are not built yet")
-        if start_pos != 0:
-            raise NotImplementedError("multi-chunk blocks over resident context are not built")
-        return [(self._prefill(layer, q, k_rope, k_raw, v, cos, sin, populate_store), 0, S)]
+            return [(self.decode_block(layer, q, k_rope, k_raw, v, start_pos), 0, S)]
+        if start_pos == 0:
+            return [(self._prefill(layer, q, k_rope, k_raw, v, cos, sin, populate_store), 0, S)]
+        segs, p, done = [], start_pos, 0
+        while done < S:
+            take = min(C - (p % C), S - done)
+            sl = slice(done, done + take)
+            segs.append((self.decode_block(layer, q[:, :, sl], k_rope[:, :, sl],
+                                           k_raw[:, :, sl], v[:, :, sl], p), done, done + take))
+            p += take
+            done += take
+        return segs
+
+    def decode_block(self, layer: int, q: torch.Tensor, k_rope: torch.Tensor,
+                     k_raw: torch.Tensor, v: torch.Tensor, start_pos: int) -> RoutedKV:
+        """Route L new tokens that all fall inside the active chunk and register them
+        (chunk_router.py:279-407); closes the chunk when its last token arrives."""
+        cfg = self.cfg
+        C = cfg.chunk_size
+        B, H, L, D = q.shape
+        n, c0 = start_pos // C, start_pos % C
+        assert c0 + L <= C, "decode_block must stay within one chunk; feed chunk-by-chunk."
+        st = self.store.layer(layer)
+        n_closed = st.n_closed
+        assert n_closed == n, f"active chunk {n} != closed {n_closed}; out-of-order block"
+        st = self.store.ensure_capacity(layer, n_closed + 1)
+        self.store.write_tokens(layer, start_pos, k_rope, v)
+        st.act_kraw[:, :, c0:c0 + L] = k_raw
+        hc = self.hcfg(B, q.dtype)
+        if n_closed > 0:
+            routing = ops.route_decode(hc, q, st.chunk_k, st.group_k, n_closed)
+        else:
+            e = torch.full((B, H, 1), -1, dtype=torch.int32, device=q.device)
+            routing = dict(mid=e, mid_thr=e, open_grp=e, open_thr=e, Kc=0, Kg=0)
+        routed = RoutedKV(hc, routing, cfg.scale, C, chunked=False,
+                          sources=self.store.sources(layer), n_closed=n_closed,
+                          start_pos=start_pos)
+        if c0 + L == C:
+            self._close_chunk(layer, n, k_rope_chunk=None)
+        return routed
+
+    def _close_chunk(self, layer: int, n: int, k_rope_chunk=None) -> None:
+        """Summaries of the full active chunk n with the fp32 anchor table, then hand it to the
+        store (ChunkRouter._close_active_chunk, chunk_router.py:631-657)."""
+        cfg = self.cfg
+        C, D = cfg.chunk_size, cfg.head_dim
+        st = self.store.layer(layer)
+        src = self.store.sources(layer)
+        if src["ring_chunks"]:
+            s = (n % src["ring_chunks"]) * C
+        else:
+            s = n * C
+        krope = src["recent_k"][:, :, s:s + C]
+        cf, sf = rotary_for_positions(cfg.theta, D, n * C, C, st.act_kraw.device)
+        hc = self.hcfg(st.act_kraw.shape[0], st.act_kraw.dtype)
+        ops.summarize(hc, st.act_kraw, krope, cf, sf, pos0=0, chunk_k=st.chunk_k[:, :, n:],
+                      group_k=st.group_k[:, :, n:])
+        self.store.close_chunk(layer, n)
+        st.n_closed = n + 1
 
     def _prefill(self, layer, q, k_rope, k_raw, v, cos, sin, populate_store) -> RoutedKV:
         cfg = self.cfg
@@ -234,38 +444,33 @@ class ChunkRouter:
             cos, sin = cos.to(dt), sin.to(dt)
         cos_r = cos.reshape(-1, D)[:S].float()
         sin_r = sin.reshape(-1, D)[:S].float()
-        n_closed = S // cfg.chunk_size
-        need_store = populate_store and n_closed > 0
-        if dt == torch.float32 or not need_store:
+        C = cfg.chunk_size
+        n_closed = S // C
+        N = (S + C - 1) // C
+        if populate_store:
+            st = self.store.layer(layer)
+            st.n_closed = 0
+            st = self.store.ensure_capacity(layer, N)
+        if dt == torch.float32 or not populate_store:
             ck, gk = ops.summarize(hc, k_raw, k_rope, cos_r, sin_r)
             ck_s, gk_s = ck, gk
         else:
+            # routing summaries with the activation-dtype table, store summaries with the fp32
+            # table written straight into the store tables (one pass over the keys)
             cf, sf = rotary_for_positions(cfg.theta, D, 0, S, dev)
-            ck, gk, ck_s, gk_s = ops.summarize(hc, k_raw, k_rope, cos_r, sin_r, cos_b=cf, sin_b=sf)
+            ck, gk = torch.empty_like(st.chunk_k[:, :, :N]), torch.empty_like(st.group_k[:, :, :N])
+            ck, gk, ck_s, gk_s = ops.summarize(hc, k_raw, k_rope, cos_r, sin_r, chunk_k=ck,
+                                               group_k=gk, cos_b=cf, sin_b=sf,
+                                               chunk_k_b=st.chunk_k[:, :, :N],
+                                               group_k_b=st.group_k[:, :, :N])
         routing = ops.route_prefill(hc, q, ck, gk, S)
         if populate_store:
-            self._seed_store(layer, k_rope, k_raw, v, ck_s, gk_s, n_closed)
-        return RoutedKV(hc, k_rope, v, routing, cfg.scale, cfg.chunk_size)
-
-    def _seed_store(self, layer, k_rope, k_raw, v, ck, gk, n_closed) -> None:
-        """Closed chunks into the record, remainder kept as the active chunk
-        (ChunkRouter._seed_store_from_block, chunk_router.py:552-598)."""
-        C = self.cfg.chunk_size
-        st = self.store.layer(layer)
-        st.n_closed = 0
-        if n_closed:
-            st = self.store.ensure_capacity(layer, n_closed)
-            e = n_closed * C
-            st.chunk_k[:, :, :n_closed] = ck[:, :, :n_closed]
-            st.group_k[:, :, :n_closed] = gk[:, :, :n_closed]
-            st.tok_k[:, :, :e] = k_rope[:, :, :e]
-            st.tok_v[:, :, :e] = v[:, :, :e]
+            if dt == torch.float32:
+                st.chunk_k[:, :, :N] = ck
+                st.group_k[:, :, :N] = gk
+            self.store.seed(layer, k_rope, v, n_closed)
+            rem = S - n_closed * C
+            if rem:
+                st.act_kraw[:, :, :rem] = k_raw[:, :, n_closed * C:]
             st.n_closed = n_closed
-        S = k_rope.shape[2]
-        rem = S - n_closed * C
-        if rem > 0:
-            st.active_krope = k_rope[:, :, n_closed * C:].contiguous()
-            st.active_kraw = k_raw[:, :, n_closed * C:].contiguous()
-            st.active_v = v[:, :, n_closed * C:].contiguous()
-        else:
-            st.active_krope = st.active_kraw = st.active_v = None
+        return RoutedKV(hc, routing, cfg.scale, C, chunked=True, k_rope=k_rope, v=v)

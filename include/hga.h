@@ -132,6 +132,55 @@ int hga_attend_prefill(const hga_config* cfg, int32_t S, const void* q, int64_t 
                        const int32_t* open_grp, const int32_t* open_thr, int32_t Kg, void* out,
                        int64_t o_sb, int64_t o_sh, int64_t o_ss, void* stream);
 
+/* Widths of the decode routing outputs with n_closed closed chunks: the routing pool is
+ * [f_hi, l_lo) of ChunkPlacementPolicy (chunk_placement_policy.py:27-38), Kc = min(topk_chunks,
+ * |pool|), Kg = min(topk_groups, Kc*C/gs)  (chunk_router.py:213-257). */
+int32_t hga_decode_widths(const hga_config* cfg, int32_t n_closed, int32_t* Kc, int32_t* Kg);
+
+/*
+ * Decode routing of an L-token block inside the active chunk (ChunkRouter._route_decision,
+ * chunk_router.py:187-277): canonical fp32 scores of every row against the closed-chunk
+ * summaries of the routing pool; chunks pooled by the max over all L rows, top-Kc selected,
+ * chunk n_closed-1 forced in when it is in the pool, each row requests its own top-Kc (first
+ * requesting row = visibility threshold, 0 for the forced chunk); all M groups of the selected
+ * chunks scored, top-Kg opened by the max over rows, each row requests its top-(topk_groups/2),
+ * a group is visible from max(first request, parent threshold).  Ties -> lower id.
+ * q: [B, H, L, Dh] view.  chunk_k element (b, kvh, c, :) at chunk_k + b*ck_sb + kvh*ck_sh +
+ * c*Dh; group_k element (b, kvh, c, m, :) at group_k + b*gk_sb + kvh*gk_sh + (c*M+m)*Dh.
+ * Outputs (int32, ascending ids, -1 padded, widths from hga_decode_widths, >= 1):
+ *   mid, mid_thr [B, H, Kc]  routed chunks visible to some row; n_mid [B, H]
+ *   open_grp, open_thr [B, H, Kg]  opened groups (chunk*M + group) visible to some row; n_open
+ */
+int hga_route_decode(const hga_config* cfg, int32_t L, int32_t n_closed, const void* q,
+                     int64_t q_sb, int64_t q_sh, int64_t q_ss, const void* chunk_k,
+                     int64_t ck_sb, int64_t ck_sh, const void* group_k, int64_t gk_sb,
+                     int64_t gk_sh, int32_t* mid, int32_t* mid_thr, int32_t* n_mid,
+                     int32_t* open_grp, int32_t* open_thr, int32_t* n_open, void* stream);
+
+/*
+ * Decode attention (decode_block's assembly, chunk_router.py:333-401, attended flat as in
+ * RoutedKV.attend, :159-162).  Row l sits at absolute position start_pos + l in active chunk
+ * n_closed and attends to the first window [0, f_hi*C), the last window [l_lo*C, n_closed*C),
+ * every opened group with open_thr <= l, and active tokens [n_closed*C, start_pos + l].
+ * Token sources (K and V share strides; element strides b, kv head, position):
+ *   recent  positions >= l_lo*C (last window + active chunk); position p at slot p when
+ *           ring_chunks == 0, else at slot (p/C % ring_chunks)*C + p%C;
+ *   first   positions [0, f_hi*C) at slot p;
+ *   record  the whole closed-token record at slot p, read for opened groups; device memory, or
+ *           pinned host memory (hipHostMalloc / torch pin_memory) when record_on_host != 0 --
+ *           the kernel then reads the opened groups across PCIe directly (zero copy).
+ * q/out: [B, H, L, Dh] views.
+ */
+int hga_attend_decode(const hga_config* cfg, int32_t L, int32_t n_closed, int64_t start_pos,
+                      const void* q, int64_t q_sb, int64_t q_sh, int64_t q_ss,
+                      const void* k_recent, const void* v_recent, int64_t r_sb, int64_t r_sh,
+                      int64_t r_ss, int32_t ring_chunks, const void* k_first,
+                      const void* v_first, int64_t f_sb, int64_t f_sh, int64_t f_ss,
+                      const void* k_record, const void* v_record, int64_t d_sb, int64_t d_sh,
+                      int64_t d_ss, int32_t record_on_host, const int32_t* open_grp,
+                      const int32_t* open_thr, int32_t Kg, void* out, int64_t o_sb,
+                      int64_t o_sh, int64_t o_ss, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -143,6 +143,37 @@ class OracleModule:
         return oracle.summarize(k_raw, k_rope, cos.numpy(), sin.numpy(), self.C, self.gs, cut,
                                 oracle.group_scale(self.gs), oracle.DT_F32, pos0=pos0)
 
+    def _decode_segment(self, q, k_rope, k_raw, v, start_pos, cos_f, sin_f):
+        """Rows inside one chunk: route against the closed chunks, attend, then close the chunk
+        when it is full (chunk_router.py:279-407, 631-657)."""
+        B, H = q.shape[:2]
+        C = self.C
+        kf, kl = self.m["keep_first"], self.m["keep_last"]
+        tc, tg = self.m["topk_chunks"], self.m["topk_groups"]
+        scale = oracle.attn_scale(self.Dh)
+        cat = (lambda a, b: b) if self.k_hist is None else (
+            lambda a, b: np.concatenate([a, b], axis=2))
+        self.k_hist = cat(self.k_hist, k_rope)
+        self.kraw_hist = cat(self.kraw_hist, k_raw)
+        self.v_hist = cat(self.v_hist, v)
+        r = None
+        if self.n_closed > 0:
+            r = oracle.route_decode(q, self.ck, self.gk, self.n_closed, kf, kl, tc, tg, scale)
+            self.decisions.append((self.n_closed, r))
+        og = r["open_grp"] if r is not None else np.full((B, H, 1), -1, np.int32)
+        ot = r["open_thr"] if r is not None else np.full((B, H, 1), -1, np.int32)
+        out = oracle.attend_decode(q, self.k_hist, self.v_hist, C, self.gs, kf, kl,
+                                   self.n_closed, start_pos, og, ot, scale, oracle.DT_F32)
+        T = self.k_hist.shape[2]
+        if T == (self.n_closed + 1) * C:       # the segment filled the active chunk
+            lo = self.n_closed * C
+            ck, gk = self._close_summaries(self.k_hist[:, :, lo:], self.kraw_hist[:, :, lo:],
+                                           lo, cos_f, sin_f)
+            self.ck = ck if self.ck is None else np.concatenate([self.ck, ck], axis=2)
+            self.gk = gk if self.gk is None else np.concatenate([self.gk, gk], axis=2)
+            self.n_closed += 1
+        return out
+
     def forward(self, x, start_pos):
         B, S, _ = x.shape
         H, KVH, Dh, C = self.H, self.KVH, self.Dh, self.C
@@ -157,12 +188,10 @@ class OracleModule:
         v = v.contiguous().numpy()
         kf, kl = self.m["keep_first"], self.m["keep_last"]
         tc, tg = self.m["topk_chunks"], self.m["topk_groups"]
-        scale = oracle.attn_scale(Dh)
         if start_pos == 0:
             self.reset()
         first_chunk, last_chunk = start_pos // C, (start_pos + S - 1) // C
-        if first_chunk != last_chunk:
-            assert start_pos == 0, "multi-chunk blocks over resident context not modelled"
+        if first_chunk != last_chunk and start_pos == 0:
             out, r, _, _ = oracle.prefill(q, k_rope, k_raw, v, cos.numpy(), sin.numpy(), C=C,
                                           gs=self.gs, keep_first=kf, keep_last=kl,
                                           topk_chunks=tc, topk_groups=tg, theta=self.theta,
@@ -174,26 +203,16 @@ class OracleModule:
                 self.ck, self.gk = self._close_summaries(k_rope[:, :, :e], k_raw[:, :, :e], 0,
                                                          cos_f, sin_f)
         else:
-            cat = (lambda a, b: b) if self.k_hist is None else (
-                lambda a, b: np.concatenate([a, b], axis=2))
-            self.k_hist = cat(self.k_hist, k_rope)
-            self.kraw_hist = cat(self.kraw_hist, k_raw)
-            self.v_hist = cat(self.v_hist, v)
-            r = None
-            if self.n_closed > 0:
-                r = oracle.route_decode(q, self.ck, self.gk, self.n_closed, kf, kl, tc, tg, scale)
-                self.decisions.append((self.n_closed, r))
-            og = r["open_grp"] if r is not None else np.full((B, H, 1), -1, np.int32)
-            ot = r["open_thr"] if r is not None else np.full((B, H, 1), -1, np.int32)
-            out = oracle.attend_decode(q, self.k_hist, self.v_hist, C, self.gs, kf, kl,
-                                       self.n_closed, start_pos, og, ot, scale, oracle.DT_F32)
-            T = self.k_hist.shape[2]
-            if T == (self.n_closed + 1) * C:       # the block filled the active chunk
-                lo = self.n_closed * C
-                ck, gk = self._close_summaries(self.k_hist[:, :, lo:], self.kraw_hist[:, :, lo:],
-                                               lo, cos_f, sin_f)
-                self.ck = ck if self.ck is None else np.concatenate([self.ck, ck], axis=2)
-                self.gk = gk if self.gk is None else np.concatenate([self.gk, gk], axis=2)
-                self.n_closed += 1
+            # one decode segment per chunk the block touches (chunk_router.py:493-516)
+            out = np.empty_like(q)
+            p, done = start_pos, 0
+            while done < S:
+                take = min(C - (p % C), S - done)
+                sl = slice(done, done + take)
+                out[:, :, sl] = self._decode_segment(q[:, :, sl], k_rope[:, :, sl],
+                                                     k_raw[:, :, sl], v[:, :, sl], p, cos_f,
+                                                     sin_f)
+                p += take
+                done += take
         o = torch.from_numpy(out).transpose(1, 2).reshape(B, S, H * Dh)
         return self._lin(o, "o_proj")

@@ -1,0 +1,299 @@
+"""GPU parity of the decode path: routing of blocks inside the active chunk, the decode attention
+over [first window | last window | opened groups | active chunk], the VRAM and pinned-RAM
+stores, and whole-module decode against the reference module's recorded outputs.
+
+Routing indices are compared bit-exactly with the oracle (fp32 canonical scores, ties to the
+lower id); attention outputs within 1e-4 (fp32) or 2e-2 max / 1e-2 mean abs (bf16)."""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from helpers import OracleModule, load_case
+
+pytestmark = pytest.mark.gpu
+
+hga = pytest.importorskip("hierarchicalglobalattention_amd")
+from hierarchicalglobalattention_amd import ops  # noqa: E402
+from hierarchicalglobalattention_amd import router as hrouter  # noqa: E402
+
+DEV = "cuda"
+BF16_MAX, BF16_MEAN, F32_TOL = 2e-2, 1e-2, 1e-4
+
+
+def _pad(a, w):
+    a = np.asarray(a)
+    return np.concatenate([a, np.full(a.shape[:-1] + (w - a.shape[-1],), -1, np.int32)], -1)
+
+
+def _same_lists(a, b):
+    w = max(a.shape[-1], b.shape[-1])
+    np.testing.assert_array_equal(_pad(a, w), _pad(b, w))
+
+
+# ----------------------------------------------------------------------------------------------
+# whole module against the reference module's recorded decode runs
+# ----------------------------------------------------------------------------------------------
+def _module(meta, g, cache_location=None):
+    m = hga.HierarchicalGlobalAttentionRouted(
+        d_model=meta["d_model"], nhead=meta["H"], kv_heads=meta["KVH"], head_dim=meta["Dh"],
+        chunk_size=meta["C"], group_size=meta["gs"], topk_chunks=meta["topk_chunks"],
+        topk_groups=meta["topk_groups"], keep_first=meta["keep_first"],
+        keep_last=meta["keep_last"], theta=meta["theta"], qk_norm=meta.get("qk_norm", False),
+        cache_location=cache_location or meta.get("cache_location", "vram"))
+    sd = {k[2:]: torch.from_numpy(v) for k, v in g.items() if k.startswith("w_")}
+    m.load_state_dict(sd, strict=True)
+    return m.to(DEV).eval()
+
+
+class _Cache:
+    pass
+
+
+def _run_module(m, x, S, gen, block=1):
+    """Prefill S tokens, then feed the rest in blocks of `block` tokens."""
+    cache = _Cache()
+    outs = []
+    with torch.no_grad():
+        o, _ = m(hidden_states=x[:, :S], past_key_value=cache,
+                 cache_position=torch.arange(S, device=DEV))
+        outs.append(o)
+        p = S
+        while p < S + gen:
+            e = min(S + gen, p + block)
+            o, _ = m(hidden_states=x[:, p:e], past_key_value=cache,
+                     cache_position=torch.arange(p, e, device=DEV))
+            outs.append(o)
+            p = e
+    torch.cuda.synchronize()
+    return torch.cat(outs, 1).cpu().numpy()
+
+
+@pytest.mark.parametrize("name", ["mod_decode", "mod_decode_prev", "mod_decode_ram"])
+def test_module_decode_matches_reference(name, monkeypatch):
+    meta, g = load_case(name)
+    print(f"[decode] module {name}", flush=True)
+    seen = []
+    real = ops.route_decode
+
+    def spy(cfg, q, ck, gk, n_closed):
+        r = real(cfg, q, ck, gk, n_closed)
+        seen.append((n_closed, r["mid"].cpu().numpy(), r["open_grp"].cpu().numpy()))
+        return r
+
+    monkeypatch.setattr(hrouter.ops, "route_decode", spy)
+    m = _module(meta, g)
+    x = torch.from_numpy(g["x"]).to(DEV)
+    out = _run_module(m, x, meta["S"], meta["gen"])
+    np.testing.assert_allclose(out, g["out"], atol=F32_TOL, rtol=0)
+    assert len(seen) == meta["gen"]
+    for i, (ncl, mid, og) in enumerate(seen):
+        assert ncl == g["dec_n_closed"][i]
+        _same_lists(mid, g["dec_sel"][i])
+        _same_lists(og, g["dec_open"][i])
+
+
+def test_module_ram_store_equals_vram_store():
+    meta, g = load_case("mod_decode")
+    x = torch.from_numpy(g["x"]).to(DEV)
+    a = _run_module(_module(meta, g, "vram"), x, meta["S"], meta["gen"])
+    b = _run_module(_module(meta, g, "ram"), x, meta["S"], meta["gen"])
+    np.testing.assert_array_equal(a, b)
+
+
+@pytest.mark.parametrize("loc", ["vram", "ram"])
+@pytest.mark.parametrize("block", [3, 11])
+def test_module_multi_token_blocks_vs_oracle(loc, block):
+    """Blocks of several tokens over resident context -- inside one chunk, and crossing chunk
+    boundaries (one decode segment per chunk, chunk_router.py:493-516) -- against the oracle
+    module fed the same blocks; routing decisions compared bit-exactly."""
+    meta, g = load_case("mod_decode_ram")
+    print(f"[decode] multi-token blocks loc={loc} block={block}", flush=True)
+    seen = []
+    real = ops.route_decode
+
+    def spy(cfg, q, ck, gk, n_closed):
+        r = real(cfg, q, ck, gk, n_closed)
+        seen.append((n_closed, r["mid"].cpu().numpy(), r["open_grp"].cpu().numpy()))
+        return r
+
+    x = torch.from_numpy(g["x"])
+    S, gen = meta["S"], meta["gen"]
+    om = OracleModule(meta, g)
+    ref = [om.forward(x[:, :S], 0)]
+    p = S
+    while p < S + gen:
+        e = min(S + gen, p + block)
+        ref.append(om.forward(x[:, p:e], p))
+        p = e
+    ref = torch.cat(ref, 1).numpy()
+    orig = hrouter.ops.route_decode
+    hrouter.ops.route_decode = spy
+    try:
+        out = _run_module(_module(meta, g, loc), x.to(DEV), S, gen, block=block)
+    finally:
+        hrouter.ops.route_decode = orig
+    np.testing.assert_allclose(out, ref, atol=F32_TOL, rtol=0)
+    assert len(seen) == len(om.decisions)
+    for (ncl, mid, og), (oncl, r) in zip(seen, om.decisions):
+        assert ncl == oncl
+        _same_lists(mid, r["mid"])
+        _same_lists(og, r["open_grp"])
+
+
+# ----------------------------------------------------------------------------------------------
+# ops level: routing and attention against the oracle at c4-like shapes
+# ----------------------------------------------------------------------------------------------
+def _cfg(B, H, KVH, Dh, C, gs, tc, tg, kf, kl, dtype):
+    return ops.make_config(batch=B, heads=H, kv_heads=KVH, head_dim=Dh, chunk_size=C,
+                           group_size=gs, topk_chunks=tc, topk_groups=tg, keep_first=kf,
+                           keep_last=kl, cutoff_pair=ops.mixed_cutoff_pair(1e6, C, Dh),
+                           dtype=dtype)
+
+
+def _summaries(gen, B, KVH, cap, M, Dh, dtype, dup=False):
+    ck = torch.randn(B, KVH, cap, Dh, generator=gen)
+    gk = torch.randn(B, KVH, cap, M, Dh, generator=gen)
+    if dup:   # exact score ties: every 3rd chunk/group repeats its predecessor
+        ck[:, :, 3::3] = ck[:, :, 2:-1:3][:, :, :ck[:, :, 3::3].shape[2]]
+        gk[:, :, :, 1::2] = gk[:, :, :, 0::2][:, :, :, :gk[:, :, :, 1::2].shape[3]]
+    return ck.to(dtype), gk.to(dtype)
+
+
+ROUTE_CASES = [
+    # B, H, KVH, Dh, C, gs, tc, tg, kf, kl, n_closed, L, dtype
+    (2, 8, 2, 128, 64, 16, 16, 64, 2, 8, 40, 1, torch.bfloat16),
+    (2, 8, 2, 128, 64, 16, 16, 64, 2, 8, 40, 7, torch.bfloat16),
+    (1, 8, 2, 128, 64, 16, 16, 64, 2, 8, 511, 1, torch.bfloat16),     # 32K context
+    (1, 4, 1, 128, 64, 16, 16, 64, 2, 8, 2047, 1, torch.bfloat16),    # 128K context
+    (1, 4, 2, 128, 64, 16, 16, 64, 2, 8, 300, 5, torch.float32),
+    (2, 4, 2, 64, 32, 8, 5, 9, 1, 3, 17, 3, torch.float32),
+    (1, 4, 2, 64, 64, 16, 4, 64, 0, 0, 9, 2, torch.float32),          # tg > Kc*M, no windows
+    (1, 4, 2, 128, 64, 16, 16, 64, 2, 8, 12, 1, torch.bfloat16),      # pool smaller than tc
+    (1, 4, 2, 128, 64, 16, 16, 64, 2, 8, 6, 1, torch.bfloat16),       # everything in windows
+]
+
+
+@pytest.mark.parametrize("case", ROUTE_CASES, ids=lambda c: f"B{c[0]}H{c[1]}n{c[10]}L{c[11]}"
+                         f"{'bf16' if c[12] is torch.bfloat16 else 'f32'}")
+def test_route_decode_vs_oracle(case):
+    B, H, KVH, Dh, C, gs, tc, tg, kf, kl, n_closed, L, dt = case
+    print(f"[decode] route {case}", flush=True)
+    M = C // gs
+    gen = torch.Generator().manual_seed(n_closed * 31 + L)
+    cap = n_closed + 3
+    ck, gk = _summaries(gen, B, KVH, cap, M, Dh, dt)
+    q = torch.randn(B, H, L, Dh, generator=gen).to(dt)
+    cfg = _cfg(B, H, KVH, Dh, C, gs, tc, tg, kf, kl, dt)
+    r = ops.route_decode(cfg, q.to(DEV), ck.to(DEV), gk.to(DEV), n_closed)
+    torch.cuda.synchronize()
+    o = oracle.route_decode(q.float().numpy(), ck.float().numpy(), gk.float().numpy(), n_closed,
+                            kf, kl, tc, tg, oracle.attn_scale(Dh))
+    for key in ("mid", "mid_thr", "open_grp", "open_thr"):
+        _same_lists(r[key].cpu().numpy(), o[key])
+    np.testing.assert_array_equal(r["n_mid"].cpu().numpy(), o["n_mid"])
+    np.testing.assert_array_equal(r["n_open"].cpu().numpy(), o["n_open"])
+
+
+@pytest.mark.parametrize("L", [1, 4])
+def test_route_decode_exact_ties(L):
+    B, H, KVH, Dh, C, gs, tc, tg, kf, kl, n_closed = 1, 8, 2, 128, 64, 16, 8, 16, 1, 2, 60
+    M = C // gs
+    gen = torch.Generator().manual_seed(77 + L)
+    ck, gk = _summaries(gen, B, KVH, n_closed, M, Dh, torch.bfloat16, dup=True)
+    q = torch.randn(B, H, L, Dh, generator=gen).to(torch.bfloat16)
+    cfg = _cfg(B, H, KVH, Dh, C, gs, tc, tg, kf, kl, torch.bfloat16)
+    r = ops.route_decode(cfg, q.to(DEV), ck.to(DEV), gk.to(DEV), n_closed)
+    o = oracle.route_decode(q.float().numpy(), ck.float().numpy(), gk.float().numpy(), n_closed,
+                            kf, kl, tc, tg, oracle.attn_scale(Dh))
+    for key in ("mid", "mid_thr", "open_grp", "open_thr"):
+        _same_lists(r[key].cpu().numpy(), o[key])
+
+
+def _history(gen, B, KVH, T, Dh, dt):
+    k = (torch.randn(B, KVH, T, Dh, generator=gen) * 0.5).to(dt)
+    v = torch.randn(B, KVH, T, Dh, generator=gen).to(dt)
+    return k, v
+
+
+ATTN_CASES = [
+    # B, H, KVH, Dh, C, gs, tc, tg, kf, kl, n_closed, c0, L, dtype
+    (2, 8, 2, 128, 64, 16, 16, 64, 2, 8, 40, 0, 1, torch.bfloat16),
+    (2, 8, 2, 128, 64, 16, 16, 64, 2, 8, 40, 37, 7, torch.bfloat16),
+    (1, 8, 2, 128, 64, 16, 16, 64, 2, 8, 511, 63, 1, torch.bfloat16),
+    (1, 4, 2, 128, 64, 16, 16, 64, 2, 8, 300, 10, 5, torch.float32),
+    (2, 4, 2, 64, 32, 8, 5, 9, 1, 3, 17, 30, 2, torch.float32),
+    (1, 4, 2, 64, 64, 16, 4, 64, 0, 0, 9, 0, 2, torch.float32),
+    (1, 4, 2, 32, 16, 4, 3, 5, 1, 1, 0, 5, 3, torch.float32),         # nothing closed yet
+]
+
+
+def _ring(k, n_closed, C, kf, kl, R):
+    """Ring of R chunk slots holding chunks [l_lo, n_closed] at slot c % R (other slots hold
+    garbage that must never be read)."""
+    B, KVH, T, Dh = k.shape
+    ring = torch.full((B, KVH, R * C, Dh), float("nan"), dtype=k.dtype)
+    l_lo = oracle.windows(n_closed, kf, kl)[1]
+    for c in range(l_lo, n_closed + 1):
+        a = c * C
+        e = min(T, a + C)
+        ring[:, :, (c % R) * C:(c % R) * C + e - a] = k[:, :, a:e]
+    return ring
+
+
+@pytest.mark.parametrize("case", ATTN_CASES, ids=lambda c: f"B{c[0]}n{c[10]}c{c[11]}L{c[12]}"
+                         f"{'bf16' if c[13] is torch.bfloat16 else 'f32'}")
+@pytest.mark.parametrize("tier", ["vram", "ram"])
+def test_attend_decode_vs_oracle(case, tier):
+    B, H, KVH, Dh, C, gs, tc, tg, kf, kl, n_closed, c0, L, dt = case
+    print(f"[decode] attend {tier} {case}", flush=True)
+    M = C // gs
+    gen = torch.Generator().manual_seed(n_closed * 7 + c0)
+    start = n_closed * C + c0
+    T = start + L
+    k, v = _history(gen, B, KVH, T, Dh, dt)
+    q = torch.randn(B, H, L, Dh, generator=gen).to(dt)
+    cfg = _cfg(B, H, KVH, Dh, C, gs, tc, tg, kf, kl, dt)
+    if n_closed:
+        ck, gk = _summaries(gen, B, KVH, n_closed, M, Dh, dt)
+        r = ops.route_decode(cfg, q.to(DEV), ck.to(DEV), gk.to(DEV), n_closed)
+        og, ot, Kg = r["open_grp"], r["open_thr"], r["Kg"]
+    else:
+        og = ot = torch.full((B, H, 1), -1, dtype=torch.int32, device=DEV)
+        Kg = 0
+    if tier == "vram":
+        kd, vd = k.to(DEV), v.to(DEV)
+        out = ops.attend_decode(cfg, q.to(DEV), n_closed, start, kd, vd, 0, kd, vd, kd, vd,
+                                False, og, ot, Kg)
+    else:
+        R = kl + 1 + 2     # wider than needed: slot = chunk % R must be honoured
+        rk, rv = _ring(k, n_closed, C, kf, kl, R), _ring(v, n_closed, C, kf, kl, R)
+        fk = k[:, :, :max(kf, 1) * C].contiguous()
+        fv = v[:, :, :max(kf, 1) * C].contiguous()
+        hk = torch.zeros(B, KVH, (n_closed + 1) * C, Dh, dtype=dt, pin_memory=True)
+        hv = torch.zeros_like(hk).pin_memory()
+        hk[:, :, :n_closed * C] = k[:, :, :n_closed * C]
+        hv[:, :, :n_closed * C] = v[:, :, :n_closed * C]
+        out = ops.attend_decode(cfg, q.to(DEV), n_closed, start, rk.to(DEV), rv.to(DEV), R,
+                                fk.to(DEV), fv.to(DEV), hk, hv, True, og, ot, Kg)
+    torch.cuda.synchronize()
+    ref = oracle.attend_decode(q.float().numpy(), k.float().numpy(), v.float().numpy(), C, gs,
+                               kf, kl, n_closed, start, og.cpu().numpy(), ot.cpu().numpy(),
+                               oracle.attn_scale(Dh),
+                               oracle.DT_BF16 if dt is torch.bfloat16 else oracle.DT_F32)
+    d = np.abs(out.float().cpu().numpy() - ref)
+    if dt is torch.bfloat16:
+        assert d.max() <= BF16_MAX and d.mean() <= BF16_MEAN, (d.max(), d.mean())
+    else:
+        assert d.max() <= F32_TOL, d.max()
+
+
+def test_attend_decode_rejects_bad_blocks():
+    cfg = _cfg(1, 4, 2, 64, 64, 16, 4, 8, 1, 1, torch.float32)
+    q = torch.zeros(1, 4, 2, 64, device=DEV)
+    kv = torch.zeros(1, 2, 256, 64, device=DEV)
+    e = torch.full((1, 4, 1), -1, dtype=torch.int32, device=DEV)
+    with pytest.raises(hga.HgaError, match="not inside active chunk"):
+        ops.attend_decode(cfg, q, 1, 64 + 63, kv, kv, 0, kv, kv, kv, kv, False, e, e, 0)
+    with pytest.raises(hga.HgaError, match="ring"):
+        ops.attend_decode(cfg, q, 3, 3 * 64, kv, kv, 1, kv, kv, kv, kv, False, e, e, 0)
