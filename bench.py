@@ -131,6 +131,113 @@ def run_gpu(args):
                 tokens=tokens, route_bytes=route_bytes)
 
 
+DEC_CFG = dict(H=32, KVH=4, Dh=128, C=64, gs=16, kf=2, kl=8, theta=1e6)
+
+
+def _rms(x):
+    return x * torch.rsqrt(x.pow(2).mean(-1, keepdim=True) + 1e-6)
+
+
+def run_decode(*, ctx, B, tc, tg, tier, steps, warmup, needles=False, seed=0):
+    """Decode of `steps + warmup` one-token steps per sequence after a seeded c3-style context of
+    `ctx` tokens.  A step is one decode_block (token write, decode routing, chunk close when the
+    active chunk fills) plus the routed attention over its working set, for all B sequences.
+    tier "ram": the closed-token record is pinned host memory (the GPU keeps summaries, the
+    first window and a ring of last-window chunks); "vram": everything in HBM.  needles: KV heads
+    0-1 of every sequence get 4 chunks of keys scaled x8 at seeded random chunk ids."""
+    from hierarchicalglobalattention_amd import ops
+    from hierarchicalglobalattention_amd.router import (ChunkPlacementPolicy, ChunkRouter,
+                                                        RamKVCacheStore, RouterConfig,
+                                                        VramKVCacheStore, rotary_for_positions)
+    c = DEC_CFG
+    dev = torch.device("cuda:0")
+    H, KVH, Dh, C = c["H"], c["KVH"], c["Dh"], c["C"]
+    T = ctx + warmup + steps
+    g = torch.Generator(device=dev).manual_seed(seed)
+    k_raw = _rms(torch.randn(B, KVH, T, Dh, device=dev, generator=g)).to(torch.bfloat16)
+    if needles:
+        gc = torch.Generator().manual_seed(seed + 1)
+        for b in range(B):
+            for kvh in range(min(2, KVH)):
+                for n in torch.randperm(ctx // C, generator=gc)[:4].tolist():
+                    k_raw[b, kvh, n * C:(n + 1) * C] *= 8
+    v = torch.randn(B, KVH, T, Dh, device=dev, generator=g).to(torch.bfloat16)
+    q_raw = _rms(torch.randn(B, H, warmup + steps, Dh, device=dev, generator=g)).to(torch.bfloat16)
+    rcfg = RouterConfig(nhead=H, kv_heads=KVH, head_dim=Dh, chunk_size=C, group_size=c["gs"],
+                        topk_chunks=tc, topk_groups=tg, theta=c["theta"])
+    pol = ChunkPlacementPolicy(keep_first=c["kf"], keep_last=c["kl"], first_token_level=True)
+    cls = RamKVCacheStore if tier == "ram" else VramKVCacheStore
+    store = cls(compute_device=dev, policy=pol, kv_heads=KVH, head_dim=Dh, chunk_size=C,
+                groups_per_chunk=C // c["gs"], batch_size=B, dtype=torch.bfloat16,
+                initial_capacity=(T + C - 1) // C + 1)
+    router = ChunkRouter(rcfg, store)
+    hc = router.hcfg(B, torch.bfloat16)
+    cos, sin = rotary_for_positions(c["theta"], Dh, 0, T, dev)
+    k_rope = ops.rope(hc, k_raw, cos, sin)
+    q = ops.rope(hc, q_raw, cos[ctx:], sin[ctx:])
+    router.seed_store_from_block(0, k_rope[:, :, :ctx], k_raw[:, :, :ctx], v[:, :, :ctx])
+    torch.cuda.synchronize()
+    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(steps)]
+    stats = dict(open_groups=0, open_groups_union=0, samples=0)
+
+    def step(i, timed):
+        p = ctx + i
+        sl = slice(p, p + 1)
+        qi = q[:, :, i:i + 1]
+        if timed is not None:
+            timed[0].record()
+        routed = router.decode_block(0, qi, k_rope[:, :, sl], k_raw[:, :, sl], v[:, :, sl], p)
+        if timed is not None:
+            timed[1].record()
+        out = routed.attend(qi)
+        if timed is not None:
+            timed[2].record()
+        return routed, out
+
+    for i in range(warmup):
+        step(i, None)
+    torch.cuda.synchronize()
+    # pass 1: per-stage events; sampled routing statistics
+    for j in range(steps):
+        routed, out = step(warmup + j, ev[j])
+        if j % max(1, steps // 8) == 0 and routed.routing["Kg"] > 0:
+            og = routed.routing["open_grp"]
+            n_open = int((og >= 0).sum().item())
+            u = 0
+            rep = H // KVH
+            for kvh in range(KVH):
+                grp = og[:, kvh * rep:(kvh + 1) * rep].reshape(B, -1)
+                for b in range(B):
+                    x = grp[b][grp[b] >= 0]
+                    u += int(torch.unique(x).numel())
+            stats["open_groups"] += n_open
+            stats["open_groups_union"] += u
+            stats["samples"] += 1
+    torch.cuda.synchronize()
+    assert torch.isfinite(out.float()).all()
+    route_ms = sum(e[0].elapsed_time(e[1]) for e in ev) / steps
+    attn_ms = sum(e[1].elapsed_time(e[2]) for e in ev) / steps
+    # pass 2: clean wall-clock loop over fresh tokens would change the context; re-seed instead
+    router.seed_store_from_block(0, k_rope[:, :, :ctx], k_raw[:, :, :ctx], v[:, :, :ctx])
+    for i in range(warmup):
+        step(i, None)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for j in range(steps):
+        step(warmup + j, None)
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) * 1e3 / steps
+    ns = max(stats["samples"], 1)
+    grp_bytes = c["gs"] * Dh * 2 * 2          # K and V of one 16-token group, bf16
+    rd = stats["open_groups"] / ns * grp_bytes
+    return dict(ctx=ctx, batch=B, topk_chunks=tc, topk_groups=tg, tier=tier, steps=steps,
+                ms_per_step=ms, us_per_step_layer=ms * 1e3, tokens_per_s=B / (ms * 1e-3),
+                device_ms=dict(decode_block=route_ms, attention=attn_ms),
+                opened_group_bytes_per_step=rd,
+                opened_group_bytes_per_step_dedup=stats["open_groups_union"] / ns * grp_bytes,
+                h2d_gbs=(rd / (attn_ms * 1e-3) / 1e9) if tier == "ram" else None)
+
+
 def cpu_baseline(budget_s: float):
     """The op-faithful torch CPU mirror of the reference path, on a bounded query-chunk slab of
     the same workload, scaled to tokens/s."""
@@ -149,12 +256,26 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-budget", type=float, default=15.0)
+    ap.add_argument("--no-decode", action="store_true", help="skip the decode legs (c4, c5)")
+    ap.add_argument("--decode-steps", type=int, default=256)
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py: this build targets a single MI355X; multi-GPU runs are out of scope "
               "(see DESIGN.md for how the path would shard)", file=sys.stderr)
         sys.exit(2)
     g = run_gpu(args)
+    dec = None
+    if not args.no_decode:
+        ds = args.decode_steps
+        dec = {
+            "c4_32k_ram": run_decode(ctx=32768, B=1, tc=16, tg=64, tier="ram", steps=ds,
+                                     warmup=8),
+            "c4_128k_ram": run_decode(ctx=131072, B=1, tc=16, tg=64, tier="ram", steps=ds,
+                                      warmup=8),
+            "c5_b64_64k_vram": run_decode(ctx=65536, B=64, tc=32, tg=128, tier="vram",
+                                          steps=max(ds // 8, 4), warmup=4, needles=True),
+        }
+        torch.cuda.empty_cache()
     cpu = None
     if not args.no_cpu:
         cpu = cpu_baseline(args.cpu_budget)
@@ -184,6 +305,7 @@ def main():
                      "unit": "TFLOP/s", "frac": g["attn_tflops"] / MFMA_BF16_PEAK_TFLOPS,
                      "traffic": None,
                      "algorithmic_flops": g["flops"], "visible_qk_pairs": g["pairs"]},
+        "decode": dec,
         "cpu_baseline": cpu,
         "host": {"cpu": platform.processor() or platform.machine(), "torch": torch.__version__},
     }

@@ -434,6 +434,31 @@ class ChunkRouter:
         self.store.close_chunk(layer, n)
         st.n_closed = n + 1
 
+    @torch.no_grad()
+    def _seed_store_from_block(self, layer: int, k_rope: torch.Tensor, k_raw: torch.Tensor,
+                               v: torch.Tensor) -> None:
+        """Populate the store from a block at position 0 without routing it
+        (chunk_router.py:552-598): store summaries of the closed chunks with the fp32 anchor
+        table, the token record, and the partial remainder as the active chunk."""
+        cfg = self.cfg
+        B, KVH, S, D = k_rope.shape
+        C = cfg.chunk_size
+        n_closed, N = S // C, (S + C - 1) // C
+        st = self.store.layer(layer)
+        st.n_closed = 0
+        st = self.store.ensure_capacity(layer, N)
+        if n_closed:
+            e = n_closed * C
+            cf, sf = rotary_for_positions(cfg.theta, D, 0, e, k_rope.device)
+            ops.summarize(self.hcfg(B, k_rope.dtype), k_raw[:, :, :e], k_rope[:, :, :e], cf, sf,
+                          chunk_k=st.chunk_k, group_k=st.group_k)
+        self.store.seed(layer, k_rope, v, n_closed)
+        if S > n_closed * C:
+            st.act_kraw[:, :, :S - n_closed * C] = k_raw[:, :, n_closed * C:]
+        st.n_closed = n_closed
+
+    seed_store_from_block = _seed_store_from_block
+
     def _prefill(self, layer, q, k_rope, k_raw, v, cos, sin, populate_store) -> RoutedKV:
         cfg = self.cfg
         B, H, S, D = q.shape
