@@ -349,15 +349,327 @@ __global__ __launch_bounds__(kVT) void attend_valu_kernel(AttnArgs A) {
     }
 }
 
+// ------------------------------------------------------------------------------------------
+// bf16 MFMA kernel v2 (group_size and chunk_size multiples of 16): no LDS operands, no barriers
+// ------------------------------------------------------------------------------------------
+// The key sequence is a list of 16-key blocks (a window or own-chunk block of 16 consecutive
+// tokens, or 16 tokens of an opened group).  One 64-lane wave owns all rows of a
+// (batch, head, chunk): S^T = K Q^T with K operands loaded straight from memory (lane = key, 8
+// consecutive dims: one 16-byte load), O^T = V^T P^T with V^T operands from a transposed copy
+// of V whose 16-key blocks store their keys in the order {0-3, 8-11, 4-7, 12-15}: the order in
+// which a lane half holds P after the score MFMA, so each operand is again one 16-byte load.
+// The next tile's K operands are fetched while the current tile's softmax and PV run.
+
+// Blocked operand copies of K and V (one pass per call), so that every MFMA operand load of
+// the attention kernel reads whole contiguous 512-byte/1-KiB runs:
+//   kb[b][kvh][blk][s][16 keys][2 halves][8 dims]   K[16 blk + key][16 s + 8 half + j]
+//   vb[b][kvh][blk][d][16 slots]                     V[16 blk + vt_key(slot)][d]
+// with keys of a 16-key block stored in the order {0-3, 8-11, 4-7, 12-15} in vb: the order in
+// which a lane half holds P after the score MFMA.  Keys >= S are zero.  Sp = keys per (b, kvh),
+// a multiple of 64.
+constexpr int kVtKeys = 64;
+
+__device__ __forceinline__ int vt_key(int slot) {   // key stored at slot (0..15) of a block
+    const int g = slot >> 3, j = slot & 7;
+    return j < 4 ? 4 * g + j : 8 + 4 * g + (j - 4);
+}
+
+template <int DH>
+__global__ __launch_bounds__(256) void kv_block_kernel(const uint16_t* __restrict__ k,
+                                                       int64_t k_sb, int64_t k_sh, int64_t k_ss,
+                                                       const uint16_t* __restrict__ v,
+                                                       int64_t v_sb, int64_t v_sh, int64_t v_ss,
+                                                       uint16_t* __restrict__ kb,
+                                                       uint16_t* __restrict__ vb, int S, int Sp,
+                                                       int KVH) {
+    constexpr int RS = DH + 8;     // LDS row stride (elements), 16-byte multiple
+    constexpr int KS = DH / 16;
+    __shared__ __align__(16) uint16_t sK[kVtKeys * RS];
+    __shared__ __align__(16) uint16_t sV[kVtKeys * RS];
+    const int k0 = blockIdx.x * kVtKeys, kvh = blockIdx.y, b = blockIdx.z;
+    const uint16_t* kg = k + b * k_sb + kvh * k_sh;
+    const uint16_t* vg = v + b * v_sb + kvh * v_sh;
+    constexpr int CPR = DH / 8;
+    for (int c = threadIdx.x; c < kVtKeys * CPR; c += 256) {
+        const int kk = c / CPR, dp = c % CPR;
+        uint4 uk = make_uint4(0u, 0u, 0u, 0u), uv = uk;
+        if (k0 + kk < S) {
+            uk = *reinterpret_cast<const uint4*>(kg + (int64_t)(k0 + kk) * k_ss + dp * 8);
+            uv = *reinterpret_cast<const uint4*>(vg + (int64_t)(k0 + kk) * v_ss + dp * 8);
+        }
+        *reinterpret_cast<uint4*>(&sK[kk * RS + dp * 8]) = uk;
+        *reinterpret_cast<uint4*>(&sV[kk * RS + dp * 8]) = uv;
+    }
+    __syncthreads();
+    const int64_t base = ((int64_t)b * KVH + kvh) * (int64_t)Sp * DH + (int64_t)k0 * DH;
+    // kb: 16-byte piece c -> (blk, s, key, half); consecutive c are consecutive in memory
+    for (int c = threadIdx.x; c < kVtKeys * DH / 8; c += 256) {
+        const int half = c & 1, key = (c >> 1) & 15, sb = c >> 5;   // sb = blk * KS + s
+        const int blk = sb / KS, st = sb % KS;
+        const uint4 u = *reinterpret_cast<const uint4*>(&sK[(16 * blk + key) * RS + 16 * st + 8 * half]);
+        *reinterpret_cast<uint4*>(kb + base + (int64_t)c * 8) = u;
+    }
+    // vb: 16-byte piece c -> (blk, d, half of the 16 slots)
+    for (int c = threadIdx.x; c < kVtKeys * DH / 8; c += 256) {
+        const int half = c & 1, d = (c >> 1) % DH, blk = (c >> 1) / DH;
+        uint32_t w[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int ka = 16 * blk + vt_key(8 * half + 2 * j);
+            const int kb2 = 16 * blk + vt_key(8 * half + 2 * j + 1);
+            w[j] = (uint32_t)sV[ka * RS + d] | ((uint32_t)sV[kb2 * RS + d] << 16);
+        }
+        *reinterpret_cast<uint4*>(vb + base + (int64_t)c * 8) = make_uint4(w[0], w[1], w[2], w[3]);
+    }
+}
+
+constexpr float kRescaleLog2 = 8.0f;   // a row's softmax reference may trail its max by 2^8
+constexpr int kV2Threads = 128;        // two waves: rows 0-31 and 32-63 of a query chunk
+
+template <int DH>
+__global__ __launch_bounds__(kV2Threads) void attend_v2_kernel(AttnArgs A,
+                                                               const uint16_t* __restrict__ kbl,
+                                                               const uint16_t* __restrict__ vbl,
+                                                               int Sp, int nb_cap) {
+    constexpr int KS = DH / 16, DB = DH / 32;
+    extern __shared__ __align__(16) int sTab[];   // block table: first position, first row
+    int* sPos = sTab;
+    int* sThr = sTab + nb_cap;
+    int b, h, n;
+    block_coords(A.B * A.H * A.N, A.B, A.H, A.N, &b, &h, &n);
+    const int kvh = h / (A.H / A.KVH);
+    const int C = A.C, gs = A.gs, M = A.M;
+    int rows = A.S - n * C;
+    if (rows > C) rows = C;
+    const int w = threadIdx.x / kWave, l = lane_id(), g = l >> 5, lr = l & 31;
+    const int row = 32 * w + lr;                   // chunk-local query row of this lane
+    const int Kgw = A.Kg > 0 ? A.Kg : 1;
+
+    // opened list length (the router compacts valid entries to the front; an invalid entry
+    // inside the list is never visible)
+    const int32_t* ogp = A.open_grp + (((int64_t)b * A.H + h) * A.N + n) * Kgw;
+    const int32_t* otp = A.open_thr + (((int64_t)b * A.H + h) * A.N + n) * Kgw;
+    int last = -1;
+    for (int i = l; i < A.Kg; i += kWave)
+        if (ogp[i] >= 0 && otp[i] >= 0) last = i;
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) last = max(last, __shfl_xor(last, o, kWave));
+    const int nopen = last + 1;                    // identical in both waves
+    int f_hi, l_lo;
+    windows(n, A.kf, A.kl, &f_hi, &l_lo);
+    const int gpb = gs / 16, bpc = C / 16;
+    const int nb1 = f_hi * bpc, nb2 = nb1 + (n - l_lo) * bpc;
+    const int nb3 = nb2 + nopen * gpb, nb4 = nb3 + (rows + 15) / 16;
+    const int ntiles = (nb4 + 1) / 2;              // tiles of two 16-key blocks
+    // block table: first token position and first visible row of every 16-key block
+    for (int gb = threadIdx.x; gb < 2 * ntiles; gb += kV2Threads) {
+        int pos = 0, thr = kNever;
+        if (gb < nb1) {
+            pos = gb * 16;
+            thr = 0;
+        } else if (gb < nb2) {
+            pos = l_lo * C + (gb - nb1) * 16;
+            thr = 0;
+        } else if (gb < nb3) {
+            const int gi = (gb - nb2) / gpb, e = (gb - nb2) % gpb;
+            const int grp = ogp[gi], t = otp[gi];
+            if (grp >= 0 && t >= 0) {
+                pos = (grp / M) * C + (grp % M) * gs + 16 * e;
+                thr = t;
+            }
+        } else if (gb < nb4) {
+            pos = n * C + 16 * (gb - nb3);
+            thr = 16 * (gb - nb3);
+        }
+        sPos[gb] = pos;
+        sThr[gb] = thr;
+    }
+    __syncthreads();
+    if (32 * w >= rows) return;                    // ragged last chunk: no rows for this wave
+
+    // blocked operand copies of this (b, kv head): 16-key blocks of 16 * DH elements
+    const int64_t kvbase = ((int64_t)b * A.KVH + kvh) * (int64_t)Sp * DH;
+    const uint16_t* kbp = kbl + kvbase + (lr & 15) * 16 + 8 * g;   // + blk * 16 * DH + s * 256
+    const uint16_t* vbp = vbl + kvbase + lr * 16 + 8 * g;          // + blk * 16 * DH + d * 512
+    const int kcol = 8 * g;                        // this lane's 8 dims per k-step
+    bf16x8 qb[KS];
+    {
+        const uint16_t* qp = reinterpret_cast<const uint16_t*>(A.q) + b * A.q_sb + h * A.q_sh +
+                             ((int64_t)n * C + row) * A.q_ss;
+#pragma unroll
+        for (int s = 0; s < KS; ++s) {
+            uint4 u = make_uint4(0u, 0u, 0u, 0u);
+            if (row < rows) u = *reinterpret_cast<const uint4*>(qp + 16 * s + kcol);
+            qb[s] = __builtin_bit_cast(bf16x8, u);
+        }
+    }
+    // K operand: lane owns key lr of the 32-key tile (8 consecutive dims per k-step)
+    auto load_k = [&](int t, bf16x8 (&kr)[KS]) {
+        const int2 p2 = *reinterpret_cast<const int2*>(&sPos[2 * t]);
+        const int pa = __builtin_amdgcn_readfirstlane(p2.x), pb = __builtin_amdgcn_readfirstlane(p2.y);
+        const int blk = ((lr >> 4) ? pb : pa) >> 4;
+        const uint16_t* kr_ = kbp + (int64_t)blk * (16 * DH);
+#pragma unroll
+        for (int s = 0; s < KS; ++s)
+            kr[s] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(kr_ + 256 * s));
+    };
+    const float c2 = A.scale * 1.4426950408889634f;
+    // scores of tile t (S^T: lane = query row, 16 keys per lane), masked to the visible keys.
+    // Opened/window blocks have one first-visible row per block (uniform), so a block is all
+    // visible, all hidden, or split at one row for this wave; own-chunk blocks (index >= nb3)
+    // are causal per key.
+    auto scores = [&](int t, const bf16x8 (&kr)[KS]) {
+        const int2 t2 = *reinterpret_cast<const int2*>(&sThr[2 * t]);
+        const int th[2] = {__builtin_amdgcn_readfirstlane(t2.x), __builtin_amdgcn_readfirstlane(t2.y)};
+        floatx16 sc = {};
+#pragma unroll
+        for (int s = 0; s < KS; ++s)
+            sc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kr[s], qb[s], sc, 0, 0, 0);
+        const int gb0 = 2 * t;
+        if (gb0 + 1 >= nb3) {
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const int j = i >> 3;
+                const int within = 8 * ((i >> 2) & 1) + 4 * g + (i & 3);
+                const int thr = th[j] + (gb0 + j >= nb3 ? within : 0);
+                sc[i] = row >= thr ? sc[i] : -INFINITY;
+            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                if (th[j] <= 32 * w) continue;          // every row of this wave sees it
+                const bool vis = th[j] <= 32 * w + 31 && row >= th[j];
+#pragma unroll
+                for (int i = 8 * j; i < 8 * j + 8; ++i) sc[i] = vis ? sc[i] : -INFINITY;
+            }
+        }
+        return sc;
+    };
+    auto row_max = [&](const floatx16& x) {
+        float m = -INFINITY;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) m = fmaxf(m, x[i]);
+        return fmaxf(m, __shfl_xor(m, 32, kWave));
+    };
+
+    // Softmax reference point per row.  The first finite tile max of a row becomes its
+    // reference (a row with no visible key so far has zero accumulators, so adopting it needs
+    // no rescale); later tiles may exceed it by up to 2^8 (p <= 256).  A tile beyond that
+    // triggers a restart: an exact row-max pass over all tiles, then the accumulation again
+    // from tile 0 without further checks.  The accumulators are thus only ever touched by
+    // MFMAs (or zeroed), never rescaled.
+    floatx16 acc[DB];
+#pragma unroll
+    for (int d = 0; d < DB; ++d) acc[d] = floatx16{};
+    float m_ref = -INFINITY, l_run = 0.0f;
+    bool exact = false;
+    bf16x8 kr[KS];
+    load_k(0, kr);
+    for (int t = 0; t < ntiles; ++t) {
+        const int2 p2 = *reinterpret_cast<const int2*>(&sPos[2 * t]);
+        const int pa[2] = {__builtin_amdgcn_readfirstlane(p2.x), __builtin_amdgcn_readfirstlane(p2.y)};
+        bf16x8 vr[DB][2];
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) {
+            const uint16_t* vb = vbp + (int64_t)(pa[ks] >> 4) * (16 * DH);
+#pragma unroll
+            for (int d = 0; d < DB; ++d)
+                vr[d][ks] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(vb + 512 * d));
+        }
+        floatx16 sc = scores(t, kr);
+        if (!exact) {
+            const float m = row_max(sc);
+            bool jump = false;
+            if (m_ref == -INFINITY) m_ref = m;                   // first visible keys
+            else jump = (m - m_ref) * c2 > kRescaleLog2;
+            if (__builtin_amdgcn_ballot_w64(jump)) {
+                // exact row maxima over the whole key sequence, then start over
+                float mt = -INFINITY;
+                for (int u = 0; u < ntiles; ++u) {
+                    bf16x8 ku[KS];
+                    load_k(u, ku);
+                    mt = fmaxf(mt, row_max(scores(u, ku)));
+                }
+                m_ref = mt;
+                l_run = 0.0f;
+#pragma unroll
+                for (int d = 0; d < DB; ++d) acc[d] = floatx16{};
+                exact = true;
+                t = -1;
+                load_k(0, kr);
+                continue;
+            }
+        }
+        if (t + 1 < ntiles) load_k(t + 1, kr);
+        const float nb = m_ref == -INFINITY ? 0.0f : -m_ref * c2;
+        bf16x8 pt[2];
+        float rs = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const float e = __builtin_amdgcn_exp2f(fmaf(sc[i], c2, nb));
+            pt[i >> 3][i & 7] = (__bf16)e;
+            rs += e;
+        }
+        l_run += rs;
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+            for (int d = 0; d < DB; ++d)
+                acc[d] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vr[d][ks], pt[ks], acc[d], 0, 0, 0);
+    }
+    const float lt = l_run + __shfl_xor(l_run, 32, kWave);
+    if (row >= rows) return;
+    const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
+    uint16_t* op = reinterpret_cast<uint16_t*>(A.out) + b * A.o_sb + h * A.o_sh +
+                   ((int64_t)C * n + row) * A.o_ss;
+#pragma unroll
+    for (int d = 0; d < DB; ++d)
+#pragma unroll
+        for (int q4 = 0; q4 < 4; ++q4) {
+            const int dim = d * 32 + 8 * q4 + 4 * g;
+            uint2 u;
+            u.x = (uint32_t)f_to_bf16(acc[d][4 * q4] * inv) |
+                  ((uint32_t)f_to_bf16(acc[d][4 * q4 + 1] * inv) << 16);
+            u.y = (uint32_t)f_to_bf16(acc[d][4 * q4 + 2] * inv) |
+                  ((uint32_t)f_to_bf16(acc[d][4 * q4 + 3] * inv) << 16);
+            *reinterpret_cast<uint2*>(op + dim) = u;
+        }
+}
+
 }  // namespace
 }  // namespace hga
+
+namespace {
+// v2 applies to bf16, head_dim 64/128, group and chunk sizes that are multiples of 16.
+bool use_v2(const hga_config* cfg) {
+    return cfg->dtype == HGA_DTYPE_BF16 && (cfg->head_dim == 64 || cfg->head_dim == 128) &&
+           cfg->group_size % 16 == 0 && cfg->chunk_size % 16 == 0;
+}
+int64_t vt_keys(const hga_config* cfg, int32_t S) {   // Sp: keys per V^T row
+    const int64_t NC = (int64_t)((S + cfg->chunk_size - 1) / cfg->chunk_size) * cfg->chunk_size;
+    return (NC + hga::kVtKeys - 1) / hga::kVtKeys * hga::kVtKeys;
+}
+}  // namespace
+
+extern "C" int hga_attend_prefill_workspace(const hga_config* cfg, int32_t S, int64_t* bytes) {
+    using namespace hga;
+    int rc = check_config(cfg);
+    if (rc) return rc;
+    HGA_REQUIRE(S >= 0 && bytes, HGA_ERR_ARG, "hga_attend_prefill_workspace: bad S/bytes");
+    // blocked copies of K and V
+    *bytes = use_v2(cfg) && S > 0
+                 ? 2 * (int64_t)cfg->batch * cfg->kv_heads * cfg->head_dim * vt_keys(cfg, S) * 2
+                 : 0;
+    return HGA_OK;
+}
 
 extern "C" int hga_attend_prefill(const hga_config* cfg, int32_t S, const void* q, int64_t q_sb,
                                   int64_t q_sh, int64_t q_ss, const void* k, int64_t k_sb,
                                   int64_t k_sh, int64_t k_ss, const void* v, int64_t v_sb,
                                   int64_t v_sh, int64_t v_ss, const int32_t* open_grp,
                                   const int32_t* open_thr, int32_t Kg, void* out, int64_t o_sb,
-                                  int64_t o_sh, int64_t o_ss, void* stream) {
+                                  int64_t o_sh, int64_t o_ss, void* workspace,
+                                  int64_t workspace_bytes, void* stream) {
     using namespace hga;
     int rc = check_config(cfg);
     if (rc) return rc;
@@ -382,6 +694,40 @@ extern "C" int hga_attend_prefill(const hga_config* cfg, int32_t S, const void* 
     const unsigned grid = (unsigned)(a.B * a.H * a.N);
     const size_t lds = sizeof(int) * 2 * (size_t)(Kg > 0 ? Kg : 1);
     hipStream_t st = (hipStream_t)stream;
+    if (use_v2(cfg)) {
+        const uintptr_t al = (uintptr_t)q | (uintptr_t)k | (uintptr_t)v | (uintptr_t)out |
+                             (uintptr_t)workspace;
+        HGA_REQUIRE(al % 16 == 0 && ((q_sb | q_sh | q_ss | k_sb | k_sh | k_ss | v_sb | v_sh |
+                                      v_ss | o_sb | o_sh | o_ss) % 8) == 0,
+                    HGA_ERR_ARG, "hga_attend_prefill: 16-byte aligned rows required");
+        int64_t need = 0;
+        hga_attend_prefill_workspace(cfg, S, &need);
+        HGA_REQUIRE(workspace && workspace_bytes >= need, HGA_ERR_ARG,
+                    "hga_attend_prefill: workspace of %lld bytes required (got %lld)",
+                    (long long)need, (long long)workspace_bytes);
+        const int Sp = (int)vt_keys(cfg, S);
+        uint16_t* kbl = (uint16_t*)workspace;
+        uint16_t* vbl = kbl + (int64_t)a.B * a.KVH * Sp * D;
+        // 16-key blocks of the longest key sequence, rounded up to whole 2-block tiles
+        const int bpc = a.C / 16;
+        const int nb_cap = ((a.kf + a.kl + 1) * bpc + Kg * (a.gs / 16) + 3) / 4 * 4;
+        const size_t lds2 = sizeof(int) * 2 * (size_t)nb_cap;
+        HGA_REQUIRE(lds2 <= 65536, HGA_ERR_UNSUPPORTED,
+                    "hga_attend_prefill: key sequence of %d blocks too long", nb_cap);
+        dim3 tg((unsigned)(Sp / kVtKeys), (unsigned)a.KVH, (unsigned)a.B);
+        if (D == 128) {
+            kv_block_kernel<128><<<tg, 256, 0, st>>>((const uint16_t*)k, k_sb, k_sh, k_ss,
+                                                     (const uint16_t*)v, v_sb, v_sh, v_ss, kbl,
+                                                     vbl, S, Sp, a.KVH);
+            attend_v2_kernel<128><<<grid, kV2Threads, lds2, st>>>(a, kbl, vbl, Sp, nb_cap);
+        } else {
+            kv_block_kernel<64><<<tg, 256, 0, st>>>((const uint16_t*)k, k_sb, k_sh, k_ss,
+                                                    (const uint16_t*)v, v_sb, v_sh, v_ss, kbl,
+                                                    vbl, S, Sp, a.KVH);
+            attend_v2_kernel<64><<<grid, kV2Threads, lds2, st>>>(a, kbl, vbl, Sp, nb_cap);
+        }
+        return launch_status("hga_attend_prefill");
+    }
     if (cfg->dtype == HGA_DTYPE_BF16 && (D == 64 || D == 128)) {
         const uintptr_t al = (uintptr_t)q | (uintptr_t)k | (uintptr_t)v | (uintptr_t)out;
         HGA_REQUIRE(al % 16 == 0 && ((q_sb | q_sh | q_ss | k_sb | k_sh | k_ss | v_sb | v_sh |

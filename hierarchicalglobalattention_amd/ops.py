@@ -183,10 +183,20 @@ def attend_prefill(cfg: HgaConfig, q: torch.Tensor, k: torch.Tensor, v: torch.Te
         out = torch.empty((B, H, S, D), dtype=q.dtype, device=q.device)
     og = open_grp.contiguous()
     ot = open_thr.contiguous()
+    ws = attend_prefill_workspace(cfg, S)
+    wbuf = torch.empty(max(ws, 16), dtype=torch.uint8, device=q.device) if ws else None
     check(lib().hga_attend_prefill(
         ctypes.byref(cfg), S, _p(q), *_s4(q), _p(k), *_s4(k), _p(v), *_s4(v), _p(og), _p(ot),
-        Kg, _p(out), *_s4(out), _stream()), "hga_attend_prefill")
+        Kg, _p(out), *_s4(out), _p(wbuf), ws, _stream()), "hga_attend_prefill")
     return out
+
+
+def attend_prefill_workspace(cfg: HgaConfig, S: int) -> int:
+    """Scratch bytes hga_attend_prefill needs for a block of S tokens."""
+    n = ctypes.c_int64()
+    check(lib().hga_attend_prefill_workspace(ctypes.byref(cfg), S, ctypes.byref(n)),
+          "hga_attend_prefill_workspace")
+    return n.value
 
 
 def decode_widths(cfg: HgaConfig, n_closed: int):

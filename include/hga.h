@@ -130,7 +130,14 @@ int hga_attend_prefill(const hga_config* cfg, int32_t S, const void* q, int64_t 
                        int64_t q_sh, int64_t q_ss, const void* k, int64_t k_sb, int64_t k_sh,
                        int64_t k_ss, const void* v, int64_t v_sb, int64_t v_sh, int64_t v_ss,
                        const int32_t* open_grp, const int32_t* open_thr, int32_t Kg, void* out,
-                       int64_t o_sb, int64_t o_sh, int64_t o_ss, void* stream);
+                       int64_t o_sb, int64_t o_sh, int64_t o_ss, void* workspace,
+                       int64_t workspace_bytes, void* stream);
+
+/* Device scratch bytes hga_attend_prefill needs for a block of S tokens (a transposed copy of
+ * V for bf16 head_dim 64/128 with group and chunk sizes that are multiples of 16; 0 otherwise).
+ * The buffer must be 16-byte aligned and is only used during the call's kernels (stream
+ * ordered).  No counterpart in the reference, whose attend materialises K/V instead. */
+int32_t hga_attend_prefill_workspace(const hga_config* cfg, int32_t S, int64_t* bytes);
 
 /* Widths of the decode routing outputs with n_closed closed chunks: the routing pool is
  * [f_hi, l_lo) of ChunkPlacementPolicy (chunk_placement_policy.py:27-38), Kc = min(topk_chunks,

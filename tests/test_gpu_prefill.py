@@ -91,6 +91,10 @@ def _bf16_case(seed, B, H, KVH, S, Dh, C, gs, kf, kl, tc, tg, theta):
     dict(B=1, H=8, KVH=2, S=4096, Dh=128, C=64, gs=16, kf=2, kl=8, tc=16, tg=64, theta=1e6),
     dict(B=2, H=4, KVH=1, S=1500, Dh=64, C=64, gs=16, kf=1, kl=2, tc=4, tg=8, theta=1e4),
     dict(B=1, H=4, KVH=2, S=203, Dh=64, C=8, gs=4, kf=0, kl=0, tc=3, tg=6, theta=1e4),
+    # shapes of the 16-key-block attention kernel: no windows, C=32, gs=32, one partial chunk
+    dict(B=1, H=4, KVH=2, S=777, Dh=128, C=32, gs=16, kf=0, kl=0, tc=3, tg=5, theta=1e4),
+    dict(B=2, H=4, KVH=2, S=640, Dh=64, C=64, gs=32, kf=1, kl=1, tc=2, tg=3, theta=1e4),
+    dict(B=1, H=2, KVH=1, S=50, Dh=128, C=64, gs=16, kf=1, kl=1, tc=2, tg=4, theta=1e4),
 ])
 def test_prefill_bf16_vs_oracle(hga, shape):
     from hierarchicalglobalattention_amd import ops
@@ -125,6 +129,25 @@ def test_prefill_bf16_vs_oracle(hga, shape):
     err = np.abs(out.float().cpu().numpy() - o_out)
     print("bf16 attention max/mean abs err:", err.max(), err.mean())
     assert err.max() <= 2e-2 and err.mean() <= 1e-2
+
+
+@pytest.mark.parametrize("Dh,gs", [(128, 16), (64, 16), (64, 4)])
+def test_attend_prefill_routing_off(hga, Dh, gs):
+    """Kg = 0 (1-element -1 lists): windows and the causal own chunk only."""
+    from hierarchicalglobalattention_amd import ops
+    B, H, KVH, S, C = 1, 4, 2, 1000, 64
+    q, k_rope, k_raw, v, cos, sin = _bf16_case(3, B, H, KVH, S, Dh, C, gs, 1, 2, 0, 0, 1e4)
+    dev = torch.device("cuda:0")
+    cfg = _cfg(ops, B=B, H=H, KVH=KVH, Dh=Dh, C=C, gs=gs, kf=1, kl=2, tc=0, tg=0, theta=1e4,
+               dtype=torch.bfloat16)
+    N = (S + C - 1) // C
+    e = torch.full((B, H, N, 1), -1, dtype=torch.int32)
+    out = ops.attend_prefill(cfg, q.to(dev), k_rope.to(dev), v.to(dev), e.to(dev), e.to(dev), 0)
+    f = lambda t: t.float().numpy()
+    o_out = oracle.attend_prefill(f(q), f(k_rope), f(v), C, gs, 1, 2, e.numpy(), e.numpy(),
+                                  oracle.attn_scale(Dh), oracle.DT_BF16)
+    err = np.abs(out.float().cpu().numpy() - o_out)
+    assert err.max() <= 2e-2 and err.mean() <= 1e-2, (err.max(), err.mean())
 
 
 def test_route_exact_ties(hga):
