@@ -135,14 +135,18 @@ __device__ __forceinline__ float sumsq_bf16x8(uint4 u) {
 // tiles w, w+8, ... of 32 candidates.
 template <int DH, class RowPtr>
 __device__ void scores_block_mfma(const uint16_t* sQ, int ncand, RowPtr rowptr, float* sRows,
-                                  int stride, float scale, uint32_t* knmax) {
+                                  int stride, float scale, uint32_t* knmax, int nrb = 1) {
     constexpr int KS = DH / 16;
     const int w = threadIdx.x / kWave, l = lane_id();
+    const int ntile = (ncand + 31) / 32;
+    // jobs (row block, candidate tile), row block fastest
+    for (int job = w; job < nrb * ntile; job += kWaves) {
+    const int rb = job % nrb, ct = job / nrb;
     bf16x8 a[KS];
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks)
-        a[ks] = as_bf16x8(*reinterpret_cast<const uint4*>(sQ + (l % 32) * DH + ks * 16 + 8 * (l / 32)));
-    for (int ct = w; ct * 32 < ncand; ct += kWaves) {
+        a[ks] = as_bf16x8(*reinterpret_cast<const uint4*>(sQ + (32 * rb + l % 32) * DH + ks * 16 + 8 * (l / 32)));
+    {
         const int c = ct * 32 + l % 32;
         const bool cv = c < ncand;
         const uint16_t* kp = cv ? rowptr(c) : nullptr;
@@ -153,21 +157,24 @@ __device__ void scores_block_mfma(const uint16_t* sQ, int ncand, RowPtr rowptr, 
             if (cv) u[ks] = *reinterpret_cast<const uint4*>(kp + ks * 16 + 8 * (l / 32));
         }
         floatx16 acc = {};
-        float nsq = 0.0f;
 #pragma unroll
-        for (int ks = 0; ks < KS; ++ks) {
-            nsq += sumsq_bf16x8(u[ks]);
+        for (int ks = 0; ks < KS; ++ks)
             acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[ks], as_bf16x8(u[ks]), acc, 0, 0, 0);
+        if (knmax && rb == 0) {   // largest candidate norm (once per candidate tile)
+            float nsq = 0.0f;
+#pragma unroll
+            for (int ks = 0; ks < KS; ++ks) nsq += sumsq_bf16x8(u[ks]);
+            nsq += __shfl_xor(nsq, 32, kWave);
+            if (cv && l < 32) atomicMax(knmax, __float_as_uint(sqrtf(nsq)));
         }
-        nsq += __shfl_xor(nsq, 32, kWave);
         if (cv) {
-            if (knmax && l < 32) atomicMax(knmax, __float_as_uint(sqrtf(nsq)));
 #pragma unroll
             for (int i = 0; i < 16; ++i) {
-                const int row = 8 * (i / 4) + 4 * (l / 32) + (i % 4);
+                const int row = 32 * rb + 8 * (i / 4) + 4 * (l / 32) + (i % 4);
                 sRows[row * stride + c] = acc[i] * scale;
             }
         }
+    }
     }
 }
 
@@ -287,6 +294,228 @@ __device__ __forceinline__ void load_block(T* sQ, const T* qg, int64_t q_ss, int
 }
 
 // ------------------------------------------------------------------------------------------
+// row-group selection: one query row per 16-lane DPP row, four rows per wave in lockstep
+// ------------------------------------------------------------------------------------------
+// Lane `seg` (= lane % 16) of a row holds candidates seg + 16*i (i < JJ) in registers.  The
+// per-row count of keys >= x is a 16-lane DPP reduction, so a search step costs 2*JJ + 8 VALU
+// operations for four rows at once.
+template <class Op>
+__device__ __forceinline__ int row16_reduce(int x, Op op) {
+    x = op(x, dpp<0xB1>(x));    // quad_perm [1,0,3,2]
+    x = op(x, dpp<0x4E>(x));    // quad_perm [2,3,0,1]
+    x = op(x, dpp<0x124>(x));   // row_ror:4
+    x = op(x, dpp<0x128>(x));   // row_ror:8
+    return x;
+}
+__device__ __forceinline__ int r16_sum(int x) { return row16_reduce(x, [](int a, int b) { return a + b; }); }
+__device__ __forceinline__ float r16_fsum(float x) {
+    return __int_as_float(row16_reduce(__float_as_int(x), [](int a, int b) {
+        return __float_as_int(__int_as_float(a) + __int_as_float(b));
+    }));
+}
+[[maybe_unused]] __device__ __forceinline__ float r16_fmin(float x) {
+    return __int_as_float(row16_reduce(__float_as_int(x), [](int a, int b) {
+        return __float_as_int(fminf(__int_as_float(a), __int_as_float(b)));
+    }));
+}
+[[maybe_unused]] __device__ __forceinline__ float r16_fmax(float x) {
+    return __int_as_float(row16_reduce(__float_as_int(x), [](int a, int b) {
+        return __float_as_int(fmaxf(__int_as_float(a), __int_as_float(b)));
+    }));
+}
+__device__ __forceinline__ uint32_t r16_umin(uint32_t x) {
+    return (uint32_t)row16_reduce((int)x, [](int a, int b) { return (int)min((uint32_t)a, (uint32_t)b); });
+}
+__device__ __forceinline__ uint32_t r16_umax(uint32_t x) {
+    return (uint32_t)row16_reduce((int)x, [](int a, int b) { return (int)max((uint32_t)a, (uint32_t)b); });
+}
+
+template <int JJ>
+__device__ __forceinline__ int r16_count_ge(const uint32_t (&kv)[JJ], uint32_t x) {
+    int c = 0;
+#pragma unroll
+    for (int i = 0; i < JJ; ++i) c += kv[i] >= x ? 1 : 0;
+    return r16_sum(c);
+}
+
+// Exact top-k of the row's keys (0 = not a candidate; larger key first, equal keys -> lower
+// candidate index seg + 16*i).  Every lane of the wave must call it (DPP reads neighbours).
+// Returns member bits.
+// Upper-tail normal quantile (Abramowitz & Stegun 26.2.23) with hardware log/sqrt: a search
+// seed only, so approximate transcendental instructions are fine.
+__device__ __forceinline__ float z_upper_fast(float p) {
+    p = fminf(fmaxf(p, 1e-6f), 1.0f - 1e-6f);
+    const bool lower = p > 0.5f;
+    const float pp = lower ? 1.0f - p : p;
+    const float t = __builtin_sqrtf(-2.0f * 0.69314718f * __builtin_amdgcn_logf(pp));
+    const float z = t - (2.515517f + 0.802853f * t + 0.010328f * t * t) *
+                            __builtin_amdgcn_rcpf(1.0f + 1.432788f * t + 0.189269f * t * t +
+                                                  0.001308f * t * t * t);
+    return lower ? -z : z;
+}
+
+template <int JJ>
+__device__ uint32_t rowgroup_topk(const uint32_t (&kv)[JJ], int k) {
+    const int l = lane_id(), seg = l & 15;
+    const int nv = r16_count_ge<JJ>(kv, 1u);
+    float s1 = 0.0f, s2 = 0.0f;
+    uint32_t kmn = 0xffffffffu, kmx = 0u;
+#pragma unroll
+    for (int i = 0; i < JJ; ++i)
+        if (kv[i] != 0u) {
+            const float x = okey_inv(kv[i]);
+            s1 += x;
+            s2 = fmaf(x, x, s2);
+            kmn = min(kmn, kv[i]);
+            kmx = max(kmx, kv[i]);
+        }
+    s1 = r16_fsum(s1);
+    s2 = r16_fsum(s2);
+    kmn = r16_umin(kmn);
+    kmx = r16_umax(kmx);
+    // state per row: threshold vsep (members: key >= vsep, or > vsep plus ties when tie)
+    bool done = nv <= k, tie = false;
+    uint32_t vsep = 1u, lo = kmn, hi = kmx;
+    int clo = nv;
+    int chi = r16_count_ge<JJ>(kv, kmx);
+    if (!done && chi >= k) {
+        vsep = kmx;
+        tie = true;
+        done = true;
+    }
+    float guess = 0.0f;
+    {
+        const float rn = __builtin_amdgcn_rcpf((float)(nv > 0 ? nv : 1));
+        const float mu = s1 * rn;
+        const float sd = __builtin_sqrtf(fmaxf(s2 * rn - mu * mu, 0.0f));
+        guess = mu + z_upper_fast((k + 0.5f) * rn) * sd;
+    }
+    for (int it = 0; __ballot(!done) != 0; ++it) {
+        uint32_t mid = lo + (hi - lo) / 2u;
+        if (it < 8) {
+            const float lf = okey_inv(lo), hf = okey_inv(hi), span = hf - lf;
+            // the interpolated probe only steers the search: approximate reciprocal is enough
+            float x = it == 0 ? guess
+                              : lf + span * (float)(clo - k) * __builtin_amdgcn_rcpf((float)(clo - chi));
+            x = fminf(fmaxf(x, lf + span * 0.0625f), hf - span * 0.0625f);
+            const uint32_t xm = okey(x);
+            mid = (x == x && span < INFINITY && xm > lo && xm < hi) ? xm : mid;
+        }
+        const int c = r16_count_ge<JJ>(kv, mid);
+        if (!done) {
+            if (c == k) {
+                vsep = mid;
+                done = true;
+            } else {
+                if (c > k) {
+                    lo = mid;
+                    clo = c;
+                } else {
+                    hi = mid;
+                    chi = c;
+                }
+                if (hi - lo <= 1u) {
+                    vsep = lo;
+                    tie = true;
+                    done = true;
+                }
+            }
+        }
+    }
+    uint32_t bits = 0;
+#pragma unroll
+    for (int i = 0; i < JJ; ++i) bits |= ((tie ? kv[i] > vsep : kv[i] >= vsep) ? 1u : 0u) << i;
+    if (__ballot(tie) != 0) {
+        // boundary ties: the lowest candidate indices (i-major, then seg) among key == vsep
+        int r = k - r16_count_ge<JJ>(kv, vsep + 1u);
+        const int sh = 16 * (l >> 4);
+#pragma unroll
+        for (int i = 0; i < JJ; ++i) {
+            const bool eq = tie && kv[i] == vsep;
+            const uint32_t m16 = (uint32_t)(__ballot(eq) >> sh) & 0xffffu;
+            const int below = __popc(m16 & ((1u << seg) - 1u));
+            if (eq && below < r) bits |= 1u << i;
+            const int n16 = __popc(m16);
+            r -= n16 < r ? n16 : r;
+        }
+    }
+    return bits;
+}
+
+// Row-group requests of block rows [r0, r0+32): lane -> (row rr = 4w + lane/16, seg); each
+// row's candidate values come from sS[rr * stride + c] (-inf if not visible).  Certified rows
+// raise the pooled key / lower the first row of their members and write their request bitmap;
+// rows whose k-th and (k+1)-th values lie within 2*delta are queued (absolute row) in sAmb for
+// the canonical path.
+template <int JJ, class Vis>
+__device__ void rowgroup_requests(int r0, int brows, int ncand, const float* sS, int stride,
+                                  int k, float dsc, const float* sQn, Vis vis, uint32_t* sPk,
+                                  int* sFirst, uint32_t* sBits, int BW, int* sAmb, int* sAmbN) {
+    const int w = threadIdx.x / kWave, l = lane_id(), seg = l & 15;
+    const int rr = 4 * w + (l >> 4), t = r0 + rr;
+    const bool act = rr < brows;
+    uint32_t kv[JJ];
+#pragma unroll
+    for (int i = 0; i < JJ; ++i) {
+        const int c = seg + 16 * i;
+        const float x = (act && c < ncand && vis(t, c)) ? sS[rr * stride + c] : -INFINITY;
+        kv[i] = x == -INFINITY ? 0u : okey(x);
+    }
+    const uint32_t bits = rowgroup_topk<JJ>(kv, k);
+    // certification: k-th and (k+1)-th values at least 2*delta apart
+    bool amb = false;
+    if (dsc > 0.0f) {
+        uint32_t kk = 0xffffffffu, kk1 = 0u;      // smallest member key, largest non-member key
+#pragma unroll
+        for (int i = 0; i < JJ; ++i) {
+            if (kv[i] == 0u) continue;
+            if ((bits >> i) & 1u) kk = min(kk, kv[i]);
+            else kk1 = max(kk1, kv[i]);
+        }
+        kk = r16_umin(kk);
+        kk1 = r16_umax(kk1);
+        const float ak = kk == 0xffffffffu ? INFINITY : okey_inv(kk);
+        const float ak1 = kk1 == 0u ? -INFINITY : okey_inv(kk1);
+        const float delta = act ? dsc * sQn[t] : 0.0f;
+        amb = act && ak1 != -INFINITY && !(ak - 2.0f * delta > ak1);
+    }
+    if (amb) {
+        if (seg == 0) sAmb[atomicAdd(sAmbN, 1)] = t;
+        return;
+    }
+    if (!act) return;
+#pragma unroll
+    for (int i = 0; i < JJ; ++i)
+        if ((bits >> i) & 1u) {
+            const int c = seg + 16 * i;
+            atomicMax(&sPk[c], kv[i]);
+            atomicMin(&sFirst[c], t);
+        }
+    // request bitmap of the row: candidate c -> word c / 32, bit c % 32
+    uint32_t word = 0;
+#pragma unroll
+    for (int i = 0; i < JJ; ++i) {
+        const uint32_t m16 = (uint32_t)(__ballot((bits >> i) & 1u) >> (16 * (l >> 4))) & 0xffffu;
+        word |= m16 << (16 * (i & 1));
+        if ((i & 1) || i == JJ - 1) {
+            if (seg == 0 && (i >> 1) < BW) sBits[t * BW + (i >> 1)] = word;
+            word = 0;
+        }
+    }
+}
+
+// Calls f(JTag<JJ>) with the smallest JJ in {1,2,4,8,16,32} such that 16*JJ >= n (n <= 512).
+template <class F>
+__device__ __forceinline__ void dispatch_jj(int n, F&& f) {
+    if (n <= 16) f(JTag<1>{});
+    else if (n <= 32) f(JTag<2>{});
+    else if (n <= 64) f(JTag<4>{});
+    else if (n <= 128) f(JTag<8>{});
+    else if (n <= 256) f(JTag<16>{});
+    else f(JTag<32>{});
+}
+
+// ------------------------------------------------------------------------------------------
 // the kernel
 // ------------------------------------------------------------------------------------------
 template <int DT, int DH>
@@ -304,6 +533,7 @@ void route_prefill_kernel(RouteArgs A) {
     int* sSel = reinterpret_cast<int*>(sBits + kRows * BW);          // [kMaxSel] sorted chunk ids
     int* sThr = sSel + kMaxSel;                                      // [kMaxSel]
     int* sScal = sThr + kMaxSel;                                     // [8] scalars
+    int* sAmb = sScal + 8;                                           // [kRows] ambiguous rows
 
     const int N = A.N, C = A.C, M = A.M;
     const int n = N - 1 - (int)(blockIdx.x / (A.B * A.H));          // heavy chunks first
@@ -368,22 +598,35 @@ void route_prefill_kernel(RouteArgs A) {
         __syncthreads();
         const float ds1 = use_mfma ? kDeltaRel * __uint_as_float((uint32_t)sScal[1]) * scale * 1.01f : 0.0f;
         const int kreq = A.Kc < P ? A.Kc : P;
-        dispatch_j(P, [&](auto jt) {
-            constexpr int J = decltype(jt)::value;
-            for (int r = w; r < brows; r += kWaves) {
-                const int t = r0 + r;
-                float v[J];
-#pragma unroll
-                for (int j = 0; j < J; ++j) {
-                    const int i = l + 64 * j;
-                    v[j] = i < P ? sS[r * SP + i] : -INFINITY;
-                }
-                const T* qr = sQ + r * DH;
-                row_request<J>(t, v, kreq, ds1 * sQn[t],
-                               [&](int i) { return canon_dot<DT, DH>(qr, crow(i), scale); }, sPk,
-                               sFirst, sBits, BW, &amb1);
-            }
+        if (threadIdx.x == 0) sScal[4] = 0;
+        __syncthreads();
+        dispatch_jj(P, [&](auto jt) {
+            constexpr int JJ = decltype(jt)::value;
+            rowgroup_requests<JJ>(r0, brows, P, sS, SP, kreq, ds1, sQn,
+                                  [](int, int) { return true; }, sPk, sFirst, sBits, BW, sAmb,
+                                  &sScal[4]);
         });
+        __syncthreads();
+        // rows the MFMA scores could not certify: canonical re-rank (one row per wave)
+        const int namb = sScal[4];
+        if (namb > 0) {
+            dispatch_j(P, [&](auto jt) {
+                constexpr int J = decltype(jt)::value;
+                for (int a = w; a < namb; a += kWaves) {
+                    const int t = sAmb[a], r = t - r0;
+                    float v[J];
+#pragma unroll
+                    for (int j = 0; j < J; ++j) {
+                        const int i = l + 64 * j;
+                        v[j] = i < P ? sS[r * SP + i] : -INFINITY;
+                    }
+                    const T* qr = sQ + r * DH;
+                    row_request<J>(t, v, kreq, ds1 * sQn[t],
+                                   [&](int i) { return canon_dot<DT, DH>(qr, crow(i), scale); },
+                                   sPk, sFirst, sBits, BW, &amb1);
+                }
+            });
+        }
         __syncthreads();
     }
     float qnmax = 0.0f;
@@ -430,35 +673,57 @@ void route_prefill_kernel(RouteArgs A) {
             return gkb + ((int64_t)sSel[i / M] * M + (i % M)) * DH;
         };
         auto canonG2 = [&](int t, int i) { return canon_dot<DT, DH>(qg + t * A.q_ss, grow(i), scale); };
+        auto vis2 = [&](int t, int i) { return sThr[i / M] <= t; };
+        // all rows at once: scores [64][SP2] at the head of sS, the 64 query rows behind them
+        T* sQ2 = reinterpret_cast<T*>(sS + ((kRows * SP2 + 3) / 4) * 4);
+        {
+            constexpr int VE = 16 / (int)sizeof(T);
+            for (int idx = threadIdx.x; idx < kRows * (DH / VE); idx += kThreads) {
+                const int r = idx / (DH / VE), d = (idx % (DH / VE)) * VE;
+                uint4 u = make_uint4(0u, 0u, 0u, 0u);
+                if (r < rows) u = *reinterpret_cast<const uint4*>(qg + (int64_t)r * A.q_ss + d);
+                *reinterpret_cast<uint4*>(sQ2 + r * DH + d) = u;
+            }
+        }
+        if (threadIdx.x == 0) sScal[4] = 0;
+        __syncthreads();
+        if (use_mfma)
+            scores_block_mfma<DH>(reinterpret_cast<const uint16_t*>(sQ2), T2,
+                                  [&](int i) { return reinterpret_cast<const uint16_t*>(grow(i)); },
+                                  sS, SP2, scale, reinterpret_cast<uint32_t*>(&sScal[2]),
+                                  (rows + 31) / 32);
+        else
+            for (int idx = threadIdx.x; idx < rows * T2; idx += kThreads)
+                sS[(idx / T2) * SP2 + idx % T2] =
+                    canon_dot<DT, DH>(sQ2 + (idx / T2) * DH, grow(idx % T2), scale);
+        __syncthreads();
+        const float ds2 = use_mfma ? kDeltaRel * __uint_as_float((uint32_t)sScal[2]) * scale * 1.01f : 0.0f;
         for (int r0 = 0; r0 < rows; r0 += kBlk) {
             const int brows = rows - r0 < kBlk ? rows - r0 : kBlk;
-            load_block<T, DH>(sQ, qg, A.q_ss, r0, rows);
-            __syncthreads();
-            if (use_mfma)
-                scores_block_mfma<DH>(reinterpret_cast<const uint16_t*>(sQ), T2,
-                                      [&](int i) { return reinterpret_cast<const uint16_t*>(grow(i)); },
-                                      sS + r0 * SP2, SP2, scale,
-                                      r0 == 0 ? reinterpret_cast<uint32_t*>(&sScal[2]) : nullptr);
-            else
-                for (int idx = threadIdx.x; idx < brows * T2; idx += kThreads)
-                    sS[(r0 + idx / T2) * SP2 + idx % T2] =
-                        canon_dot<DT, DH>(sQ + (idx / T2) * DH, grow(idx % T2), scale);
-            __syncthreads();
+            dispatch_jj(T2, [&](auto jt) {
+                constexpr int JJ = decltype(jt)::value;
+                rowgroup_requests<JJ>(r0, brows, T2, sS + r0 * SP2, SP2, A.Kgr, ds2, sQn, vis2,
+                                      sPk, sFirst, sBits, BW, sAmb, &sScal[4]);
+            });
         }
-        const float ds2 = use_mfma ? kDeltaRel * __uint_as_float((uint32_t)sScal[2]) * scale * 1.01f : 0.0f;
-        dispatch_j(T2, [&](auto jt) {
-            constexpr int J = decltype(jt)::value;
-            for (int t = w; t < rows; t += kWaves) {
-                float v[J];
+        __syncthreads();
+        const int namb = sScal[4];
+        if (namb > 0) {
+            dispatch_j(T2, [&](auto jt) {
+                constexpr int J = decltype(jt)::value;
+                for (int a = w; a < namb; a += kWaves) {
+                    const int t = sAmb[a];
+                    float v[J];
 #pragma unroll
-                for (int j = 0; j < J; ++j) {
-                    const int i = l + 64 * j;
-                    v[j] = (i < T2 && sThr[i / M] <= t) ? sS[t * SP2 + i] : -INFINITY;
+                    for (int j = 0; j < J; ++j) {
+                        const int i = l + 64 * j;
+                        v[j] = (i < T2 && sThr[i / M] <= t) ? sS[t * SP2 + i] : -INFINITY;
+                    }
+                    row_request<J>(t, v, A.Kgr, ds2 * sQn[t], [&](int i) { return canonG2(t, i); },
+                                   sPk, sFirst, sBits, BW, &amb2);
                 }
-                row_request<J>(t, v, A.Kgr, ds2 * sQn[t], [&](int i) { return canonG2(t, i); },
-                               sPk, sFirst, sBits, BW, &amb2);
-            }
-        });
+            });
+        }
         __syncthreads();
         if (w == 0) {
             const float dpool2 = ds2 * qnmax;
@@ -563,14 +828,18 @@ extern "C" int hga_route_prefill(const hga_config* cfg, int32_t S, const void* q
     auto odd_above = [](int x) { return (x + 1) | 1; };   // smallest odd stride > x
     a.SP = odd_above(Pmax);
     a.SP2 = odd_above(T2max);
-    a.SSZ = ((kBlk * a.SP > kRows * a.SP2 ? kBlk * a.SP : kRows * a.SP2) + 3) / 4 * 4;
+    // stage 1: [32][SP] scores; stage 2: [64][SP2] scores followed by the 64 query rows
+    const int D0 = cfg->head_dim;
+    const int esz0 = cfg->dtype == HGA_DTYPE_BF16 ? 2 : 4;
+    const int s2sz = (kRows * a.SP2 + 3) / 4 * 4 + kRows * D0 * esz0 / 4;
+    a.SSZ = ((kBlk * a.SP > s2sz ? kBlk * a.SP : s2sz) + 3) / 4 * 4;
     a.SPP = (Pmax > T2max ? Pmax : T2max) + 1;
     a.BW = (a.SPP + 31) / 32;
     const int D = cfg->head_dim;
     const size_t esz = cfg->dtype == HGA_DTYPE_BF16 ? 2 : 4;
     const size_t lds = sizeof(float) * (size_t)a.SSZ + esz * kBlk * D + sizeof(float) * kRows +
                        2 * sizeof(int) * (size_t)a.SPP + sizeof(uint32_t) * (size_t)kRows * a.BW +
-                       sizeof(int) * (2 * kMaxSel + 8);
+                       sizeof(int) * (2 * kMaxSel + 8 + kRows);
     HGA_REQUIRE(lds <= 163840, HGA_ERR_UNSUPPORTED,
                 "hga_route_prefill: %zu bytes of LDS needed (pool %d, head_dim %d)", lds, Pmax, D);
     {
