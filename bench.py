@@ -84,51 +84,88 @@ def run_gpu(args):
     hc = router.hcfg(c["B"], torch.bfloat16)
     cos, sin = rotary_for_positions(c["theta"], c["Dh"], 0, c["S"], dev)
     cos_r, sin_r = cos.to(torch.bfloat16), sin.to(torch.bfloat16)
-    ev = [torch.cuda.Event(enable_timing=True) for _ in range(4)]
-    tsum = [0.0, 0.0, 0.0]
     state = {}
 
-    def step(timed):
-        if timed:
-            ev[0].record()
+    def step():
         q = ops.rope(hc, q_raw, cos, sin)
         k_rope = ops.rope(hc, k_raw, cos, sin)
-        if timed:
-            ev[1].record()
         (routed, lo, hi), = router.route_query_block(0, q, k_rope, k_raw, v, 0, cos=cos_r,
                                                      sin=sin_r)
-        if timed:
-            ev[2].record()
         out = routed.attend(q)
-        if timed:
-            ev[3].record()
         state["routing"], state["out"] = routed.routing, out
 
+    # Per-kernel timing pass: the same launches as step(), issued op by op with HIP events in
+    # between (torch's current stream, the stream every op launches on).
+    B, S, D, C = c["B"], c["S"], c["Dh"], c["C"]
+    N, M = (S + C - 1) // C, C // c["gs"]
+    cos_rf, sin_rf = cos_r.float(), sin_r.float()
+    names = ["rope_q_k", "summarize", "route", "store_seed", "attention"]
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(len(names) + 1)]
+    tsum = [0.0] * len(names)
+
+    def step_timed():
+        st = store.layer(0)
+        store.ensure_capacity(0, N)
+        ev[0].record()
+        q = ops.rope(hc, q_raw, cos, sin)
+        k_rope = ops.rope(hc, k_raw, cos, sin)
+        ev[1].record()
+        ck, gk, _, _ = ops.summarize(hc, k_raw, k_rope, cos_rf, sin_rf, cos_b=cos, sin_b=sin,
+                                     chunk_k_b=st.chunk_k[:, :, :N], group_k_b=st.group_k[:, :, :N])
+        ev[2].record()
+        r = ops.route_prefill(hc, q, ck, gk, S)
+        ev[3].record()
+        store.seed(0, k_rope, v, S // C)
+        ev[4].record()
+        ops.attend_prefill(hc, q, k_rope, v, r["open_grp"], r["open_thr"], r["Kg"])
+        ev[5].record()
+        return r
+
     for _ in range(args.warmup):
-        step(False)
+        step()
     torch.cuda.synchronize()
-    # per-stage timing pass (events between stages), then the clean timed loop
     for _ in range(args.steps):
-        step(True)
+        r_t = step_timed()
         torch.cuda.synchronize()
-        for i in range(3):
+        for i in range(len(names)):
             tsum[i] += ev[i].elapsed_time(ev[i + 1])
+    for _ in range(args.warmup):
+        step()
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for _ in range(args.steps):
-        step(False)
+        step()
     torch.cuda.synchronize()
     t1 = time.perf_counter()
     ms = (t1 - t0) * 1e3 / args.steps
-    st = [x / args.steps for x in tsum]
+    st_ms = {n: x / args.steps for n, x in zip(names, tsum)}
     pairs = useful_pairs(state["routing"], c)
     flops = 4.0 * c["Dh"] * pairs
-    attn_tflops = flops / (st[2] * 1e-3) / 1e12
-    tokens = c["B"] * c["S"]
     assert torch.isfinite(state["out"].float()).all()
-    route_bytes = 2 * (c["B"] * c["H"] * c["S"] * c["Dh"]) + 2 * 2.5 * 2 ** 20
-    return dict(ms=ms, stage_ms=st, pairs=pairs, flops=flops, attn_tflops=attn_tflops,
-                tokens=tokens, route_bytes=route_bytes)
+    # router: algorithmic HBM bytes (q rows, summaries, routing lists) and score FLOPs
+    Kcw, Kgw = r_t["sel_chunk"].shape[-1], r_t["open_grp"].shape[-1]
+    route_bytes = (2 * B * c["H"] * S * D + 2 * B * c["KVH"] * N * (1 + M) * D
+                   + 4 * B * c["H"] * N * (2 * Kcw + 2 * Kgw + 2))
+    n_idx = torch.arange(N)
+    f_hi = torch.clamp(n_idx, max=c["kf"])
+    l_lo = torch.minimum(torch.clamp(n_idx - c["kl"], min=c["kf"]), n_idx)
+    pool = torch.clamp(l_lo - f_hi, min=0)
+    rows = torch.clamp(S - n_idx * C, max=C)
+    nsel = r_t["n_sel"].long().cpu().sum(dim=(0, 1))             # per chunk, summed over heads
+    score_flops = float(2 * D * (c["H"] * B * (rows * pool).sum() + (rows * nsel * M).sum()))
+    return dict(ms=ms, stage_ms=st_ms, pairs=pairs, flops=flops, tokens=B * S,
+                route_bytes=route_bytes, score_flops=score_flops)
+
+
+def copy_calibration(nbytes: int = 1 << 30, reps: int = 3):
+    """A plain device copy of known size, for scaling the FETCH_SIZE / WRITE_SIZE counters."""
+    dev = torch.device("cuda:0")
+    a = torch.empty(nbytes // 2, dtype=torch.bfloat16, device=dev).normal_()
+    b = torch.empty_like(a)
+    for _ in range(reps):
+        b.copy_(a)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_bytes_read": nbytes, "copy_bytes_written": nbytes, "reps": reps}))
 
 
 DEC_CFG = dict(H=32, KVH=4, Dh=128, C=64, gs=16, kf=2, kl=8, theta=1e6)
@@ -238,6 +275,19 @@ def run_decode(*, ctx, B, tc, tg, tier, steps, warmup, needles=False, seed=0):
                 h2d_gbs=(rd / (attn_ms * 1e-3) / 1e9) if tier == "ram" else None)
 
 
+def _measured_traffic():
+    """HBM bytes per launch of the dominant kernel, from the committed rocprofv3 counter summary
+    (FETCH_SIZE + WRITE_SIZE, scaled by the same counters over a plain copy); None if absent."""
+    path = os.path.join(HERE, "profiles", "c3_route_prefill_traffic.md")
+    try:
+        for line in open(path):
+            if line.startswith("traffic_bytes_per_launch:"):
+                return float(line.split(":", 1)[1])
+    except OSError:
+        pass
+    return None
+
+
 def cpu_baseline(budget_s: float):
     """The op-faithful torch CPU mirror of the reference path, on a bounded query-chunk slab of
     the same workload, scaled to tokens/s."""
@@ -258,12 +308,33 @@ def main():
     ap.add_argument("--cpu-budget", type=float, default=15.0)
     ap.add_argument("--no-decode", action="store_true", help="skip the decode legs (c4, c5)")
     ap.add_argument("--decode-steps", type=int, default=256)
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="run only a 1 GiB device copy (scales the HBM byte counters)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py: this build targets a single MI355X; multi-GPU runs are out of scope "
               "(see DESIGN.md for how the path would shard)", file=sys.stderr)
         sys.exit(2)
+    if args.copy_calibration:
+        copy_calibration()
+        return
     g = run_gpu(args)
+    t_route, t_attn = g["stage_ms"]["route"], g["stage_ms"]["attention"]
+    attn_tflops = g["flops"] / (t_attn * 1e-3) / 1e12
+    route_gbs = g["route_bytes"] / (t_route * 1e-3) / 1e9
+    traffic = _measured_traffic()
+    if t_route >= t_attn:
+        roofline = {"kernel": "route_prefill_kernel<bf16,128>", "bound": "hbm",
+                    "achieved": route_gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                    "frac": route_gbs / HBM_PEAK_GBS, "traffic": traffic,
+                    "algorithmic_bytes": g["route_bytes"],
+                    "score_mfma_tflops": g["score_flops"] / (t_route * 1e-3) / 1e12,
+                    "score_mfma_frac": g["score_flops"] / (t_route * 1e-3) / 1e12
+                                       / MFMA_BF16_PEAK_TFLOPS}
+    else:
+        roofline = {"kernel": "kv_block_kernel + attend_v2_kernel<128>", "bound": "mfma",
+                    "achieved": attn_tflops, "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                    "frac": attn_tflops / MFMA_BF16_PEAK_TFLOPS, "traffic": traffic}
     dec = None
     if not args.no_decode:
         ds = args.decode_steps
@@ -298,13 +369,13 @@ def main():
                    "head_dim": CFG["Dh"], "chunk_size": CFG["C"], "group_size": CFG["gs"],
                    "keep_first": CFG["kf"], "keep_last": CFG["kl"],
                    "topk_chunks": CFG["tc"], "topk_groups": CFG["tg"], "rope_theta": CFG["theta"]},
-        "stages_ms": {"rope_q_k": g["stage_ms"][0], "summaries_route_seed": g["stage_ms"][1],
-                      "attention": g["stage_ms"][2]},
-        "roofline": {"kernel": "attend_mfma_kernel<128>", "bound": "mfma",
-                     "achieved": g["attn_tflops"], "peak": MFMA_BF16_PEAK_TFLOPS,
-                     "unit": "TFLOP/s", "frac": g["attn_tflops"] / MFMA_BF16_PEAK_TFLOPS,
-                     "traffic": None,
-                     "algorithmic_flops": g["flops"], "visible_qk_pairs": g["pairs"]},
+        "stages_ms": g["stage_ms"],
+        "roofline": roofline,
+        "roofline_attention": {"kernel": "kv_block_kernel + attend_v2_kernel<128>",
+                               "bound": "mfma", "achieved": attn_tflops,
+                               "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                               "frac": attn_tflops / MFMA_BF16_PEAK_TFLOPS,
+                               "algorithmic_flops": g["flops"], "visible_qk_pairs": g["pairs"]},
         "decode": dec,
         "cpu_baseline": cpu,
         "host": {"cpu": platform.processor() or platform.machine(), "torch": torch.__version__},
