@@ -50,7 +50,7 @@ struct RouteArgs {
     int32_t *sel_chunk, *sel_thr, *n_sel, *open_grp, *open_thr, *n_open;
     int32_t* stats;
     int B, H, KVH, S, N, C, M, kf, kl, Kc, Kg, Kgr;
-    int SP, SP2, SSZ, SPP, BW, canonical;
+    int SP, SP2, SSZ, SPP, BW, SPP2, BW2, canonical;
     float scale;
 };
 
@@ -133,14 +133,14 @@ __device__ __forceinline__ float sumsq_bf16x8(uint4 u) {
 // candidates, written to sRows[row * stride + c]; the largest candidate norm is folded into
 // *knmax (uint bits of a non-negative float) when knmax is not NULL.  Wave w handles candidate
 // tiles w, w+8, ... of 32 candidates.
-template <int DH, class RowPtr>
+template <int DH, int NW = kWaves, class RowPtr>
 __device__ void scores_block_mfma(const uint16_t* sQ, int ncand, RowPtr rowptr, float* sRows,
                                   int stride, float scale, uint32_t* knmax, int nrb = 1) {
     constexpr int KS = DH / 16;
     const int w = threadIdx.x / kWave, l = lane_id();
     const int ntile = (ncand + 31) / 32;
     // jobs (row block, candidate tile), row block fastest
-    for (int job = w; job < nrb * ntile; job += kWaves) {
+    for (int job = w; job < nrb * ntile; job += NW) {
     const int rb = job % nrb, ct = job / nrb;
     bf16x8 a[KS];
 #pragma unroll
@@ -520,11 +520,11 @@ __device__ __forceinline__ void dispatch_jj(int n, F&& f) {
 // ------------------------------------------------------------------------------------------
 template <int DT, int DH>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4)))
-void route_prefill_kernel(RouteArgs A) {
+void route_stage1_kernel(RouteArgs A) {
     typedef typename Elem<DT>::T T;
     extern __shared__ __align__(16) unsigned char smem_raw[];
-    const int SP = A.SP, SP2 = A.SP2, BW = A.BW;
-    float* sS = reinterpret_cast<float*>(smem_raw);                 // [32][SP] | [64][SP2]
+    const int SP = A.SP, BW = A.BW;
+    float* sS = reinterpret_cast<float*>(smem_raw);                 // [32][SP]
     T* sQ = reinterpret_cast<T*>(sS + A.SSZ);                        // [32][DH]
     float* sQn = reinterpret_cast<float*>(sQ + kBlk * DH);           // [64]
     uint32_t* sPk = reinterpret_cast<uint32_t*>(sQn + kRows);        // [SPP] pooled key
@@ -535,7 +535,7 @@ void route_prefill_kernel(RouteArgs A) {
     int* sScal = sThr + kMaxSel;                                     // [8] scalars
     int* sAmb = sScal + 8;                                           // [kRows] ambiguous rows
 
-    const int N = A.N, C = A.C, M = A.M;
+    const int N = A.N, C = A.C;
     const int n = N - 1 - (int)(blockIdx.x / (A.B * A.H));          // heavy chunks first
     const int bh = blockIdx.x % (A.B * A.H);
     const int b = bh / A.H, h = bh % A.H, kvh = h / (A.H / A.KVH);
@@ -546,21 +546,18 @@ void route_prefill_kernel(RouteArgs A) {
     windows(n, A.kf, A.kl, &f_hi, &l_lo);
     const int P = l_lo > f_hi ? l_lo - f_hi : 0;
     const int64_t o = ((int64_t)b * A.H + h) * N + n;
-    const int Kcw = A.Kc > 0 ? A.Kc : 1, Kgw = A.Kg > 0 ? A.Kg : 1;
+    const int Kcw = A.Kc > 0 ? A.Kc : 1;
     int32_t* out_sc = A.sel_chunk + o * Kcw;
     int32_t* out_st = A.sel_thr + o * Kcw;
-    int32_t* out_og = A.open_grp + o * Kgw;
-    int32_t* out_ot = A.open_thr + o * Kgw;
 
     if (A.Kc == 0 || P == 0) {
         for (int i = threadIdx.x; i < Kcw; i += kThreads) out_sc[i] = out_st[i] = -1;
-        for (int i = threadIdx.x; i < Kgw; i += kThreads) out_og[i] = out_ot[i] = -1;
-        if (threadIdx.x == 0) A.n_sel[o] = A.n_open[o] = 0;
+        if (threadIdx.x == 0) A.n_sel[o] = 0;
         return;
     }
     const bool use_mfma = (DT == HGA_DTYPE_BF16) && !A.canonical;
     const float scale = A.scale;
-    int amb1 = 0, amb1p = 0, amb2 = 0, amb2p = 0;
+    int amb1 = 0, amb1p = 0;
     const T* qg = reinterpret_cast<const T*>(A.q) + b * A.q_sb + h * A.q_sh + (int64_t)n * C * A.q_ss;
     const T* ckb = reinterpret_cast<const T*>(A.ck) + b * A.ck_sb + kvh * A.ck_sh;
     auto crow = [&](int i) -> const T* { return ckb + (int64_t)(f_hi + i) * DH; };
@@ -657,122 +654,186 @@ void route_prefill_kernel(RouteArgs A) {
     }
     if (threadIdx.x == 0) A.n_sel[o] = nsel;
 
-    // ---- stage 2: groups of the selected chunks, all rows ----------------------------------
-    const int T2 = nsel * M;
+    if (A.stats && l == 0) {
+        if (amb1) atomicAdd(&A.stats[0], amb1);
+        if (amb1p) atomicAdd(&A.stats[1], amb1p);
+    }
+}
+
+
+// ------------------------------------------------------------------------------------------
+// stage 2: groups of the selected chunks, all rows of a query chunk (4 waves)
+// ------------------------------------------------------------------------------------------
+constexpr int kThreads2 = 256;
+constexpr int kWaves2 = kThreads2 / kWave;
+
+template <int DT, int DH>
+__global__ __launch_bounds__(kThreads2) __attribute__((amdgpu_waves_per_eu(4)))
+void route_stage2_kernel(RouteArgs A) {
+    typedef typename Elem<DT>::T T;
+    extern __shared__ __align__(16) unsigned char smem_raw[];
+    const int SP2 = A.SP2, BW = A.BW2;
+    float* sS = reinterpret_cast<float*>(smem_raw);                 // [64][SP2] scores
+    T* sQ2 = reinterpret_cast<T*>(sS + (kRows * SP2 + 3) / 4 * 4);  // [64][DH] query rows
+    float* sQn = reinterpret_cast<float*>(sQ2 + kRows * DH);         // [64]
+    uint32_t* sPk = reinterpret_cast<uint32_t*>(sQn + kRows);        // [SPP2] pooled key
+    int* sFirst = reinterpret_cast<int*>(sPk + A.SPP2);              // [SPP2]
+    uint32_t* sBits = reinterpret_cast<uint32_t*>(sFirst + A.SPP2);  // [64][BW2]
+    int* sSel = reinterpret_cast<int*>(sBits + kRows * BW);          // [kMaxSel]
+    int* sThr = sSel + kMaxSel;                                      // [kMaxSel]
+    int* sScal = sThr + kMaxSel;                                     // [8]
+    int* sAmb = sScal + 8;                                           // [kRows]
+
+    const int N = A.N, C = A.C, M = A.M;
+    const int n = N - 1 - (int)(blockIdx.x / (A.B * A.H));          // heavy chunks first
+    const int bh = blockIdx.x % (A.B * A.H);
+    const int b = bh / A.H, h = bh % A.H, kvh = h / (A.H / A.KVH);
+    const int w = threadIdx.x / kWave, l = lane_id();
+    int rows = A.S - n * C;
+    if (rows > C) rows = C;
+    const int64_t o = ((int64_t)b * A.H + h) * N + n;
+    const int Kcw = A.Kc > 0 ? A.Kc : 1, Kgw = A.Kg > 0 ? A.Kg : 1;
+    int32_t* out_og = A.open_grp + o * Kgw;
+    int32_t* out_ot = A.open_thr + o * Kgw;
+    const int nsel = A.Kc > 0 ? A.n_sel[o] : 0;
     if (A.Kg == 0 || A.Kgr == 0 || nsel == 0) {
-        for (int i = threadIdx.x; i < Kgw; i += kThreads) out_og[i] = out_ot[i] = -1;
+        for (int i = threadIdx.x; i < Kgw; i += kThreads2) out_og[i] = out_ot[i] = -1;
         if (threadIdx.x == 0) A.n_open[o] = 0;
-    } else {
-        for (int i = threadIdx.x; i < A.SPP; i += kThreads) {
-            sPk[i] = 0u;
-            sFirst[i] = kNoRow;
+        return;
+    }
+    const bool use_mfma = (DT == HGA_DTYPE_BF16) && !A.canonical;
+    const float scale = A.scale;
+    int amb2 = 0, amb2p = 0;
+    const T* qg = reinterpret_cast<const T*>(A.q) + b * A.q_sb + h * A.q_sh + (int64_t)n * C * A.q_ss;
+    const T* gkb = reinterpret_cast<const T*>(A.gk) + b * A.gk_sb + kvh * A.gk_sh;
+    const int T2 = nsel * M;
+    for (int i = threadIdx.x; i < nsel; i += kThreads2) {
+        sSel[i] = A.sel_chunk[o * Kcw + i];
+        sThr[i] = A.sel_thr[o * Kcw + i];
+    }
+    for (int i = threadIdx.x; i < A.SPP2; i += kThreads2) {
+        sPk[i] = 0u;
+        sFirst[i] = kNoRow;
+    }
+    for (int i = threadIdx.x; i < kRows * BW; i += kThreads2) sBits[i] = 0u;
+    if (threadIdx.x < 8) sScal[threadIdx.x] = 0;
+    {
+        constexpr int VE = 16 / (int)sizeof(T);
+        for (int idx = threadIdx.x; idx < kRows * (DH / VE); idx += kThreads2) {
+            const int r = idx / (DH / VE), d = (idx % (DH / VE)) * VE;
+            uint4 u = make_uint4(0u, 0u, 0u, 0u);
+            if (r < rows) u = *reinterpret_cast<const uint4*>(qg + (int64_t)r * A.q_ss + d);
+            *reinterpret_cast<uint4*>(sQ2 + r * DH + d) = u;
         }
-        for (int i = threadIdx.x; i < kRows * BW; i += kThreads) sBits[i] = 0u;
-        const T* gkb = reinterpret_cast<const T*>(A.gk) + b * A.gk_sb + kvh * A.gk_sh;
-        auto grow = [&](int i) -> const T* {
-            return gkb + ((int64_t)sSel[i / M] * M + (i % M)) * DH;
-        };
-        auto canonG2 = [&](int t, int i) { return canon_dot<DT, DH>(qg + t * A.q_ss, grow(i), scale); };
-        auto vis2 = [&](int t, int i) { return sThr[i / M] <= t; };
-        // all rows at once: scores [64][SP2] at the head of sS, the 64 query rows behind them
-        T* sQ2 = reinterpret_cast<T*>(sS + ((kRows * SP2 + 3) / 4) * 4);
-        {
-            constexpr int VE = 16 / (int)sizeof(T);
-            for (int idx = threadIdx.x; idx < kRows * (DH / VE); idx += kThreads) {
-                const int r = idx / (DH / VE), d = (idx % (DH / VE)) * VE;
-                uint4 u = make_uint4(0u, 0u, 0u, 0u);
-                if (r < rows) u = *reinterpret_cast<const uint4*>(qg + (int64_t)r * A.q_ss + d);
-                *reinterpret_cast<uint4*>(sQ2 + r * DH + d) = u;
-            }
+    }
+    __syncthreads();
+    for (int r = w; r < kRows; r += kWaves2) {       // query row norms (certification bound)
+        float x = 0.0f;
+        for (int d = l; d < DH; d += kWave) {
+            const float e = Elem<DT>::ld(sQ2, r * DH + d);
+            x = fmaf(e, e, x);
         }
-        if (threadIdx.x == 0) sScal[4] = 0;
-        __syncthreads();
-        if (use_mfma)
-            scores_block_mfma<DH>(reinterpret_cast<const uint16_t*>(sQ2), T2,
-                                  [&](int i) { return reinterpret_cast<const uint16_t*>(grow(i)); },
-                                  sS, SP2, scale, reinterpret_cast<uint32_t*>(&sScal[2]),
-                                  (rows + 31) / 32);
-        else
-            for (int idx = threadIdx.x; idx < rows * T2; idx += kThreads)
-                sS[(idx / T2) * SP2 + idx % T2] =
-                    canon_dot<DT, DH>(sQ2 + (idx / T2) * DH, grow(idx % T2), scale);
-        __syncthreads();
-        const float ds2 = use_mfma ? kDeltaRel * __uint_as_float((uint32_t)sScal[2]) * scale * 1.01f : 0.0f;
-        for (int r0 = 0; r0 < rows; r0 += kBlk) {
-            const int brows = rows - r0 < kBlk ? rows - r0 : kBlk;
-            dispatch_jj(T2, [&](auto jt) {
-                constexpr int JJ = decltype(jt)::value;
-                rowgroup_requests<JJ>(r0, brows, T2, sS + r0 * SP2, SP2, A.Kgr, ds2, sQn, vis2,
-                                      sPk, sFirst, sBits, BW, sAmb, &sScal[4]);
-            });
-        }
-        __syncthreads();
-        const int namb = sScal[4];
-        if (namb > 0) {
-            dispatch_j(T2, [&](auto jt) {
-                constexpr int J = decltype(jt)::value;
-                for (int a = w; a < namb; a += kWaves) {
-                    const int t = sAmb[a];
-                    float v[J];
-#pragma unroll
-                    for (int j = 0; j < J; ++j) {
-                        const int i = l + 64 * j;
-                        v[j] = (i < T2 && sThr[i / M] <= t) ? sS[t * SP2 + i] : -INFINITY;
-                    }
-                    row_request<J>(t, v, A.Kgr, ds2 * sQn[t], [&](int i) { return canonG2(t, i); },
-                                   sPk, sFirst, sBits, BW, &amb2);
-                }
-            });
-        }
-        __syncthreads();
-        if (w == 0) {
-            const float dpool2 = ds2 * qnmax;
-            int cnt = 0;
-            dispatch_j(T2, [&](auto jt) {
-                constexpr int J = decltype(jt)::value;
+        x = wsum(x);
+        if (l == 0) sQn[r] = sqrtf(x);
+    }
+    auto grow = [&](int i) -> const T* {
+        return gkb + ((int64_t)sSel[i / M] * M + (i % M)) * DH;
+    };
+    auto canonG2 = [&](int t, int i) { return canon_dot<DT, DH>(qg + t * A.q_ss, grow(i), scale); };
+    auto vis2 = [&](int t, int i) { return sThr[i / M] <= t; };
+    if (use_mfma)
+        scores_block_mfma<DH, kWaves2>(reinterpret_cast<const uint16_t*>(sQ2), T2,
+                                       [&](int i) { return reinterpret_cast<const uint16_t*>(grow(i)); },
+                                       sS, SP2, scale, reinterpret_cast<uint32_t*>(&sScal[2]),
+                                       (rows + 31) / 32);
+    else
+        for (int idx = threadIdx.x; idx < rows * T2; idx += kThreads2)
+            sS[(idx / T2) * SP2 + idx % T2] =
+                canon_dot<DT, DH>(sQ2 + (idx / T2) * DH, grow(idx % T2), scale);
+    __syncthreads();
+    float qnmax = 0.0f;
+    {
+        float x = 0.0f;
+        if (l < rows) x = sQn[l];
+        qnmax = wmax(x);
+    }
+    const float ds2 = use_mfma ? kDeltaRel * __uint_as_float((uint32_t)sScal[2]) * scale * 1.01f : 0.0f;
+    // four waves x four rows per pass
+    for (int r0 = 0; r0 < rows; r0 += 4 * kWaves2) {
+        const int brows = rows - r0 < 4 * kWaves2 ? rows - r0 : 4 * kWaves2;
+        dispatch_jj(T2, [&](auto jt) {
+            constexpr int JJ = decltype(jt)::value;
+            rowgroup_requests<JJ>(r0, brows, T2, sS + r0 * SP2, SP2, A.Kgr, ds2, sQn, vis2,
+                                  sPk, sFirst, sBits, BW, sAmb, &sScal[4]);
+        });
+    }
+    __syncthreads();
+    const int namb = sScal[4];
+    if (namb > 0) {
+        dispatch_j(T2, [&](auto jt) {
+            constexpr int J = decltype(jt)::value;
+            for (int a = w; a < namb; a += kWaves2) {
+                const int t = sAmb[a];
                 float v[J];
 #pragma unroll
                 for (int j = 0; j < J; ++j) {
                     const int i = l + 64 * j;
-                    v[j] = (i < T2 && sFirst[i] < kNoRow) ? okey_inv(sPk[i]) : -INFINITY;
+                    v[j] = (i < T2 && sThr[i / M] <= t) ? sS[t * SP2 + i] : -INFINITY;
                 }
-                auto canon_pool2 = [&](int i) { return pooled_exact(i, rows, sBits, BW, canonG2); };
-                const uint32_t op = select_certified<J>(v, A.Kg, dpool2, canon_pool2, &amb2p);
-                int base = 0;
+                row_request<J>(t, v, A.Kgr, ds2 * sQn[t], [&](int i) { return canonG2(t, i); },
+                               sPk, sFirst, sBits, BW, &amb2);
+            }
+        });
+    }
+    __syncthreads();
+    if (w == 0) {
+        const float dpool2 = ds2 * qnmax;
+        int cnt = 0;
+        dispatch_j(T2, [&](auto jt) {
+            constexpr int J = decltype(jt)::value;
+            float v[J];
 #pragma unroll
-                for (int j = 0; j < J; ++j) {
-                    const bool m = (op >> j) & 1u;
-                    const uint64_t bal = __ballot(m);
-                    if (m) {
-                        const int i = l + 64 * j;
-                        const int pos = base + lanes_below(bal);
-                        if (pos < Kgw) {
-                            out_og[pos] = sSel[i / M] * M + (i % M);
-                            out_ot[pos] = sFirst[i];
-                        }
+            for (int j = 0; j < J; ++j) {
+                const int i = l + 64 * j;
+                v[j] = (i < T2 && sFirst[i] < kNoRow) ? okey_inv(sPk[i]) : -INFINITY;
+            }
+            auto canon_pool2 = [&](int i) { return pooled_exact(i, rows, sBits, BW, canonG2); };
+            const uint32_t op = select_certified<J>(v, A.Kg, dpool2, canon_pool2, &amb2p);
+            int base = 0;
+#pragma unroll
+            for (int j = 0; j < J; ++j) {
+                const bool m = (op >> j) & 1u;
+                const uint64_t bal = __ballot(m);
+                if (m) {
+                    const int i = l + 64 * j;
+                    const int pos = base + lanes_below(bal);
+                    if (pos < Kgw) {
+                        out_og[pos] = sSel[i / M] * M + (i % M);
+                        out_ot[pos] = sFirst[i];
                     }
-                    base += __popcll(bal);
                 }
-                cnt = base;
-            });
-            for (int i = cnt + l; i < Kgw; i += kWave) out_og[i] = out_ot[i] = -1;
-            if (l == 0) A.n_open[o] = cnt;
-        }
+                base += __popcll(bal);
+            }
+            cnt = base;
+        });
+        for (int i = cnt + l; i < Kgw; i += kWave) out_og[i] = out_ot[i] = -1;
+        if (l == 0) A.n_open[o] = cnt;
     }
     if (A.stats && l == 0) {
-        if (amb1) atomicAdd(&A.stats[0], amb1);
-        if (amb1p) atomicAdd(&A.stats[1], amb1p);
         if (amb2) atomicAdd(&A.stats[2], amb2);
         if (amb2p) atomicAdd(&A.stats[3], amb2p);
     }
 }
 
 template <int DT, int DH>
-int launch_route(const RouteArgs& a, size_t lds, hipStream_t st) {
-    auto kern = route_prefill_kernel<DT, DH>;
+int launch_route(const RouteArgs& a, size_t lds1, size_t lds2, hipStream_t st) {
+    auto k1 = route_stage1_kernel<DT, DH>;
+    auto k2 = route_stage2_kernel<DT, DH>;
     static bool attr_done = false;
     if (!attr_done) {
-        if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
+        if (hipFuncSetAttribute((const void*)k1, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                163840) != hipSuccess ||
+            hipFuncSetAttribute((const void*)k2, hipFuncAttributeMaxDynamicSharedMemorySize,
                                 163840) != hipSuccess) {
             set_error("hga_route_prefill: cannot raise the LDS limit");
             return HGA_ERR_LAUNCH;
@@ -780,8 +841,11 @@ int launch_route(const RouteArgs& a, size_t lds, hipStream_t st) {
         attr_done = true;
     }
     const unsigned grid = (unsigned)(a.B * a.H * a.N);
-    kern<<<dim3(grid), dim3(kThreads), lds, st>>>(a);
-    return launch_status("hga_route_prefill");
+    k1<<<dim3(grid), dim3(kThreads), lds1, st>>>(a);
+    int rc = launch_status("hga_route_prefill (stage 1)");
+    if (rc) return rc;
+    k2<<<dim3(grid), dim3(kThreads2), lds2, st>>>(a);
+    return launch_status("hga_route_prefill (stage 2)");
 }
 
 }  // namespace
@@ -828,20 +892,25 @@ extern "C" int hga_route_prefill(const hga_config* cfg, int32_t S, const void* q
     auto odd_above = [](int x) { return (x + 1) | 1; };   // smallest odd stride > x
     a.SP = odd_above(Pmax);
     a.SP2 = odd_above(T2max);
-    // stage 1: [32][SP] scores; stage 2: [64][SP2] scores followed by the 64 query rows
-    const int D0 = cfg->head_dim;
-    const int esz0 = cfg->dtype == HGA_DTYPE_BF16 ? 2 : 4;
-    const int s2sz = (kRows * a.SP2 + 3) / 4 * 4 + kRows * D0 * esz0 / 4;
-    a.SSZ = ((kBlk * a.SP > s2sz ? kBlk * a.SP : s2sz) + 3) / 4 * 4;
-    a.SPP = (Pmax > T2max ? Pmax : T2max) + 1;
-    a.BW = (a.SPP + 31) / 32;
     const int D = cfg->head_dim;
     const size_t esz = cfg->dtype == HGA_DTYPE_BF16 ? 2 : 4;
-    const size_t lds = sizeof(float) * (size_t)a.SSZ + esz * kBlk * D + sizeof(float) * kRows +
-                       2 * sizeof(int) * (size_t)a.SPP + sizeof(uint32_t) * (size_t)kRows * a.BW +
-                       sizeof(int) * (2 * kMaxSel + 8 + kRows);
-    HGA_REQUIRE(lds <= 163840, HGA_ERR_UNSUPPORTED,
-                "hga_route_prefill: %zu bytes of LDS needed (pool %d, head_dim %d)", lds, Pmax, D);
+    // stage 1: [32][SP] scores, the 32 query rows of a block, pooled state over the pool
+    a.SSZ = (kBlk * a.SP + 3) / 4 * 4;
+    a.SPP = Pmax + 1;
+    a.BW = (a.SPP + 31) / 32;
+    const size_t lds1 = sizeof(float) * (size_t)a.SSZ + esz * kBlk * D + sizeof(float) * kRows +
+                        2 * sizeof(int) * (size_t)a.SPP + sizeof(uint32_t) * (size_t)kRows * a.BW +
+                        sizeof(int) * (2 * kMaxSel + 8 + kRows);
+    // stage 2: [64][SP2] scores, the 64 query rows, pooled state over the group candidates
+    a.SPP2 = T2max + 1;
+    a.BW2 = (a.SPP2 + 31) / 32;
+    const size_t lds2 = sizeof(float) * (size_t)((kRows * a.SP2 + 3) / 4 * 4) + esz * kRows * D +
+                        sizeof(float) * kRows + 2 * sizeof(int) * (size_t)a.SPP2 +
+                        sizeof(uint32_t) * (size_t)kRows * a.BW2 +
+                        sizeof(int) * (2 * kMaxSel + 8 + kRows);
+    HGA_REQUIRE(lds1 <= 163840 && lds2 <= 163840, HGA_ERR_UNSUPPORTED,
+                "hga_route_prefill: %zu / %zu bytes of LDS needed (pool %d, head_dim %d)", lds1,
+                lds2, Pmax, D);
     {
         const int64_t ve = cfg->dtype == HGA_DTYPE_BF16 ? 8 : 4;   // elements per 16 bytes
         const uintptr_t al = (uintptr_t)chunk_k | (uintptr_t)group_k | (uintptr_t)q;
@@ -850,7 +919,7 @@ extern "C" int hga_route_prefill(const hga_config* cfg, int32_t S, const void* q
     }
     hipStream_t st = (hipStream_t)stream;
 #define HGA_ROUTE_CASE(DTV, DHV) \
-    if (cfg->dtype == DTV && D == DHV) return launch_route<DTV, DHV>(a, lds, st);
+    if (cfg->dtype == DTV && D == DHV) return launch_route<DTV, DHV>(a, lds1, lds2, st);
     HGA_ROUTE_CASE(HGA_DTYPE_BF16, 128)
     HGA_ROUTE_CASE(HGA_DTYPE_BF16, 64)
     HGA_ROUTE_CASE(HGA_DTYPE_BF16, 32)
