@@ -354,53 +354,58 @@ __device__ __forceinline__ float z_upper_fast(float p) {
     return lower ? -z : z;
 }
 
+// Row statistics gathered while loading: nv valid candidates, sum and sum of squares of their
+// values, smallest and largest key (row-reduced).
+struct RowStats {
+    int nv;
+    float s1, s2;
+    uint32_t kmn, kmx;
+};
+
 template <int JJ>
-__device__ uint32_t rowgroup_topk(const uint32_t (&kv)[JJ], int k) {
+__device__ uint32_t rowgroup_topk(const uint32_t (&kv)[JJ], int k, const RowStats& rs) {
     const int l = lane_id(), seg = l & 15;
-    const int nv = r16_count_ge<JJ>(kv, 1u);
-    float s1 = 0.0f, s2 = 0.0f;
-    uint32_t kmn = 0xffffffffu, kmx = 0u;
-#pragma unroll
-    for (int i = 0; i < JJ; ++i)
-        if (kv[i] != 0u) {
-            const float x = okey_inv(kv[i]);
-            s1 += x;
-            s2 = fmaf(x, x, s2);
-            kmn = min(kmn, kv[i]);
-            kmx = max(kmx, kv[i]);
-        }
-    s1 = r16_fsum(s1);
-    s2 = r16_fsum(s2);
-    kmn = r16_umin(kmn);
-    kmx = r16_umax(kmx);
-    // state per row: threshold vsep (members: key >= vsep, or > vsep plus ties when tie)
+    const int nv = rs.nv;
+    // state per row: threshold vsep (members: key >= vsep, or > vsep plus ties when tie).
+    // Bracket [lo, hi) with clo = count(>= lo) > k > chi = count(>= hi); hi starts one past
+    // the largest key (count 0), so ties at the maximum end in the tie path like any other.
     bool done = nv <= k, tie = false;
-    uint32_t vsep = 1u, lo = kmn, hi = kmx;
-    int clo = nv;
-    int chi = r16_count_ge<JJ>(kv, kmx);
-    if (!done && chi >= k) {
-        vsep = kmx;
-        tie = true;
-        done = true;
+    uint32_t vsep = 1u, lo = rs.kmn;
+    uint32_t hi = rs.kmx == 0xffffffffu ? rs.kmx : rs.kmx + 1u;
+    int clo = nv, chi = 0;
+    if (__ballot(rs.kmx == 0xffffffffu) != 0) {   // degenerate top key: count it exactly
+        const int c = r16_count_ge<JJ>(kv, hi);
+        if (rs.kmx == 0xffffffffu) chi = c;
+        if (!done && rs.kmx == 0xffffffffu && c >= k) {
+            vsep = hi;
+            tie = true;
+            done = true;
+        }
     }
+    float lf = okey_inv(lo), hf = okey_inv(hi);
     float guess = 0.0f;
     {
         const float rn = __builtin_amdgcn_rcpf((float)(nv > 0 ? nv : 1));
-        const float mu = s1 * rn;
-        const float sd = __builtin_sqrtf(fmaxf(s2 * rn - mu * mu, 0.0f));
+        const float mu = rs.s1 * rn;
+        const float sd = __builtin_sqrtf(fmaxf(rs.s2 * rn - mu * mu, 0.0f));
         guess = mu + z_upper_fast((k + 0.5f) * rn) * sd;
     }
     for (int it = 0; __ballot(!done) != 0; ++it) {
         uint32_t mid = lo + (hi - lo) / 2u;
+        float midf = 0.0f;
+        bool interp = false;
         if (it < 8) {
-            const float lf = okey_inv(lo), hf = okey_inv(hi), span = hf - lf;
+            const float span = hf - lf;
             // the interpolated probe only steers the search: approximate reciprocal is enough
             float x = it == 0 ? guess
                               : lf + span * (float)(clo - k) * __builtin_amdgcn_rcpf((float)(clo - chi));
             x = fminf(fmaxf(x, lf + span * 0.0625f), hf - span * 0.0625f);
             const uint32_t xm = okey(x);
-            mid = (x == x && span < INFINITY && xm > lo && xm < hi) ? xm : mid;
+            interp = x == x && span < INFINITY && xm > lo && xm < hi;
+            mid = interp ? xm : mid;
+            midf = x;
         }
+        if (!interp) midf = okey_inv(mid);
         const int c = r16_count_ge<JJ>(kv, mid);
         if (!done) {
             if (c == k) {
@@ -410,9 +415,11 @@ __device__ uint32_t rowgroup_topk(const uint32_t (&kv)[JJ], int k) {
                 if (c > k) {
                     lo = mid;
                     clo = c;
+                    lf = midf;
                 } else {
                     hi = mid;
                     chi = c;
+                    hf = midf;
                 }
                 if (hi - lo <= 1u) {
                     vsep = lo;
@@ -455,13 +462,25 @@ __device__ void rowgroup_requests(int r0, int brows, int ncand, const float* sS,
     const int rr = 4 * w + (l >> 4), t = r0 + rr;
     const bool act = rr < brows;
     uint32_t kv[JJ];
+    RowStats rs{0, 0.0f, 0.0f, 0xffffffffu, 0u};
 #pragma unroll
     for (int i = 0; i < JJ; ++i) {
         const int c = seg + 16 * i;
-        const float x = (act && c < ncand && vis(t, c)) ? sS[rr * stride + c] : -INFINITY;
-        kv[i] = x == -INFINITY ? 0u : okey(x);
+        const bool valid = act && c < ncand && vis(t, c);
+        const float x = valid ? sS[rr * stride + c] : 0.0f;
+        kv[i] = valid ? okey(x) : 0u;
+        rs.nv += valid ? 1 : 0;
+        rs.s1 += x;
+        rs.s2 = fmaf(x, x, rs.s2);
+        rs.kmn = valid ? min(rs.kmn, kv[i]) : rs.kmn;
+        rs.kmx = max(rs.kmx, kv[i]);
     }
-    const uint32_t bits = rowgroup_topk<JJ>(kv, k);
+    rs.nv = r16_sum(rs.nv);
+    rs.s1 = r16_fsum(rs.s1);
+    rs.s2 = r16_fsum(rs.s2);
+    rs.kmn = r16_umin(rs.kmn);
+    rs.kmx = r16_umax(rs.kmx);
+    const uint32_t bits = rowgroup_topk<JJ>(kv, k, rs);
     // certification: k-th and (k+1)-th values at least 2*delta apart
     bool amb = false;
     if (dsc > 0.0f) {
@@ -484,13 +503,12 @@ __device__ void rowgroup_requests(int r0, int brows, int ncand, const float* sS,
         return;
     }
     if (!act) return;
-#pragma unroll
-    for (int i = 0; i < JJ; ++i)
-        if ((bits >> i) & 1u) {
-            const int c = seg + 16 * i;
-            atomicMax(&sPk[c], kv[i]);
-            atomicMin(&sFirst[c], t);
-        }
+    // members only (a lane holds about k/16 of them)
+    for (uint32_t mb = bits; mb != 0u; mb &= mb - 1u) {
+        const int c = seg + 16 * __builtin_ctz(mb);
+        atomicMax(&sPk[c], okey(sS[rr * stride + c]));
+        atomicMin(&sFirst[c], t);
+    }
     // request bitmap of the row: candidate c -> word c / 32, bit c % 32
     uint32_t word = 0;
 #pragma unroll
