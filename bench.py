@@ -324,7 +324,8 @@ def main():
     route_gbs = g["route_bytes"] / (t_route * 1e-3) / 1e9
     traffic = _measured_traffic()
     if t_route >= t_attn:
-        roofline = {"kernel": "route_prefill_kernel<bf16,128>", "bound": "hbm",
+        roofline = {"kernel": "route_stage1_kernel + route_stage2_kernel <bf16,128>",
+                    "bound": "hbm",
                     "achieved": route_gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                     "frac": route_gbs / HBM_PEAK_GBS, "traffic": traffic,
                     "algorithmic_bytes": g["route_bytes"],

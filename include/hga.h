@@ -133,8 +133,9 @@ int hga_attend_prefill(const hga_config* cfg, int32_t S, const void* q, int64_t 
                        int64_t o_sb, int64_t o_sh, int64_t o_ss, void* workspace,
                        int64_t workspace_bytes, void* stream);
 
-/* Device scratch bytes hga_attend_prefill needs for a block of S tokens (a transposed copy of
- * V for bf16 head_dim 64/128 with group and chunk sizes that are multiples of 16; 0 otherwise).
+/* Device scratch bytes hga_attend_prefill needs for a block of S tokens (16-key blocked copies
+ * of K and V, 2*B*KVH*Dh*roundup(S,64) bf16 elements, for bf16 head_dim 64/128 with group and
+ * chunk sizes that are multiples of 16; 0 otherwise).
  * The buffer must be 16-byte aligned and is only used during the call's kernels (stream
  * ordered).  No counterpart in the reference, whose attend materialises K/V instead. */
 int32_t hga_attend_prefill_workspace(const hga_config* cfg, int32_t S, int64_t* bytes);
