@@ -1,20 +1,22 @@
 // Two-level prefill router (vectorized.py:242-396) for gfx950.
 //
-// One 512-thread workgroup per (batch, query head, query chunk n); at most ~80 KB of LDS so that
-// two workgroups share a CU.  Nothing is materialised in HBM except the routing lists.
+// Stage 1: one 512-thread workgroup per (batch, query head, query chunk n), at most ~80 KB of LDS
+// so that two share a CU; stage 2: one 256-thread workgroup per chunk.  Nothing is materialised
+// in HBM except the routing lists.
 //
-//   1. Stage 1, per 32-row block of the chunk: the block's query rows go to LDS; scores of the
-//      rows against every candidate of the routing pool P(n) = [f_hi, l_lo) are produced into LDS
-//      by bf16 MFMA (v_mfma_f32_32x32x16_bf16, fp32 accumulate), or by the canonical fp32 FMA
-//      chain for fp32 inputs / HGA_ROUTE_CANONICAL.
-//   2. Each wave selects, for one query row at a time, the row's top-min(Kc,|P|) candidates:
-//      an interpolation search for a separating threshold (seeded from the row's mean and
-//      standard deviation, secant steps on the ballot counts, then key-space bisection), ties to
-//      the lower chunk id.  MFMA scores differ from the canonical chain by at most
-//      delta = 2^-16 * |q| * |k| * scale (both are fp32 accumulations of the same exact bf16
-//      products); when the k-th and (k+1)-th scores are closer than 2*delta the candidates
-//      inside the band are re-scored with the canonical chain and the remaining slots filled
-//      exactly, so selections equal the canonical oracle's.
+//   1. Stage 1, per 32-row block of the chunk: scores of the block's query rows against every
+//      candidate of the routing pool P(n) = [f_hi, l_lo) are produced into LDS by bf16 MFMA
+//      (S^T = K * Q^T, v_mfma_f32_32x32x16_bf16, fp32 accumulate, both operands straight from
+//      global memory), or by the canonical fp32 FMA chain for fp32 inputs / HGA_ROUTE_CANONICAL.
+//   2. Per-row top-min(Kc,|P|) by row groups: 16 lanes own one row (four rows per wave), hold
+//      its scores in registers as order-preserving keys and run an interpolation search for a
+//      separating threshold (seeded from the row's mean and standard deviation, secant steps on
+//      DPP-reduced counts, then key-space bisection), ties to the lower chunk id.  MFMA scores
+//      differ from the canonical chain by at most delta = 2^-16 * |q| * |k| * scale (both are
+//      fp32 accumulations of the same exact bf16 products); a row whose k-th and (k+1)-th scores
+//      are closer than 2*delta goes to the canonical path: the candidates inside the band are
+//      re-scored with the canonical chain and the remaining slots filled exactly, so selections
+//      equal the canonical oracle's.
 //   3. Requests are pooled per chunk (max score, first requesting row) with LDS atomics; one
 //      wave takes the top-Kc pooled chunks (same certification; ambiguous pooled maxima are
 //      recomputed canonically over the requesting rows), forces in chunk n-1 when it lies in the
@@ -22,7 +24,6 @@
 //   4. Stage 2 repeats 1-3 for all rows at once over the M groups of each selected chunk, a
 //      group being visible to a row from its parent's first row on; top-Kgr requests per row,
 //      top-Kg opened.
-// Wave-wide reductions use DPP row operations and lane reads (no LDS round trips).
 #include "hga_common.h"
 #include "hga_select.h"
 
@@ -50,7 +51,7 @@ struct RouteArgs {
     int32_t *sel_chunk, *sel_thr, *n_sel, *open_grp, *open_thr, *n_open;
     int32_t* stats;
     int B, H, KVH, S, N, C, M, kf, kl, Kc, Kg, Kgr;
-    int SP, SP2, SSZ, SPP, BW, SPP2, BW2, canonical;
+    int SP, SP2, SSZ, SPP, BW, SPP2, BW2, VT2, canonical;
     float scale;
 };
 
@@ -117,64 +118,98 @@ __device__ __forceinline__ float canon_dot(const typename Elem<DT>::T* q,
 
 __device__ __forceinline__ bf16x8 as_bf16x8(uint4 u) { return __builtin_bit_cast(bf16x8, u); }
 
+// Sum of squares of the 8 bf16 values of a 16-byte word (packed bf16 dot products).  Only used
+// for the certification bound, which carries a 1% margin for its rounding.
 __device__ __forceinline__ float sumsq_bf16x8(uint4 u) {
-    float s = 0.0f;
+    typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
     const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+    float s = 0.0f;
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-        const float a = __uint_as_float(w[e] << 16), b = __uint_as_float(w[e] & 0xffff0000u);
-        s = fmaf(a, a, s);
-        s = fmaf(b, b, s);
-    }
+    for (int e = 0; e < 4; ++e)
+        s = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, w[e]),
+                                            __builtin_bit_cast(bf16x2, w[e]), s, false);
     return s;
 }
 
-// bf16 MFMA scores (scaled) of one 32-row block (query rows in sQ, stride DH) against all
-// candidates, written to sRows[row * stride + c]; the largest candidate norm is folded into
-// *knmax (uint bits of a non-negative float) when knmax is not NULL.  Wave w handles candidate
-// tiles w, w+8, ... of 32 candidates.
-template <int DH, int NW = kWaves, class RowPtr>
-__device__ void scores_block_mfma(const uint16_t* sQ, int ncand, RowPtr rowptr, float* sRows,
-                                  int stride, float scale, uint32_t* knmax, int nrb = 1) {
+// bf16 MFMA scores (scaled; -0 folded into +0) of the query rows [32*rb, 32*rb + 32) (rb < nrb)
+// against all candidates, written row-major to sRows[row * stride + c].  Computed as
+// S^T = K * Q^T with v_mfma_f32_32x32x16_bf16 (candidates on the M side, query rows on the N
+// side), so a lane's 16 results are four runs of four consecutive candidates of one query row
+// and are written with 16-byte stores at constant offsets (stride: a multiple of 4 covering
+// every candidate tile).  Both operands are read from global memory: candidate rows through
+// rowptr, query row t at qg + t*q_ss (rows >= `rows` read as zero).  Wave w takes the jobs
+// (row block, candidate tile) w, w+NW, ..., row block fastest.  The wave holding tile 0 of a row
+// block writes the block's query norms to sQn[t]; with knmax the largest candidate norm (row
+// block 0's tiles) is folded into *knmax (uint bits of a non-negative float).  VIS: candidate c
+// of row t gets -inf unless vthr[c] <= t.
+template <int DH, int NW, bool VIS, class RowPtr>
+__device__ void scores_st(const uint16_t* qg, int64_t q_ss, int rows, int nrb, int ncand,
+                          RowPtr rowptr, const int* vthr, float* sRows, int stride, float scale,
+                          uint32_t* knmax, float* sQn) {
     constexpr int KS = DH / 16;
-    const int w = threadIdx.x / kWave, l = lane_id();
+    const int w = threadIdx.x / kWave, l = lane_id(), j = l % 32, hh = l / 32;
     const int ntile = (ncand + 31) / 32;
-    // jobs (row block, candidate tile), row block fastest
+    int cur = -1;
+    bf16x8 b[KS];
     for (int job = w; job < nrb * ntile; job += NW) {
-    const int rb = job % nrb, ct = job / nrb;
-    bf16x8 a[KS];
+        const int rb = job % nrb, ct = job / nrb;
+        const int t = 32 * rb + j;
+        if (rb != cur) {            // wave-uniform: query operand of the row block
+            cur = rb;
+            uint4 u[KS];
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks)
-        a[ks] = as_bf16x8(*reinterpret_cast<const uint4*>(sQ + (32 * rb + l % 32) * DH + ks * 16 + 8 * (l / 32)));
-    {
-        const int c = ct * 32 + l % 32;
+            for (int ks = 0; ks < KS; ++ks) {
+                u[ks] = make_uint4(0u, 0u, 0u, 0u);
+                if (t < rows)
+                    u[ks] = *reinterpret_cast<const uint4*>(qg + (int64_t)t * q_ss + ks * 16 + 8 * hh);
+            }
+            if (ct == 0) {
+                float x = 0.0f;
+#pragma unroll
+                for (int ks = 0; ks < KS; ++ks) x += sumsq_bf16x8(u[ks]);
+                x += __shfl_xor(x, 32, kWave);
+                if (hh == 0) sQn[t] = __builtin_sqrtf(x);
+            }
+#pragma unroll
+            for (int ks = 0; ks < KS; ++ks) b[ks] = as_bf16x8(u[ks]);
+        }
+        const int c = ct * 32 + j;
         const bool cv = c < ncand;
-        const uint16_t* kp = cv ? rowptr(c) : nullptr;
-        uint4 u[KS];
+        const uint16_t* kp = rowptr(cv ? c : 0);
+        uint4 a[KS];
 #pragma unroll
         for (int ks = 0; ks < KS; ++ks) {
-            u[ks] = make_uint4(0u, 0u, 0u, 0u);
-            if (cv) u[ks] = *reinterpret_cast<const uint4*>(kp + ks * 16 + 8 * (l / 32));
+            a[ks] = make_uint4(0u, 0u, 0u, 0u);
+            if (cv) a[ks] = *reinterpret_cast<const uint4*>(kp + ks * 16 + 8 * hh);
         }
         floatx16 acc = {};
 #pragma unroll
         for (int ks = 0; ks < KS; ++ks)
-            acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[ks], as_bf16x8(u[ks]), acc, 0, 0, 0);
-        if (knmax && rb == 0) {   // largest candidate norm (once per candidate tile)
+            acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(a[ks]), b[ks], acc, 0, 0, 0);
+        if (knmax && rb == 0) {
             float nsq = 0.0f;
 #pragma unroll
-            for (int ks = 0; ks < KS; ++ks) nsq += sumsq_bf16x8(u[ks]);
+            for (int ks = 0; ks < KS; ++ks) nsq += sumsq_bf16x8(a[ks]);
             nsq += __shfl_xor(nsq, 32, kWave);
-            if (cv && l < 32) atomicMax(knmax, __float_as_uint(sqrtf(nsq)));
+            if (cv && hh == 0) atomicMax(knmax, __float_as_uint(__builtin_sqrtf(nsq)));
         }
-        if (cv) {
+        float* dst = sRows + t * stride + ct * 32 + 4 * hh;
 #pragma unroll
-            for (int i = 0; i < 16; ++i) {
-                const int row = 32 * rb + 8 * (i / 4) + 4 * (l / 32) + (i % 4);
-                sRows[row * stride + c] = acc[i] * scale;
+        for (int g = 0; g < 4; ++g) {
+            float4 o;
+            o.x = fmaf(acc[4 * g + 0], scale, 0.0f);
+            o.y = fmaf(acc[4 * g + 1], scale, 0.0f);
+            o.z = fmaf(acc[4 * g + 2], scale, 0.0f);
+            o.w = fmaf(acc[4 * g + 3], scale, 0.0f);
+            if constexpr (VIS) {
+                const int4 th = *reinterpret_cast<const int4*>(vthr + ct * 32 + 8 * g + 4 * hh);
+                o.x = th.x <= t ? o.x : -INFINITY;
+                o.y = th.y <= t ? o.y : -INFINITY;
+                o.z = th.z <= t ? o.z : -INFINITY;
+                o.w = th.w <= t ? o.w : -INFINITY;
             }
+            *reinterpret_cast<float4*>(dst + 8 * g) = o;
         }
-    }
     }
 }
 
@@ -281,24 +316,13 @@ __device__ int pooled_select(int ncand, int k, int rows, const uint32_t* sBits, 
     return base;
 }
 
-// Query rows [r0, r0+32) of the chunk into sQ (stride DH), zero beyond `rows`.
-template <class T, int DH>
-__device__ __forceinline__ void load_block(T* sQ, const T* qg, int64_t q_ss, int r0, int rows) {
-    constexpr int VE = 16 / (int)sizeof(T);
-    for (int idx = threadIdx.x; idx < kBlk * (DH / VE); idx += kThreads) {
-        const int r = idx / (DH / VE), d = (idx % (DH / VE)) * VE;
-        uint4 u = make_uint4(0u, 0u, 0u, 0u);
-        if (r0 + r < rows) u = *reinterpret_cast<const uint4*>(qg + (int64_t)(r0 + r) * q_ss + d);
-        *reinterpret_cast<uint4*>(sQ + r * DH + d) = u;
-    }
-}
-
 // ------------------------------------------------------------------------------------------
 // row-group selection: one query row per 16-lane DPP row, four rows per wave in lockstep
 // ------------------------------------------------------------------------------------------
-// Lane `seg` (= lane % 16) of a row holds candidates seg + 16*i (i < JJ) in registers.  The
-// per-row count of keys >= x is a 16-lane DPP reduction, so a search step costs 2*JJ + 8 VALU
-// operations for four rows at once.
+// Lane `seg` (= lane % 16) of a row holds JJ candidates in registers: with W = min(JJ, 4),
+// register W*g + e holds candidate 16*W*g + W*seg + e (g < JJ/W, e < W), so that a lane reads
+// W consecutive scores at once.  The per-row count of keys >= x is a 16-lane DPP reduction, so
+// a search step costs 2*JJ + 8 VALU operations for four rows at once.
 template <class Op>
 __device__ __forceinline__ int row16_reduce(int x, Op op) {
     x = op(x, dpp<0xB1>(x));    // quad_perm [1,0,3,2]
@@ -311,16 +335,6 @@ __device__ __forceinline__ int r16_sum(int x) { return row16_reduce(x, [](int a,
 __device__ __forceinline__ float r16_fsum(float x) {
     return __int_as_float(row16_reduce(__float_as_int(x), [](int a, int b) {
         return __float_as_int(__int_as_float(a) + __int_as_float(b));
-    }));
-}
-[[maybe_unused]] __device__ __forceinline__ float r16_fmin(float x) {
-    return __int_as_float(row16_reduce(__float_as_int(x), [](int a, int b) {
-        return __float_as_int(fminf(__int_as_float(a), __int_as_float(b)));
-    }));
-}
-[[maybe_unused]] __device__ __forceinline__ float r16_fmax(float x) {
-    return __int_as_float(row16_reduce(__float_as_int(x), [](int a, int b) {
-        return __float_as_int(fmaxf(__int_as_float(a), __int_as_float(b)));
     }));
 }
 __device__ __forceinline__ uint32_t r16_umin(uint32_t x) {
@@ -338,16 +352,20 @@ __device__ __forceinline__ int r16_count_ge(const uint32_t (&kv)[JJ], uint32_t x
     return r16_sum(c);
 }
 
-// Exact top-k of the row's keys (0 = not a candidate; larger key first, equal keys -> lower
-// candidate index seg + 16*i).  Every lane of the wave must call it (DPP reads neighbours).
-// Returns member bits.
-// Upper-tail normal quantile (Abramowitz & Stegun 26.2.23) with hardware log/sqrt: a search
+// Order-preserving key in three operations; differs from okey only for -0, which the score
+// producers never emit (the MFMA epilogue adds +0, canon_dot folds -0).
+__device__ __forceinline__ uint32_t okey_fast(float f) {
+    const uint32_t u = __float_as_uint(f);
+    return u ^ ((uint32_t)((int32_t)u >> 31) | 0x80000000u);
+}
+
+// Upper-tail normal quantile (Abramowitz & Stegun 26.2.23) with hardware log/sqrt/rcp: a search
 // seed only, so approximate transcendental instructions are fine.
 __device__ __forceinline__ float z_upper_fast(float p) {
     p = fminf(fmaxf(p, 1e-6f), 1.0f - 1e-6f);
     const bool lower = p > 0.5f;
     const float pp = lower ? 1.0f - p : p;
-    const float t = __builtin_sqrtf(-2.0f * 0.69314718f * __builtin_amdgcn_logf(pp));
+    const float t = __builtin_amdgcn_sqrtf(-2.0f * 0.69314718f * __builtin_amdgcn_logf(pp));
     const float z = t - (2.515517f + 0.802853f * t + 0.010328f * t * t) *
                             __builtin_amdgcn_rcpf(1.0f + 1.432788f * t + 0.189269f * t * t +
                                                   0.001308f * t * t * t);
@@ -362,8 +380,12 @@ struct RowStats {
     uint32_t kmn, kmx;
 };
 
+// Exact top-k of the row's keys (0 = not a candidate; larger key first, equal keys -> lower
+// candidate index).  Every lane of the wave must call it (DPP reads neighbours).  Returns
+// member bits (bit i <-> register i).
 template <int JJ>
 __device__ uint32_t rowgroup_topk(const uint32_t (&kv)[JJ], int k, const RowStats& rs) {
+    constexpr int W = JJ < 4 ? JJ : 4;
     const int l = lane_id(), seg = l & 15;
     const int nv = rs.nv;
     // state per row: threshold vsep (members: key >= vsep, or > vsep plus ties when tie).
@@ -387,7 +409,7 @@ __device__ uint32_t rowgroup_topk(const uint32_t (&kv)[JJ], int k, const RowStat
     {
         const float rn = __builtin_amdgcn_rcpf((float)(nv > 0 ? nv : 1));
         const float mu = rs.s1 * rn;
-        const float sd = __builtin_sqrtf(fmaxf(rs.s2 * rn - mu * mu, 0.0f));
+        const float sd = __builtin_amdgcn_sqrtf(fmaxf(rs.s2 * rn - mu * mu, 0.0f));
         guess = mu + z_upper_fast((k + 0.5f) * rn) * sd;
     }
     for (int it = 0; __ballot(!done) != 0; ++it) {
@@ -433,49 +455,98 @@ __device__ uint32_t rowgroup_topk(const uint32_t (&kv)[JJ], int k, const RowStat
 #pragma unroll
     for (int i = 0; i < JJ; ++i) bits |= ((tie ? kv[i] > vsep : kv[i] >= vsep) ? 1u : 0u) << i;
     if (__ballot(tie) != 0) {
-        // boundary ties: the lowest candidate indices (i-major, then seg) among key == vsep
+        // boundary ties: the lowest candidate indices among key == vsep.  Candidate order is
+        // (group g, lane seg, e): within a group, lanes below first, then the lane's own e order.
         int r = k - r16_count_ge<JJ>(kv, vsep + 1u);
         const int sh = 16 * (l >> 4);
+        const uint32_t lower = (1u << seg) - 1u;
 #pragma unroll
-        for (int i = 0; i < JJ; ++i) {
-            const bool eq = tie && kv[i] == vsep;
-            const uint32_t m16 = (uint32_t)(__ballot(eq) >> sh) & 0xffffu;
-            const int below = __popc(m16 & ((1u << seg) - 1u));
-            if (eq && below < r) bits |= 1u << i;
-            const int n16 = __popc(m16);
-            r -= n16 < r ? n16 : r;
+        for (int g = 0; g < JJ / W; ++g) {
+            int below = 0, tot = 0;
+#pragma unroll
+            for (int e = 0; e < W; ++e) {
+                const uint32_t m16 =
+                    (uint32_t)(__ballot(tie && kv[W * g + e] == vsep) >> sh) & 0xffffu;
+                below += __popc(m16 & lower);
+                tot += __popc(m16);
+            }
+            int own = 0;
+#pragma unroll
+            for (int e = 0; e < W; ++e) {
+                const bool eq = tie && kv[W * g + e] == vsep;
+                if (eq && below + own < r) bits |= 1u << (W * g + e);
+                own += eq ? 1 : 0;
+            }
+            r -= tot < r ? tot : r;
         }
     }
     return bits;
 }
 
-// Row-group requests of block rows [r0, r0+32): lane -> (row rr = 4w + lane/16, seg); each
-// row's candidate values come from sS[rr * stride + c] (-inf if not visible).  Certified rows
-// raise the pooled key / lower the first row of their members and write their request bitmap;
-// rows whose k-th and (k+1)-th values lie within 2*delta are queued (absolute row) in sAmb for
-// the canonical path.
-template <int JJ, class Vis>
+// Row-group requests of block rows [r0, r0+32): lane -> (row rr = 4w + lane/16, seg); row rr's
+// candidate values are sS[rr * stride + c] for c < ncand (-inf = not visible when VIS; without
+// VIS every candidate is visible).  Certified rows raise the pooled key / lower the first row of
+// their members and set their request bits; rows whose k-th and (k+1)-th values lie within
+// 2*delta are queued (absolute row) in sAmb for the canonical path.
+template <int JJ, bool VIS>
 __device__ void rowgroup_requests(int r0, int brows, int ncand, const float* sS, int stride,
-                                  int k, float dsc, const float* sQn, Vis vis, uint32_t* sPk,
+                                  int k, float dsc, const float* sQn, uint32_t* sPk,
                                   int* sFirst, uint32_t* sBits, int BW, int* sAmb, int* sAmbN) {
+    constexpr int W = JJ < 4 ? JJ : 4;
+    constexpr int G = JJ / W;
     const int w = threadIdx.x / kWave, l = lane_id(), seg = l & 15;
     const int rr = 4 * w + (l >> 4), t = r0 + rr;
     const bool act = rr < brows;
+    const float* rowp = sS + rr * stride;
     uint32_t kv[JJ];
     RowStats rs{0, 0.0f, 0.0f, 0xffffffffu, 0u};
+    int nvl = 0;
 #pragma unroll
-    for (int i = 0; i < JJ; ++i) {
-        const int c = seg + 16 * i;
-        const bool valid = act && c < ncand && vis(t, c);
-        const float x = valid ? sS[rr * stride + c] : 0.0f;
-        kv[i] = valid ? okey(x) : 0u;
-        rs.nv += valid ? 1 : 0;
-        rs.s1 += x;
-        rs.s2 = fmaf(x, x, rs.s2);
-        rs.kmn = valid ? min(rs.kmn, kv[i]) : rs.kmn;
-        rs.kmx = max(rs.kmx, kv[i]);
+    for (int g = 0; g < G; ++g) {
+        const int c0 = 16 * W * g + W * seg;
+        float x[W];
+#pragma unroll
+        for (int e = 0; e < W; ++e) x[e] = 0.0f;
+        if (16 * W * g < ncand) {                    // wave-uniform; rows are 16-byte aligned
+            if constexpr (W == 4) {
+                const float4 v4 = *reinterpret_cast<const float4*>(rowp + c0);
+                x[0] = v4.x; x[1] = v4.y; x[2] = v4.z; x[3] = v4.w;
+            } else if constexpr (W == 2) {
+                const float2 v2 = *reinterpret_cast<const float2*>(rowp + c0);
+                x[0] = v2.x; x[1] = v2.y;
+            } else {
+                x[0] = rowp[c0];
+            }
+        }
+        const bool full = 16 * W * (g + 1) <= ncand;  // wave-uniform
+        if (full && !VIS) {
+#pragma unroll
+            for (int e = 0; e < W; ++e) {
+                kv[W * g + e] = okey_fast(x[e]);
+                rs.s1 += x[e];
+                rs.s2 = fmaf(x[e], x[e], rs.s2);
+                rs.kmn = min(rs.kmn, kv[W * g + e]);
+                rs.kmx = max(rs.kmx, kv[W * g + e]);
+            }
+        } else if (16 * W * g < ncand) {
+#pragma unroll
+            for (int e = 0; e < W; ++e) {
+                const bool valid = (full || c0 + e < ncand) && (!VIS || x[e] != -INFINITY);
+                const float xm = valid ? x[e] : 0.0f;
+                const uint32_t key = valid ? okey_fast(x[e]) : 0u;
+                kv[W * g + e] = key;
+                nvl += valid ? 1 : 0;
+                rs.s1 += xm;
+                rs.s2 = fmaf(xm, xm, rs.s2);
+                rs.kmn = min(rs.kmn, valid ? key : 0xffffffffu);
+                rs.kmx = max(rs.kmx, key);
+            }
+        } else {
+#pragma unroll
+            for (int e = 0; e < W; ++e) kv[W * g + e] = 0u;
+        }
     }
-    rs.nv = r16_sum(rs.nv);
+    rs.nv = act ? (VIS ? r16_sum(nvl) : ncand) : 0;
     rs.s1 = r16_fsum(rs.s1);
     rs.s2 = r16_fsum(rs.s2);
     rs.kmn = r16_umin(rs.kmn);
@@ -503,22 +574,13 @@ __device__ void rowgroup_requests(int r0, int brows, int ncand, const float* sS,
         return;
     }
     if (!act) return;
-    // members only (a lane holds about k/16 of them)
+    // members only (a lane holds about k/16 of them): pooled key, first row, request bit
     for (uint32_t mb = bits; mb != 0u; mb &= mb - 1u) {
-        const int c = seg + 16 * __builtin_ctz(mb);
-        atomicMax(&sPk[c], okey(sS[rr * stride + c]));
+        const int i = __builtin_ctz(mb);
+        const int c = 16 * W * (i / W) + W * seg + (i % W);
+        atomicMax(&sPk[c], okey(rowp[c]));
         atomicMin(&sFirst[c], t);
-    }
-    // request bitmap of the row: candidate c -> word c / 32, bit c % 32
-    uint32_t word = 0;
-#pragma unroll
-    for (int i = 0; i < JJ; ++i) {
-        const uint32_t m16 = (uint32_t)(__ballot((bits >> i) & 1u) >> (16 * (l >> 4))) & 0xffffu;
-        word |= m16 << (16 * (i & 1));
-        if ((i & 1) || i == JJ - 1) {
-            if (seg == 0 && (i >> 1) < BW) sBits[t * BW + (i >> 1)] = word;
-            word = 0;
-        }
+        atomicOr(&sBits[t * BW + c / 32], 1u << (c % 32));
     }
 }
 
@@ -542,9 +604,8 @@ void route_stage1_kernel(RouteArgs A) {
     typedef typename Elem<DT>::T T;
     extern __shared__ __align__(16) unsigned char smem_raw[];
     const int SP = A.SP, BW = A.BW;
-    float* sS = reinterpret_cast<float*>(smem_raw);                 // [32][SP]
-    T* sQ = reinterpret_cast<T*>(sS + A.SSZ);                        // [32][DH]
-    float* sQn = reinterpret_cast<float*>(sQ + kBlk * DH);           // [64]
+    float* sS = reinterpret_cast<float*>(smem_raw);                 // [32][SP] block scores
+    float* sQn = sS + A.SSZ;                                         // [64] query row norms
     uint32_t* sPk = reinterpret_cast<uint32_t*>(sQn + kRows);        // [SPP] pooled key
     int* sFirst = reinterpret_cast<int*>(sPk + A.SPP);               // [SPP]
     uint32_t* sBits = reinterpret_cast<uint32_t*>(sFirst + A.SPP);   // [64][BW]
@@ -587,39 +648,36 @@ void route_stage1_kernel(RouteArgs A) {
     }
     for (int i = threadIdx.x; i < kRows * BW; i += kThreads) sBits[i] = 0u;
     if (threadIdx.x < 8) sScal[threadIdx.x] = 0;
+    __syncthreads();
 
     // ---- stage 1, per 32-row block -----------------------------------------------------------
     for (int r0 = 0; r0 < rows; r0 += kBlk) {
         const int brows = rows - r0 < kBlk ? rows - r0 : kBlk;
-        load_block<T, DH>(sQ, qg, A.q_ss, r0, rows);
-        __syncthreads();
-        for (int r = w; r < kBlk; r += kWaves) {
-            float x = 0.0f;
-            for (int d = l; d < DH; d += kWave) {
-                const float e = Elem<DT>::ld(sQ, r * DH + d);
-                x = fmaf(e, e, x);
+        bool scored = false;
+        if constexpr (DT == HGA_DTYPE_BF16) {
+            if (use_mfma) {
+                scores_st<DH, kWaves, false>(reinterpret_cast<const uint16_t*>(qg + (int64_t)r0 * A.q_ss),
+                                             A.q_ss, brows, 1, P,
+                                             [&](int i) { return reinterpret_cast<const uint16_t*>(crow(i)); },
+                                             nullptr, sS, SP, scale,
+                                             r0 == 0 ? reinterpret_cast<uint32_t*>(&sScal[1]) : nullptr,
+                                             sQn + r0);
+                scored = true;
             }
-            x = wsum(x);
-            if (l == 0 && r0 + r < kRows) sQn[r0 + r] = sqrtf(x);
         }
-        if (use_mfma)
-            scores_block_mfma<DH>(reinterpret_cast<const uint16_t*>(sQ), P,
-                                  [&](int i) { return reinterpret_cast<const uint16_t*>(crow(i)); },
-                                  sS, SP, scale,
-                                  r0 == 0 ? reinterpret_cast<uint32_t*>(&sScal[1]) : nullptr);
-        else
+        if (!scored) {
             for (int idx = threadIdx.x; idx < brows * P; idx += kThreads)
-                sS[(idx / P) * SP + idx % P] = canon_dot<DT, DH>(sQ + (idx / P) * DH, crow(idx % P), scale);
+                sS[(idx / P) * SP + idx % P] = canonG1(r0 + idx / P, idx % P);
+            if (threadIdx.x < kBlk) sQn[r0 + threadIdx.x] = 0.0f;   // no certification
+        }
+        if (threadIdx.x == 0) sScal[4] = 0;
         __syncthreads();
         const float ds1 = use_mfma ? kDeltaRel * __uint_as_float((uint32_t)sScal[1]) * scale * 1.01f : 0.0f;
         const int kreq = A.Kc < P ? A.Kc : P;
-        if (threadIdx.x == 0) sScal[4] = 0;
-        __syncthreads();
         dispatch_jj(P, [&](auto jt) {
             constexpr int JJ = decltype(jt)::value;
-            rowgroup_requests<JJ>(r0, brows, P, sS, SP, kreq, ds1, sQn,
-                                  [](int, int) { return true; }, sPk, sFirst, sBits, BW, sAmb,
-                                  &sScal[4]);
+            rowgroup_requests<JJ, false>(r0, brows, P, sS, SP, kreq, ds1, sQn, sPk, sFirst, sBits,
+                                         BW, sAmb, &sScal[4]);
         });
         __syncthreads();
         // rows the MFMA scores could not certify: canonical re-rank (one row per wave)
@@ -635,9 +693,7 @@ void route_stage1_kernel(RouteArgs A) {
                         const int i = l + 64 * j;
                         v[j] = i < P ? sS[r * SP + i] : -INFINITY;
                     }
-                    const T* qr = sQ + r * DH;
-                    row_request<J>(t, v, kreq, ds1 * sQn[t],
-                                   [&](int i) { return canon_dot<DT, DH>(qr, crow(i), scale); },
+                    row_request<J>(t, v, kreq, ds1 * sQn[t], [&](int i) { return canonG1(t, i); },
                                    sPk, sFirst, sBits, BW, &amb1);
                 }
             });
@@ -692,9 +748,9 @@ void route_stage2_kernel(RouteArgs A) {
     extern __shared__ __align__(16) unsigned char smem_raw[];
     const int SP2 = A.SP2, BW = A.BW2;
     float* sS = reinterpret_cast<float*>(smem_raw);                 // [64][SP2] scores
-    T* sQ2 = reinterpret_cast<T*>(sS + (kRows * SP2 + 3) / 4 * 4);  // [64][DH] query rows
-    float* sQn = reinterpret_cast<float*>(sQ2 + kRows * DH);         // [64]
-    uint32_t* sPk = reinterpret_cast<uint32_t*>(sQn + kRows);        // [SPP2] pooled key
+    float* sQn = sS + kRows * SP2;                                   // [64] query row norms
+    int* sVthr = reinterpret_cast<int*>(sQn + kRows);                // [VT2] candidate -> first row
+    uint32_t* sPk = reinterpret_cast<uint32_t*>(sVthr + A.VT2);      // [SPP2] pooled key
     int* sFirst = reinterpret_cast<int*>(sPk + A.SPP2);              // [SPP2]
     uint32_t* sBits = reinterpret_cast<uint32_t*>(sFirst + A.SPP2);  // [64][BW2]
     int* sSel = reinterpret_cast<int*>(sBits + kRows * BW);          // [kMaxSel]
@@ -735,39 +791,31 @@ void route_stage2_kernel(RouteArgs A) {
     }
     for (int i = threadIdx.x; i < kRows * BW; i += kThreads2) sBits[i] = 0u;
     if (threadIdx.x < 8) sScal[threadIdx.x] = 0;
-    {
-        constexpr int VE = 16 / (int)sizeof(T);
-        for (int idx = threadIdx.x; idx < kRows * (DH / VE); idx += kThreads2) {
-            const int r = idx / (DH / VE), d = (idx % (DH / VE)) * VE;
-            uint4 u = make_uint4(0u, 0u, 0u, 0u);
-            if (r < rows) u = *reinterpret_cast<const uint4*>(qg + (int64_t)r * A.q_ss + d);
-            *reinterpret_cast<uint4*>(sQ2 + r * DH + d) = u;
-        }
-    }
+    for (int i = threadIdx.x; i < A.VT2; i += kThreads2)   // a group is visible from its parent's row
+        sVthr[i] = i < T2 ? A.sel_thr[o * Kcw + i / M] : kNoRow;
     __syncthreads();
-    for (int r = w; r < kRows; r += kWaves2) {       // query row norms (certification bound)
-        float x = 0.0f;
-        for (int d = l; d < DH; d += kWave) {
-            const float e = Elem<DT>::ld(sQ2, r * DH + d);
-            x = fmaf(e, e, x);
-        }
-        x = wsum(x);
-        if (l == 0) sQn[r] = sqrtf(x);
-    }
     auto grow = [&](int i) -> const T* {
         return gkb + ((int64_t)sSel[i / M] * M + (i % M)) * DH;
     };
     auto canonG2 = [&](int t, int i) { return canon_dot<DT, DH>(qg + t * A.q_ss, grow(i), scale); };
-    auto vis2 = [&](int t, int i) { return sThr[i / M] <= t; };
-    if (use_mfma)
-        scores_block_mfma<DH, kWaves2>(reinterpret_cast<const uint16_t*>(sQ2), T2,
-                                       [&](int i) { return reinterpret_cast<const uint16_t*>(grow(i)); },
-                                       sS, SP2, scale, reinterpret_cast<uint32_t*>(&sScal[2]),
-                                       (rows + 31) / 32);
-    else
-        for (int idx = threadIdx.x; idx < rows * T2; idx += kThreads2)
-            sS[(idx / T2) * SP2 + idx % T2] =
-                canon_dot<DT, DH>(sQ2 + (idx / T2) * DH, grow(idx % T2), scale);
+    bool scored = false;
+    if constexpr (DT == HGA_DTYPE_BF16) {
+        if (use_mfma) {
+            scores_st<DH, kWaves2, true>(reinterpret_cast<const uint16_t*>(qg), A.q_ss, rows,
+                                         (rows + 31) / 32, T2,
+                                         [&](int i) { return reinterpret_cast<const uint16_t*>(grow(i)); },
+                                         sVthr, sS, SP2, scale, reinterpret_cast<uint32_t*>(&sScal[2]),
+                                         sQn);
+            scored = true;
+        }
+    }
+    if (!scored) {
+        for (int idx = threadIdx.x; idx < rows * T2; idx += kThreads2) {
+            const int t = idx / T2, i = idx % T2;
+            sS[t * SP2 + i] = sVthr[i] <= t ? canonG2(t, i) : -INFINITY;
+        }
+        if (threadIdx.x < kRows) sQn[threadIdx.x] = 0.0f;   // no certification
+    }
     __syncthreads();
     float qnmax = 0.0f;
     {
@@ -781,8 +829,8 @@ void route_stage2_kernel(RouteArgs A) {
         const int brows = rows - r0 < 4 * kWaves2 ? rows - r0 : 4 * kWaves2;
         dispatch_jj(T2, [&](auto jt) {
             constexpr int JJ = decltype(jt)::value;
-            rowgroup_requests<JJ>(r0, brows, T2, sS + r0 * SP2, SP2, A.Kgr, ds2, sQn, vis2,
-                                  sPk, sFirst, sBits, BW, sAmb, &sScal[4]);
+            rowgroup_requests<JJ, true>(r0, brows, T2, sS + r0 * SP2, SP2, A.Kgr, ds2, sQn,
+                                        sPk, sFirst, sBits, BW, sAmb, &sScal[4]);
         });
     }
     __syncthreads();
@@ -907,23 +955,25 @@ extern "C" int hga_route_prefill(const hga_config* cfg, int32_t S, const void* q
     HGA_REQUIRE(Pmax <= kJ * 64 && T2max <= kJ * 64, HGA_ERR_UNSUPPORTED,
                 "hga_route_prefill: routing pool %d / group candidates %d exceed %d", Pmax,
                 T2max, kJ * 64);
-    auto odd_above = [](int x) { return (x + 1) | 1; };   // smallest odd stride > x
-    a.SP = odd_above(Pmax);
-    a.SP2 = odd_above(T2max);
+    // Score rows: a multiple of 4 floats (16-byte stores of the MFMA epilogue) covering every
+    // 64-candidate read group, = 4 mod 32 so that the epilogue's stores are conflict-free.
+    auto row_stride = [](int x) { return (x + 63) / 64 * 64 + 4; };
+    a.SP = row_stride(Pmax);
+    a.SP2 = row_stride(T2max);
+    a.VT2 = (T2max + 63) / 64 * 64;
     const int D = cfg->head_dim;
-    const size_t esz = cfg->dtype == HGA_DTYPE_BF16 ? 2 : 4;
-    // stage 1: [32][SP] scores, the 32 query rows of a block, pooled state over the pool
-    a.SSZ = (kBlk * a.SP + 3) / 4 * 4;
+    // stage 1: [32][SP] scores of a row block, row norms, pooled state over the pool
+    a.SSZ = kBlk * a.SP;
     a.SPP = Pmax + 1;
     a.BW = (a.SPP + 31) / 32;
-    const size_t lds1 = sizeof(float) * (size_t)a.SSZ + esz * kBlk * D + sizeof(float) * kRows +
+    const size_t lds1 = sizeof(float) * (size_t)a.SSZ + sizeof(float) * kRows +
                         2 * sizeof(int) * (size_t)a.SPP + sizeof(uint32_t) * (size_t)kRows * a.BW +
                         sizeof(int) * (2 * kMaxSel + 8 + kRows);
-    // stage 2: [64][SP2] scores, the 64 query rows, pooled state over the group candidates
+    // stage 2: [64][SP2] scores of all rows, row norms, visibility table, pooled state
     a.SPP2 = T2max + 1;
     a.BW2 = (a.SPP2 + 31) / 32;
-    const size_t lds2 = sizeof(float) * (size_t)((kRows * a.SP2 + 3) / 4 * 4) + esz * kRows * D +
-                        sizeof(float) * kRows + 2 * sizeof(int) * (size_t)a.SPP2 +
+    const size_t lds2 = sizeof(float) * (size_t)kRows * a.SP2 + sizeof(float) * kRows +
+                        sizeof(int) * (size_t)a.VT2 + 2 * sizeof(int) * (size_t)a.SPP2 +
                         sizeof(uint32_t) * (size_t)kRows * a.BW2 +
                         sizeof(int) * (2 * kMaxSel + 8 + kRows);
     HGA_REQUIRE(lds1 <= 163840 && lds2 <= 163840, HGA_ERR_UNSUPPORTED,
