@@ -353,17 +353,18 @@ __global__ __launch_bounds__(kVT) void attend_valu_kernel(AttnArgs A) {
 // bf16 MFMA kernel v2 (group_size and chunk_size multiples of 16): no LDS operands, no barriers
 // ------------------------------------------------------------------------------------------
 // The key sequence is a list of 16-key blocks (a window or own-chunk block of 16 consecutive
-// tokens, or 16 tokens of an opened group).  One 64-lane wave owns all rows of a
-// (batch, head, chunk): S^T = K Q^T with K operands loaded straight from memory (lane = key, 8
-// consecutive dims: one 16-byte load), O^T = V^T P^T with V^T operands from a transposed copy
-// of V whose 16-key blocks store their keys in the order {0-3, 8-11, 4-7, 12-15}: the order in
-// which a lane half holds P after the score MFMA, so each operand is again one 16-byte load.
-// The next tile's K operands are fetched while the current tile's softmax and PV run.
+// tokens, or 16 tokens of an opened group), processed in tiles of two blocks.  One workgroup of
+// two waves owns a (batch, head, chunk), wave w rows 32w..32w+31: S^T = K Q^T, then
+// O^T = V^T P^T, both on v_mfma_f32_32x32x16_bf16.  The two waves share a double-buffered LDS
+// stage per tile: while tile t is computed, tile t+1's K and V blocks are copied into the other
+// stage by direct global->LDS 16-byte loads (global_load_lds_dwordx4), so the copies get a whole
+// tile of cover and hold no registers.
 
-// Blocked operand copies of K and V (one pass per call), so that every MFMA operand load of
-// the attention kernel reads whole contiguous 512-byte/1-KiB runs:
-//   kb[b][kvh][blk][s][16 keys][2 halves][8 dims]   K[16 blk + key][16 s + 8 half + j]
-//   vb[b][kvh][blk][d][16 slots]                     V[16 blk + vt_key(slot)][d]
+// Blocked operand copies of K and V (one pass per call): a 16-key block is one contiguous run
+// that a stage copy takes verbatim, laid out so that every 16-byte operand read of a wave from
+// LDS is conflict-free (eight consecutive lanes read 128 consecutive bytes):
+//   kb[b][kvh][blk][s][2 halves][16 keys][8 dims]     K[16 blk + key][16 s + 8 half + j]
+//   vb[b][kvh][blk][d/32][2 halves][32 dims][8 slots] V[16 blk + vt_key(8 half + j)][d]
 // with keys of a 16-key block stored in the order {0-3, 8-11, 4-7, 12-15} in vb: the order in
 // which a lane half holds P after the score MFMA.  Keys >= S are zero.  Sp = keys per (b, kvh),
 // a multiple of 64.
@@ -402,16 +403,17 @@ __global__ __launch_bounds__(256) void kv_block_kernel(const uint16_t* __restric
     }
     __syncthreads();
     const int64_t base = ((int64_t)b * KVH + kvh) * (int64_t)Sp * DH + (int64_t)k0 * DH;
-    // kb: 16-byte piece c -> (blk, s, key, half); consecutive c are consecutive in memory
+    // kb: 16-byte piece c -> (blk, s, half, key): dims 16s + 8half .. +7 of one key
     for (int c = threadIdx.x; c < kVtKeys * DH / 8; c += 256) {
-        const int half = c & 1, key = (c >> 1) & 15, sb = c >> 5;   // sb = blk * KS + s
+        const int key = c & 15, half = (c >> 4) & 1, sb = c >> 5;   // sb = blk * KS + s
         const int blk = sb / KS, st = sb % KS;
         const uint4 u = *reinterpret_cast<const uint4*>(&sK[(16 * blk + key) * RS + 16 * st + 8 * half]);
         *reinterpret_cast<uint4*>(kb + base + (int64_t)c * 8) = u;
     }
-    // vb: 16-byte piece c -> (blk, d, half of the 16 slots)
+    // vb: 16-byte piece c -> (blk, dim group, half, dim): slots 8half .. +7 of dim 32*group + dim
+    constexpr int DB = DH / 32;
     for (int c = threadIdx.x; c < kVtKeys * DH / 8; c += 256) {
-        const int half = c & 1, d = (c >> 1) % DH, blk = (c >> 1) / DH;
+        const int half = (c >> 5) & 1, d = 32 * ((c >> 6) % DB) + (c & 31), blk = (c >> 6) / DB;
         uint32_t w[4];
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
@@ -422,6 +424,19 @@ __global__ __launch_bounds__(256) void kv_block_kernel(const uint16_t* __restric
         *reinterpret_cast<uint4*>(vb + base + (int64_t)c * 8) = make_uint4(w[0], w[1], w[2], w[3]);
     }
 }
+
+// Direct global->LDS copy of 16 bytes per lane: lane i's 16 bytes at src land at the
+// wave-uniform LDS byte address lds_addr + 16 * i.  Issued as inline assembly so that the compiler,
+// which cannot prove that a copy into one stage does not alias reads of the other, inserts no
+// waits for it; the caller waits (vmcnt) before the barrier that publishes a stage.  M0 holds
+// the LDS address; nothing else in these kernels uses M0.
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ __forceinline__ void lds_copy16(const void* src, uint32_t lds_addr) {
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off"
+                 :: "s"(__builtin_amdgcn_readfirstlane(lds_addr)), "v"(src) : "memory", "m0");
+}
+#pragma clang diagnostic pop
 
 constexpr float kRescaleLog2 = 8.0f;   // a row's softmax reference may trail its max by 2^8
 constexpr int kV2Threads = 128;        // two waves: rows 0-31 and 32-63 of a query chunk
@@ -441,7 +456,8 @@ __global__ __launch_bounds__(kV2Threads) void attend_v2_kernel(AttnArgs A,
     const int C = A.C, gs = A.gs, M = A.M;
     int rows = A.S - n * C;
     if (rows > C) rows = C;
-    const int w = threadIdx.x / kWave, l = lane_id(), g = l >> 5, lr = l & 31;
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+    const int l = lane_id(), g = l >> 5, lr = l & 31;
     const int row = 32 * w + lr;                   // chunk-local query row of this lane
     const int Kgw = A.Kg > 0 ? A.Kg : 1;
 
@@ -454,7 +470,7 @@ __global__ __launch_bounds__(kV2Threads) void attend_v2_kernel(AttnArgs A,
         if (ogp[i] >= 0 && otp[i] >= 0) last = i;
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) last = max(last, __shfl_xor(last, o, kWave));
-    const int nopen = last + 1;                    // identical in both waves
+    const int nopen = __builtin_amdgcn_readfirstlane(last + 1);   // identical in both waves
     int f_hi, l_lo;
     windows(n, A.kf, A.kl, &f_hi, &l_lo);
     const int gpb = gs / 16, bpc = C / 16;
@@ -485,12 +501,32 @@ __global__ __launch_bounds__(kV2Threads) void attend_v2_kernel(AttnArgs A,
         sThr[gb] = thr;
     }
     __syncthreads();
-    if (32 * w >= rows) return;                    // ragged last chunk: no rows for this wave
+    // (a wave without rows in a ragged last chunk still takes its share of the stage copies)
 
-    // blocked operand copies of this (b, kv head): 16-key blocks of 16 * DH elements
+    constexpr int BB = 32 * DH;                    // bytes of one 16-key block of K or of V
+    constexpr int STG = 4 * BB;                    // a stage: K blocks a, b, then V blocks a, b
+    unsigned char* sStage = reinterpret_cast<unsigned char*>(sTab + 2 * nb_cap);
+    const uint32_t stage_lds = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) unsigned char*)sStage;
     const int64_t kvbase = ((int64_t)b * A.KVH + kvh) * (int64_t)Sp * DH;
-    const uint16_t* kbp = kbl + kvbase + (lr & 15) * 16 + 8 * g;   // + blk * 16 * DH + s * 256
-    const uint16_t* vbp = vbl + kvbase + lr * 16 + 8 * g;          // + blk * 16 * DH + d * 512
+    const unsigned char* kblk = reinterpret_cast<const unsigned char*>(kbl + kvbase);
+    const unsigned char* vblk = reinterpret_cast<const unsigned char*>(vbl + kvbase);
+    // Stage copy of tile t: 16-byte piece p = 128 r + thread; a wave's 64 pieces of one r are
+    // consecutive within one block (BB/16 pieces per block), so the LDS side is the wave-uniform
+    // base + 16 * lane that the direct load writes.
+    auto copy_tile = [&](int t, int stg) {
+        const int2 p2 = *reinterpret_cast<const int2*>(&sPos[2 * t]);
+        const int64_t ba = (int64_t)(__builtin_amdgcn_readfirstlane(p2.x) >> 4) * BB;
+        const int64_t bbk = (int64_t)(__builtin_amdgcn_readfirstlane(p2.y) >> 4) * BB;
+        const uint32_t dst = stage_lds + (uint32_t)(stg * STG);
+#pragma unroll
+        for (int r = 0; r < STG / (16 * kV2Threads); ++r) {
+            const int p0 = 128 * r + 64 * w;
+            const int region = p0 / (BB / 16);
+            const unsigned char* src = (region < 2 ? kblk : vblk) + ((region & 1) ? bbk : ba) +
+                                       (p0 % (BB / 16)) * 16 + 16 * l;
+            lds_copy16(src, dst + (uint32_t)(16 * p0));
+        }
+    };
     const int kcol = 8 * g;                        // this lane's 8 dims per k-step
     bf16x8 qb[KS];
     {
@@ -503,28 +539,26 @@ __global__ __launch_bounds__(kV2Threads) void attend_v2_kernel(AttnArgs A,
             qb[s] = __builtin_bit_cast(bf16x8, u);
         }
     }
-    // K operand: lane owns key lr of the 32-key tile (8 consecutive dims per k-step)
-    auto load_k = [&](int t, bf16x8 (&kr)[KS]) {
-        const int2 p2 = *reinterpret_cast<const int2*>(&sPos[2 * t]);
-        const int pa = __builtin_amdgcn_readfirstlane(p2.x), pb = __builtin_amdgcn_readfirstlane(p2.y);
-        const int blk = ((lr >> 4) ? pb : pa) >> 4;
-        const uint16_t* kr_ = kbp + (int64_t)blk * (16 * DH);
-#pragma unroll
-        for (int s = 0; s < KS; ++s)
-            kr[s] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(kr_ + 256 * s));
-    };
+    __builtin_amdgcn_s_waitcnt(0);   // q is in registers: no compiler wait inside the tile loop
+    // operand reads from a stage: K lane = key lr of the tile (block lr/16), V lane = dim lr of
+    // each 32-dim group; g selects the 8-element half
+    const int koff = ((lr >> 4) ? BB : 0) + 256 * g + 16 * (lr & 15);
+    const int voff = 2 * BB + 512 * g + 16 * lr;
     const float c2 = A.scale * 1.4426950408889634f;
-    // scores of tile t (S^T: lane = query row, 16 keys per lane), masked to the visible keys.
-    // Opened/window blocks have one first-visible row per block (uniform), so a block is all
-    // visible, all hidden, or split at one row for this wave; own-chunk blocks (index >= nb3)
-    // are causal per key.
-    auto scores = [&](int t, const bf16x8 (&kr)[KS]) {
-        const int2 t2 = *reinterpret_cast<const int2*>(&sThr[2 * t]);
-        const int th[2] = {__builtin_amdgcn_readfirstlane(t2.x), __builtin_amdgcn_readfirstlane(t2.y)};
+    // raw scores of a tile (S^T: lane = query row, 16 keys per lane)
+    auto scores_raw = [&](const bf16x8 (&kr)[KS]) {
         floatx16 sc = {};
 #pragma unroll
         for (int s = 0; s < KS; ++s)
             sc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kr[s], qb[s], sc, 0, 0, 0);
+        return sc;
+    };
+    // Mask tile t's scores to the visible keys.  Opened/window blocks have one first-visible
+    // row per block (uniform), so a block is all visible, all hidden, or split at one row for
+    // this wave; own-chunk blocks (index >= nb3) are causal per key.
+    auto mask = [&](int t, floatx16& sc) {
+        const int2 t2 = *reinterpret_cast<const int2*>(&sThr[2 * t]);
+        const int th[2] = {__builtin_amdgcn_readfirstlane(t2.x), __builtin_amdgcn_readfirstlane(t2.y)};
         const int gb0 = 2 * t;
         if (gb0 + 1 >= nb3) {
 #pragma unroll
@@ -543,7 +577,6 @@ __global__ __launch_bounds__(kV2Threads) void attend_v2_kernel(AttnArgs A,
                 for (int i = 8 * j; i < 8 * j + 8; ++i) sc[i] = vis ? sc[i] : -INFINITY;
             }
         }
-        return sc;
     };
     auto row_max = [&](const floatx16& x) {
         float m = -INFINITY;
@@ -551,56 +584,56 @@ __global__ __launch_bounds__(kV2Threads) void attend_v2_kernel(AttnArgs A,
         for (int i = 0; i < 16; ++i) m = fmaxf(m, x[i]);
         return fmaxf(m, __shfl_xor(m, 32, kWave));
     };
+    auto read_k = [&](int t, bf16x8 (&kr)[KS]) {
+        const unsigned char* stg = sStage + (t & 1) * STG + koff;
+#pragma unroll
+        for (int s = 0; s < KS; ++s)
+            kr[s] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(stg + 512 * s));
+    };
+    auto read_v = [&](int t, bf16x8 (&vr)[DB][2]) {
+        const unsigned char* stg = sStage + (t & 1) * STG + voff;
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+            for (int d = 0; d < DB; ++d)
+                vr[d][ks] = __builtin_bit_cast(
+                    bf16x8, *reinterpret_cast<const uint4*>(stg + ks * BB + 1024 * d));
+    };
 
-    // Softmax reference point per row.  The first finite tile max of a row becomes its
-    // reference (a row with no visible key so far has zero accumulators, so adopting it needs
-    // no rescale); later tiles may exceed it by up to 2^8 (p <= 256).  A tile beyond that
-    // triggers a restart: an exact row-max pass over all tiles, then the accumulation again
-    // from tile 0 without further checks.  The accumulators are thus only ever touched by
-    // MFMAs (or zeroed), never rescaled.
+    // Softmax reference point per row: the first finite tile max of the row (the accumulators
+    // are still zero then, so adopting it needs no rescale).  Later tiles may exceed it by up
+    // to 2^8 (p <= 256); a row whose tile max goes beyond that rescales its accumulators and
+    // running sum to the new max (rare: a wave-uniform branch skips it otherwise).
     floatx16 acc[DB];
 #pragma unroll
     for (int d = 0; d < DB; ++d) acc[d] = floatx16{};
     float m_ref = -INFINITY, l_run = 0.0f;
-    bool exact = false;
-    bf16x8 kr[KS];
-    load_k(0, kr);
+    copy_tile(0, 0);
     for (int t = 0; t < ntiles; ++t) {
-        const int2 p2 = *reinterpret_cast<const int2*>(&sPos[2 * t]);
-        const int pa[2] = {__builtin_amdgcn_readfirstlane(p2.x), __builtin_amdgcn_readfirstlane(p2.y)};
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // this thread's copies of tile t
+        __syncthreads();                                    // everyone's; stage t+1 is free
+        if (t + 1 < ntiles) copy_tile(t + 1, (t + 1) & 1);
+        bf16x8 kr[KS];
+        read_k(t, kr);
         bf16x8 vr[DB][2];
+        read_v(t, vr);
+        floatx16 sc = scores_raw(kr);
+        mask(t, sc);
+        const float m = row_max(sc);
+        bool jump = false;
+        if (m_ref == -INFINITY) m_ref = m;                   // first visible keys (or none yet)
+        else jump = (m - m_ref) * c2 > kRescaleLog2;
+        if (__builtin_amdgcn_ballot_w64(jump)) {
+            if (jump) {
+                const float f = __builtin_amdgcn_exp2f((m_ref - m) * c2);
 #pragma unroll
-        for (int ks = 0; ks < 2; ++ks) {
-            const uint16_t* vb = vbp + (int64_t)(pa[ks] >> 4) * (16 * DH);
+                for (int d = 0; d < DB; ++d)
 #pragma unroll
-            for (int d = 0; d < DB; ++d)
-                vr[d][ks] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(vb + 512 * d));
-        }
-        floatx16 sc = scores(t, kr);
-        if (!exact) {
-            const float m = row_max(sc);
-            bool jump = false;
-            if (m_ref == -INFINITY) m_ref = m;                   // first visible keys
-            else jump = (m - m_ref) * c2 > kRescaleLog2;
-            if (__builtin_amdgcn_ballot_w64(jump)) {
-                // exact row maxima over the whole key sequence, then start over
-                float mt = -INFINITY;
-                for (int u = 0; u < ntiles; ++u) {
-                    bf16x8 ku[KS];
-                    load_k(u, ku);
-                    mt = fmaxf(mt, row_max(scores(u, ku)));
-                }
-                m_ref = mt;
-                l_run = 0.0f;
-#pragma unroll
-                for (int d = 0; d < DB; ++d) acc[d] = floatx16{};
-                exact = true;
-                t = -1;
-                load_k(0, kr);
-                continue;
+                    for (int i = 0; i < 16; ++i) acc[d][i] *= f;
+                l_run *= f;
+                m_ref = m;
             }
         }
-        if (t + 1 < ntiles) load_k(t + 1, kr);
         const float nb = m_ref == -INFINITY ? 0.0f : -m_ref * c2;
         bf16x8 pt[2];
         float rs = 0.0f;
@@ -622,17 +655,18 @@ __global__ __launch_bounds__(kV2Threads) void attend_v2_kernel(AttnArgs A,
     const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
     uint16_t* op = reinterpret_cast<uint16_t*>(A.out) + b * A.o_sb + h * A.o_sh +
                    ((int64_t)C * n + row) * A.o_ss;
+    typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
 #pragma unroll
     for (int d = 0; d < DB; ++d)
 #pragma unroll
         for (int q4 = 0; q4 < 4; ++q4) {
             const int dim = d * 32 + 8 * q4 + 4 * g;
-            uint2 u;
-            u.x = (uint32_t)f_to_bf16(acc[d][4 * q4] * inv) |
-                  ((uint32_t)f_to_bf16(acc[d][4 * q4 + 1] * inv) << 16);
-            u.y = (uint32_t)f_to_bf16(acc[d][4 * q4 + 2] * inv) |
-                  ((uint32_t)f_to_bf16(acc[d][4 * q4 + 3] * inv) << 16);
-            *reinterpret_cast<uint2*>(op + dim) = u;
+            bf16x4 o;   // hardware round-to-nearest-even conversion
+            o[0] = (__bf16)(acc[d][4 * q4] * inv);
+            o[1] = (__bf16)(acc[d][4 * q4 + 1] * inv);
+            o[2] = (__bf16)(acc[d][4 * q4 + 2] * inv);
+            o[3] = (__bf16)(acc[d][4 * q4 + 3] * inv);
+            *reinterpret_cast<uint2*>(op + dim) = __builtin_bit_cast(uint2, o);
         }
 }
 
@@ -711,7 +745,8 @@ extern "C" int hga_attend_prefill(const hga_config* cfg, int32_t S, const void* 
         // 16-key blocks of the longest key sequence, rounded up to whole 2-block tiles
         const int bpc = a.C / 16;
         const int nb_cap = ((a.kf + a.kl + 1) * bpc + Kg * (a.gs / 16) + 3) / 4 * 4;
-        const size_t lds2 = sizeof(int) * 2 * (size_t)nb_cap;
+        // block table, then two stages of one tile (K and V of two 16-key blocks)
+        const size_t lds2 = sizeof(int) * 2 * (size_t)nb_cap + 2 * 4 * 32 * (size_t)D;
         HGA_REQUIRE(lds2 <= 65536, HGA_ERR_UNSUPPORTED,
                     "hga_attend_prefill: key sequence of %d blocks too long", nb_cap);
         dim3 tg((unsigned)(Sp / kVtKeys), (unsigned)a.KVH, (unsigned)a.B);
