@@ -143,7 +143,7 @@ __device__ __forceinline__ float sumsq_bf16x8(uint4 u) {
 // block 0's tiles) is folded into *knmax (uint bits of a non-negative float).  VIS: candidate c
 // of row t gets -inf unless vthr[c] <= t.
 template <int DH, int NW, bool VIS, class RowPtr>
-__device__ void scores_st(const uint16_t* qg, int64_t q_ss, int rows, int nrb, int ncand,
+__device__ __forceinline__ void scores_st(const uint16_t* qg, int64_t q_ss, int rows, int nrb, int ncand,
                           RowPtr rowptr, const int* vthr, float* sRows, int stride, float scale,
                           uint32_t* knmax, float* sQn) {
     constexpr int KS = DH / 16;
@@ -323,25 +323,36 @@ __device__ int pooled_select(int ncand, int k, int rows, const uint32_t* sBits, 
 // register W*g + e holds candidate 16*W*g + W*seg + e (g < JJ/W, e < W), so that a lane reads
 // W consecutive scores at once.  The per-row count of keys >= x is a 16-lane DPP reduction, so
 // a search step costs 2*JJ + 8 VALU operations for four rows at once.
-template <class Op>
+// DPP source with the operation's identity as the "old" value and bound_ctrl set (every lane
+// reads a valid source in these patterns), so the compiler can fold the move into the op.
+template <int CTRL, int IDENT>
+__device__ __forceinline__ int dppi(int x) {
+    return __builtin_amdgcn_update_dpp(IDENT, x, CTRL, 0xf, 0xf, true);
+}
+// Butterfly over the 16 lanes of a DPP row: every step pairs each lane with a partner that
+// pairs back with it (xor 1, xor 2, then the half-row and row mirrors, which act as xor 4 and
+// xor 8 once values are uniform within quads and half-rows), so with a commutative op all 16
+// lanes end bit-identical even for floating-point sums (a rotation pattern would add the
+// partial sums in a lane-dependent order and leave lanes of one row with different roundings).
+template <int IDENT, class Op>
 __device__ __forceinline__ int row16_reduce(int x, Op op) {
-    x = op(x, dpp<0xB1>(x));    // quad_perm [1,0,3,2]
-    x = op(x, dpp<0x4E>(x));    // quad_perm [2,3,0,1]
-    x = op(x, dpp<0x124>(x));   // row_ror:4
-    x = op(x, dpp<0x128>(x));   // row_ror:8
+    x = op(x, dppi<0xB1, IDENT>(x));    // quad_perm [1,0,3,2]
+    x = op(x, dppi<0x4E, IDENT>(x));    // quad_perm [2,3,0,1]
+    x = op(x, dppi<0x141, IDENT>(x));   // row_half_mirror
+    x = op(x, dppi<0x140, IDENT>(x));   // row_mirror
     return x;
 }
-__device__ __forceinline__ int r16_sum(int x) { return row16_reduce(x, [](int a, int b) { return a + b; }); }
+__device__ __forceinline__ int r16_sum(int x) { return row16_reduce<0>(x, [](int a, int b) { return a + b; }); }
 __device__ __forceinline__ float r16_fsum(float x) {
-    return __int_as_float(row16_reduce(__float_as_int(x), [](int a, int b) {
+    return __int_as_float(row16_reduce<0>(__float_as_int(x), [](int a, int b) {
         return __float_as_int(__int_as_float(a) + __int_as_float(b));
     }));
 }
 __device__ __forceinline__ uint32_t r16_umin(uint32_t x) {
-    return (uint32_t)row16_reduce((int)x, [](int a, int b) { return (int)min((uint32_t)a, (uint32_t)b); });
+    return (uint32_t)row16_reduce<-1>((int)x, [](int a, int b) { return (int)min((uint32_t)a, (uint32_t)b); });
 }
 __device__ __forceinline__ uint32_t r16_umax(uint32_t x) {
-    return (uint32_t)row16_reduce((int)x, [](int a, int b) { return (int)max((uint32_t)a, (uint32_t)b); });
+    return (uint32_t)row16_reduce<0>((int)x, [](int a, int b) { return (int)max((uint32_t)a, (uint32_t)b); });
 }
 
 template <int JJ>
@@ -372,62 +383,56 @@ __device__ __forceinline__ float z_upper_fast(float p) {
     return lower ? -z : z;
 }
 
-// Row statistics gathered while loading: nv valid candidates, sum and sum of squares of their
-// values, smallest and largest key (row-reduced).
+// Row statistics gathered while loading: nv valid candidates; the search seed's sample (the
+// row's first read group, at most 64 candidates): ns values, their sum and sum of squares.
 struct RowStats {
-    int nv;
+    int nv, ns;
     float s1, s2;
-    uint32_t kmn, kmx;
 };
 
-// Exact top-k of the row's keys (0 = not a candidate; larger key first, equal keys -> lower
-// candidate index).  Every lane of the wave must call it (DPP reads neighbours).  Returns
-// member bits (bit i <-> register i).
+// Top-k of the row's keys (0 = not a candidate; larger key first).  Every lane of the wave
+// must call it (DPP reads neighbours).  Returns the member bits (bit i <-> register i: keys >=
+// the separating key vsep_out) when the search separated exactly k keys; tie_out reports rows
+// whose k-th and (k+1)-th keys are equal (their bits are not a selection: such rows take the
+// canonical path, which orders equal keys by candidate index).  Keys are below 0xffffffff
+// (okey of a NaN with an all-ones payload, which no score producer emits).
 template <int JJ>
-__device__ uint32_t rowgroup_topk(const uint32_t (&kv)[JJ], int k, const RowStats& rs) {
-    constexpr int W = JJ < 4 ? JJ : 4;
-    const int l = lane_id(), seg = l & 15;
+__device__ __forceinline__ uint32_t rowgroup_topk(const uint32_t (&kv)[JJ], int k, const RowStats& rs,
+                                                  uint32_t& vsep_out, bool& tie_out) {
     const int nv = rs.nv;
     // state per row: threshold vsep (members: key >= vsep, or > vsep plus ties when tie).
-    // Bracket [lo, hi) with clo = count(>= lo) > k > chi = count(>= hi); hi starts one past
-    // the largest key (count 0), so ties at the maximum end in the tie path like any other.
+    // Bracket [lo, hi) with clo = count(>= lo) > k > chi = count(>= hi): key 1 (every valid
+    // candidate) and the largest key value (none).  lf/hf only steer the interpolation: they
+    // start as mean -/+ 8 standard deviations of the sample and become probe values.
     bool done = nv <= k, tie = false;
-    uint32_t vsep = 1u, lo = rs.kmn;
-    uint32_t hi = rs.kmx == 0xffffffffu ? rs.kmx : rs.kmx + 1u;
+    uint32_t vsep = 1u, lo = 1u, hi = 0xffffffffu;
     int clo = nv, chi = 0;
-    if (__ballot(rs.kmx == 0xffffffffu) != 0) {   // degenerate top key: count it exactly
-        const int c = r16_count_ge<JJ>(kv, hi);
-        if (rs.kmx == 0xffffffffu) chi = c;
-        if (!done && rs.kmx == 0xffffffffu && c >= k) {
-            vsep = hi;
-            tie = true;
-            done = true;
-        }
-    }
-    float lf = okey_inv(lo), hf = okey_inv(hi);
-    float guess = 0.0f;
+    float lf, hf, guess;
     {
-        const float rn = __builtin_amdgcn_rcpf((float)(nv > 0 ? nv : 1));
+        const float rn = __builtin_amdgcn_rcpf((float)(rs.ns > 0 ? rs.ns : 1));
         const float mu = rs.s1 * rn;
         const float sd = __builtin_amdgcn_sqrtf(fmaxf(rs.s2 * rn - mu * mu, 0.0f));
-        guess = mu + z_upper_fast((k + 0.5f) * rn) * sd;
+        const float rv = __builtin_amdgcn_rcpf((float)(nv > 0 ? nv : 1));
+        guess = mu + z_upper_fast((k + 0.5f) * rv) * sd;
+        lf = mu - 8.0f * sd - 1e-30f;
+        hf = mu + 8.0f * sd + 1e-30f;
     }
     for (int it = 0; __ballot(!done) != 0; ++it) {
         uint32_t mid = lo + (hi - lo) / 2u;
         float midf = 0.0f;
-        bool interp = false;
         if (it < 8) {
+            // interpolated probe (only steers the search: approximate reciprocal is enough),
+            // kept at least 1/16 of the span inside the bracket and clamped into (lo, hi) in
+            // key space
             const float span = hf - lf;
-            // the interpolated probe only steers the search: approximate reciprocal is enough
             float x = it == 0 ? guess
                               : lf + span * (float)(clo - k) * __builtin_amdgcn_rcpf((float)(clo - chi));
             x = fminf(fmaxf(x, lf + span * 0.0625f), hf - span * 0.0625f);
-            const uint32_t xm = okey(x);
-            interp = x == x && span < INFINITY && xm > lo && xm < hi;
-            mid = interp ? xm : mid;
+            mid = min(max(okey_fast(x), lo + 1u), hi - 1u);
             midf = x;
+        } else {
+            midf = okey_inv(mid);
         }
-        if (!interp) midf = okey_inv(mid);
         const int c = r16_count_ge<JJ>(kv, mid);
         if (!done) {
             if (c == k) {
@@ -451,35 +456,11 @@ __device__ uint32_t rowgroup_topk(const uint32_t (&kv)[JJ], int k, const RowStat
             }
         }
     }
+    tie_out = tie;
+    vsep_out = vsep;
     uint32_t bits = 0;
 #pragma unroll
-    for (int i = 0; i < JJ; ++i) bits |= ((tie ? kv[i] > vsep : kv[i] >= vsep) ? 1u : 0u) << i;
-    if (__ballot(tie) != 0) {
-        // boundary ties: the lowest candidate indices among key == vsep.  Candidate order is
-        // (group g, lane seg, e): within a group, lanes below first, then the lane's own e order.
-        int r = k - r16_count_ge<JJ>(kv, vsep + 1u);
-        const int sh = 16 * (l >> 4);
-        const uint32_t lower = (1u << seg) - 1u;
-#pragma unroll
-        for (int g = 0; g < JJ / W; ++g) {
-            int below = 0, tot = 0;
-#pragma unroll
-            for (int e = 0; e < W; ++e) {
-                const uint32_t m16 =
-                    (uint32_t)(__ballot(tie && kv[W * g + e] == vsep) >> sh) & 0xffffu;
-                below += __popc(m16 & lower);
-                tot += __popc(m16);
-            }
-            int own = 0;
-#pragma unroll
-            for (int e = 0; e < W; ++e) {
-                const bool eq = tie && kv[W * g + e] == vsep;
-                if (eq && below + own < r) bits |= 1u << (W * g + e);
-                own += eq ? 1 : 0;
-            }
-            r -= tot < r ? tot : r;
-        }
-    }
+    for (int i = JJ - 1; i >= 0; --i) bits = 2u * bits + (kv[i] >= vsep ? 1u : 0u);
     return bits;
 }
 
@@ -489,7 +470,7 @@ __device__ uint32_t rowgroup_topk(const uint32_t (&kv)[JJ], int k, const RowStat
 // their members and set their request bits; rows whose k-th and (k+1)-th values lie within
 // 2*delta are queued (absolute row) in sAmb for the canonical path.
 template <int JJ, bool VIS>
-__device__ void rowgroup_requests(int r0, int brows, int ncand, const float* sS, int stride,
+__device__ __forceinline__ void rowgroup_requests(int r0, int brows, int ncand, const float* sS, int stride,
                                   int k, float dsc, const float* sQn, uint32_t* sPk,
                                   int* sFirst, uint32_t* sBits, int BW, int* sAmb, int* sAmbN) {
     constexpr int W = JJ < 4 ? JJ : 4;
@@ -499,8 +480,8 @@ __device__ void rowgroup_requests(int r0, int brows, int ncand, const float* sS,
     const bool act = rr < brows;
     const float* rowp = sS + rr * stride;
     uint32_t kv[JJ];
-    RowStats rs{0, 0.0f, 0.0f, 0xffffffffu, 0u};
-    int nvl = 0;
+    RowStats rs{0, 0, 0.0f, 0.0f};
+    int nvl = 0, nsl = 0;
 #pragma unroll
     for (int g = 0; g < G; ++g) {
         const int c0 = 16 * W * g + W * seg;
@@ -523,51 +504,64 @@ __device__ void rowgroup_requests(int r0, int brows, int ncand, const float* sS,
 #pragma unroll
             for (int e = 0; e < W; ++e) {
                 kv[W * g + e] = okey_fast(x[e]);
-                rs.s1 += x[e];
-                rs.s2 = fmaf(x[e], x[e], rs.s2);
-                rs.kmn = min(rs.kmn, kv[W * g + e]);
-                rs.kmx = max(rs.kmx, kv[W * g + e]);
+                if (g == 0) {
+                    rs.s1 += x[e];
+                    rs.s2 = fmaf(x[e], x[e], rs.s2);
+                }
             }
         } else if (16 * W * g < ncand) {
 #pragma unroll
             for (int e = 0; e < W; ++e) {
                 const bool valid = (full || c0 + e < ncand) && (!VIS || x[e] != -INFINITY);
-                const float xm = valid ? x[e] : 0.0f;
-                const uint32_t key = valid ? okey_fast(x[e]) : 0u;
-                kv[W * g + e] = key;
+                kv[W * g + e] = valid ? okey_fast(x[e]) : 0u;
                 nvl += valid ? 1 : 0;
-                rs.s1 += xm;
-                rs.s2 = fmaf(xm, xm, rs.s2);
-                rs.kmn = min(rs.kmn, valid ? key : 0xffffffffu);
-                rs.kmx = max(rs.kmx, key);
+                if (g == 0) {
+                    const float xm = valid ? x[e] : 0.0f;
+                    nsl += valid ? 1 : 0;
+                    rs.s1 += xm;
+                    rs.s2 = fmaf(xm, xm, rs.s2);
+                }
             }
         } else {
 #pragma unroll
             for (int e = 0; e < W; ++e) kv[W * g + e] = 0u;
         }
     }
+    // valid counts: without VIS every candidate below ncand is valid
     rs.nv = act ? (VIS ? r16_sum(nvl) : ncand) : 0;
+    rs.ns = VIS ? r16_sum(nsl) : (ncand < 16 * W ? ncand : 16 * W);
     rs.s1 = r16_fsum(rs.s1);
     rs.s2 = r16_fsum(rs.s2);
-    rs.kmn = r16_umin(rs.kmn);
-    rs.kmx = r16_umax(rs.kmx);
-    const uint32_t bits = rowgroup_topk<JJ>(kv, k, rs);
-    // certification: k-th and (k+1)-th values at least 2*delta apart
-    bool amb = false;
+    uint32_t vsep;
+    bool tie;
+    const uint32_t bits = rowgroup_topk<JJ>(kv, k, rs, vsep, tie);
+    // A tie at the boundary goes to the canonical path (equal keys ordered by candidate index
+    // there; with MFMA scores such a row is never certifiable anyway).  Certification: k-th and
+    // (k+1)-th values at least 2*delta apart.  Rows with at most k candidates have no (k+1)-th.
+    // A row that ended with count(>= vsep) == k is certified when no key lies in
+    // [value(vsep) - 2 delta, vsep) (one more count); only rows failing that test get the exact
+    // k-th / (k+1)-th comparison.
+    const bool open = act && rs.nv > k;
+    bool amb = open && tie;
     if (dsc > 0.0f) {
-        uint32_t kk = 0xffffffffu, kk1 = 0u;      // smallest member key, largest non-member key
-#pragma unroll
-        for (int i = 0; i < JJ; ++i) {
-            if (kv[i] == 0u) continue;
-            if ((bits >> i) & 1u) kk = min(kk, kv[i]);
-            else kk1 = max(kk1, kv[i]);
-        }
-        kk = r16_umin(kk);
-        kk1 = r16_umax(kk1);
-        const float ak = kk == 0xffffffffu ? INFINITY : okey_inv(kk);
-        const float ak1 = kk1 == 0u ? -INFINITY : okey_inv(kk1);
         const float delta = act ? dsc * sQn[t] : 0.0f;
-        amb = act && ak1 != -INFINITY && !(ak - 2.0f * delta > ak1);
+        const uint32_t probe = okey_fast(okey_inv(vsep) - 2.0f * delta);
+        const int cp = r16_count_ge<JJ>(kv, probe);
+        const bool unsure = open && !tie && cp != k;
+        if (__ballot(unsure) != 0) {
+            uint32_t kk = 0xffffffffu, kk1 = 0u;  // smallest member key, largest non-member key
+#pragma unroll
+            for (int i = 0; i < JJ; ++i) {
+                if (kv[i] == 0u) continue;
+                if ((bits >> i) & 1u) kk = min(kk, kv[i]);
+                else kk1 = max(kk1, kv[i]);
+            }
+            kk = r16_umin(kk);
+            kk1 = r16_umax(kk1);
+            const float ak = kk == 0xffffffffu ? INFINITY : okey_inv(kk);
+            const float ak1 = kk1 == 0u ? -INFINITY : okey_inv(kk1);
+            if (unsure) amb = ak1 != -INFINITY && !(ak - 2.0f * delta > ak1);
+        }
     }
     if (amb) {
         if (seg == 0) sAmb[atomicAdd(sAmbN, 1)] = t;
@@ -584,14 +578,31 @@ __device__ void rowgroup_requests(int r0, int brows, int ncand, const float* sS,
     }
 }
 
-// Calls f(JTag<JJ>) with the smallest JJ in {1,2,4,8,16,32} such that 16*JJ >= n (n <= 512).
+// Out-of-line entry for the wide variants in stage 1: called, they get the whole register
+// budget instead of sharing it with the kernel's live state (fewer spills than inlined).
+template <int JJ, bool VIS>
+__device__ __noinline__ void rowgroup_requests_call(int r0, int brows, int ncand, const float* sS,
+                                                    int stride, int k, float dsc,
+                                                    const float* sQn, uint32_t* sPk,
+                                                    int* sFirst, uint32_t* sBits, int BW,
+                                                    int* sAmb, int* sAmbN) {
+    rowgroup_requests<JJ, VIS>(r0, brows, ncand, sS, stride, k, dsc, sQn, sPk, sFirst, sBits, BW,
+                               sAmb, sAmbN);
+}
+
+// Calls f(JTag<JJ>) with the smallest JJ in {1, 2, 4, 8, 12, ..., 32} such that 16*JJ >= n
+// (n <= 512): rows are at most 64 slots longer than the candidate count.
 template <class F>
 __device__ __forceinline__ void dispatch_jj(int n, F&& f) {
     if (n <= 16) f(JTag<1>{});
     else if (n <= 32) f(JTag<2>{});
     else if (n <= 64) f(JTag<4>{});
     else if (n <= 128) f(JTag<8>{});
+    else if (n <= 192) f(JTag<12>{});
     else if (n <= 256) f(JTag<16>{});
+    else if (n <= 320) f(JTag<20>{});
+    else if (n <= 384) f(JTag<24>{});
+    else if (n <= 448) f(JTag<28>{});
     else f(JTag<32>{});
 }
 
@@ -676,8 +687,12 @@ void route_stage1_kernel(RouteArgs A) {
         const int kreq = A.Kc < P ? A.Kc : P;
         dispatch_jj(P, [&](auto jt) {
             constexpr int JJ = decltype(jt)::value;
-            rowgroup_requests<JJ, false>(r0, brows, P, sS, SP, kreq, ds1, sQn, sPk, sFirst, sBits,
-                                         BW, sAmb, &sScal[4]);
+            if constexpr (JJ >= 8)
+                rowgroup_requests_call<JJ, false>(r0, brows, P, sS, SP, kreq, ds1, sQn, sPk,
+                                                  sFirst, sBits, BW, sAmb, &sScal[4]);
+            else
+                rowgroup_requests<JJ, false>(r0, brows, P, sS, SP, kreq, ds1, sQn, sPk, sFirst,
+                                             sBits, BW, sAmb, &sScal[4]);
         });
         __syncthreads();
         // rows the MFMA scores could not certify: canonical re-rank (one row per wave)

@@ -167,10 +167,13 @@ def test_route_exact_ties(hga):
     gk[:, :, :, 3] = gk[:, :, :, 1]    # group 3 of every chunk ties with group 1
     stats = torch.zeros(4, dtype=torch.int32, device=dev)
     r = ops.route_prefill(cfg, q.to(dev), ck, gk, stats=stats)
+    stats_c = torch.zeros(4, dtype=torch.int32, device=dev)
+    rc = ops.route_prefill(cfg, q.to(dev), ck, gk, canonical=True, stats=stats_c)
     f = lambda t: t.float().cpu().numpy()
     o_r = oracle.route_prefill(f(q), f(ck), f(gk), S, C, gs, 1, 1, 4, 8, oracle.attn_scale(Dh))
-    _cmp_sets(r, o_r["sel_chunk"], o_r["sel_thr"], "sel_chunk", "sel_thr")
-    _cmp_sets(r, o_r["open_grp"], o_r["open_thr"], "open_grp", "open_thr")
-    print("ambiguous rows/pools:", stats.cpu().tolist())
+    for rr in (r, rc):                   # MFMA-certified and canonical scoring
+        _cmp_sets(rr, o_r["sel_chunk"], o_r["sel_thr"], "sel_chunk", "sel_thr")
+        _cmp_sets(rr, o_r["open_grp"], o_r["open_thr"], "open_grp", "open_thr")
+    print("ambiguous rows/pools:", stats.cpu().tolist(), "canonical:", stats_c.cpu().tolist())
     assert (o_r["sel_chunk"] == 2).sum() > 0
     assert stats[0].item() > 0           # the tie path really ran
