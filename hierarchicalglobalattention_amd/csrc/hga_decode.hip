@@ -274,6 +274,69 @@ struct DecAttnArgs {
     float scale;
 };
 
+// The key sequence of a decode block for (b, query head): [first window | last window | opened
+// groups | active chunk], key k -> (key row, value row, first visible query row).  sOG/sOT hold
+// the head's opened list in LDS; nopen is its valid length.
+template <class T>
+struct DecKeys {
+    const T *kr, *vr, *kf, *vf, *kd, *vd;
+    int64_t r_ss, f_ss, d_ss, c0;
+    const int *sOG, *sOT;
+    int a1, a2, a3, a4, C, gs, M, n_closed, l_lo, ring;
+
+    __device__ void init(const DecAttnArgs& A, int b, int kvh, const int* og, const int* ot,
+                         int nopen) {
+        int f_hi;
+        windows(A.n_closed, A.kf, A.kl, &f_hi, &l_lo);
+        C = A.C; gs = A.gs; M = A.M; n_closed = A.n_closed; ring = A.ring;
+        sOG = og; sOT = ot;
+        c0 = A.start_pos - (int64_t)A.n_closed * C;
+        a1 = f_hi * C;
+        a2 = a1 + (A.n_closed - l_lo) * C;
+        a3 = a2 + nopen * gs;
+        a4 = a3 + (int)c0 + A.L;
+        kr = reinterpret_cast<const T*>(A.kr) + b * A.r_sb + kvh * A.r_sh;
+        vr = reinterpret_cast<const T*>(A.vr) + b * A.r_sb + kvh * A.r_sh;
+        kf = reinterpret_cast<const T*>(A.kfst) + b * A.f_sb + kvh * A.f_sh;
+        vf = reinterpret_cast<const T*>(A.vfst) + b * A.f_sb + kvh * A.f_sh;
+        kd = reinterpret_cast<const T*>(A.kd) + b * A.d_sb + kvh * A.d_sh;
+        vd = reinterpret_cast<const T*>(A.vd) + b * A.d_sb + kvh * A.d_sh;
+        r_ss = A.r_ss; f_ss = A.f_ss; d_ss = A.d_ss;
+    }
+    __device__ void locate(int k, const T*& kp, const T*& vp, int& thr) const {
+        if (k < a1) {
+            kp = kf + (int64_t)k * f_ss;
+            vp = vf + (int64_t)k * f_ss;
+            thr = 0;
+            return;
+        }
+        int64_t pos;
+        if (k < a2) {
+            pos = (int64_t)l_lo * C + (k - a1);
+            thr = 0;
+        } else if (k < a3) {
+            const int g = (k - a2) / gs, e = (k - a2) % gs, grp = sOG[g];
+            if (grp < 0 || grp >= n_closed * M || sOT[g] < 0) {   // padding / invalid id
+                kp = vp = nullptr;
+                thr = kNoRow;
+                return;
+            }
+            const int64_t p = (int64_t)(grp / M) * C + (grp % M) * gs + e;
+            kp = kd + p * d_ss;
+            vp = vd + p * d_ss;
+            thr = sOT[g];
+            return;
+        } else {
+            pos = (int64_t)n_closed * C + (k - a3);
+            thr = (int)((k - a3) - c0);
+            if (thr < 0) thr = 0;
+        }
+        const int64_t slot = ring > 0 ? ((pos / C) % ring) * C + pos % C : pos;
+        kp = kr + slot * r_ss;
+        vp = vr + slot * r_ss;
+    }
+};
+
 template <int DT, int DH>
 __global__ __launch_bounds__(kDT) void attend_decode_kernel(DecAttnArgs A) {
     typedef typename Elem<DT>::T T;
@@ -284,9 +347,6 @@ __global__ __launch_bounds__(kDT) void attend_decode_kernel(DecAttnArgs A) {
     __shared__ int sOG[256], sOT[256];
     const int bh = blockIdx.x, b = bh / A.H, h = bh % A.H, kvh = h / (A.H / A.KVH);
     const int w = threadIdx.x / kWave, l = lane_id();
-    const int C = A.C, gs = A.gs, M = A.M;
-    int f_hi, l_lo;
-    windows(A.n_closed, A.kf, A.kl, &f_hi, &l_lo);
     const int Kgw = A.Kg > 0 ? A.Kg : 1;
     for (int i = threadIdx.x; i < A.Kg; i += kDT) {
         sOG[i] = A.open_grp[(int64_t)bh * Kgw + i];
@@ -296,48 +356,10 @@ __global__ __launch_bounds__(kDT) void attend_decode_kernel(DecAttnArgs A) {
     int nopen = 0;
     for (int i = 0; i < A.Kg; ++i)
         if (sOG[i] >= 0 && sOT[i] >= 0) nopen = i + 1;
-    const int64_t c0 = A.start_pos - (int64_t)A.n_closed * C;
-    const int a1 = f_hi * C, a2 = a1 + (A.n_closed - l_lo) * C, a3 = a2 + nopen * gs;
-    const int a4 = a3 + (int)c0 + A.L;
-    const T* kr = reinterpret_cast<const T*>(A.kr) + b * A.r_sb + kvh * A.r_sh;
-    const T* vr = reinterpret_cast<const T*>(A.vr) + b * A.r_sb + kvh * A.r_sh;
-    const T* kf = reinterpret_cast<const T*>(A.kfst) + b * A.f_sb + kvh * A.f_sh;
-    const T* vf = reinterpret_cast<const T*>(A.vfst) + b * A.f_sb + kvh * A.f_sh;
-    const T* kd = reinterpret_cast<const T*>(A.kd) + b * A.d_sb + kvh * A.d_sh;
-    const T* vd = reinterpret_cast<const T*>(A.vd) + b * A.d_sb + kvh * A.d_sh;
-    // key k -> (key row, value row, first visible query row)
-    auto key = [&](int k, const T*& kp, const T*& vp, int& thr) {
-        if (k < a1) {
-            kp = kf + (int64_t)k * A.f_ss;
-            vp = vf + (int64_t)k * A.f_ss;
-            thr = 0;
-            return;
-        }
-        int64_t pos;
-        if (k < a2) {
-            pos = (int64_t)l_lo * C + (k - a1);
-            thr = 0;
-        } else if (k < a3) {
-            const int g = (k - a2) / gs, e = (k - a2) % gs, grp = sOG[g];
-            if (grp < 0 || grp >= A.n_closed * M || sOT[g] < 0) {   // padding / invalid id
-                kp = vp = nullptr;
-                thr = kNoRow;
-                return;
-            }
-            const int64_t p = (int64_t)(grp / M) * C + (grp % M) * gs + e;
-            kp = kd + p * A.d_ss;
-            vp = vd + p * A.d_ss;
-            thr = sOT[g];
-            return;
-        } else {
-            pos = (int64_t)A.n_closed * C + (k - a3);
-            thr = (int)((k - a3) - c0);
-            if (thr < 0) thr = 0;
-        }
-        const int64_t slot = A.ring > 0 ? ((pos / C) % A.ring) * C + pos % C : pos;
-        kp = kr + slot * A.r_ss;
-        vp = vr + slot * A.r_ss;
-    };
+    DecKeys<T> keys;
+    keys.init(A, b, kvh, sOG, sOT, nopen);
+    const int a4 = keys.a4;
+    auto key = [&](int k, const T*& kp, const T*& vp, int& thr) { keys.locate(k, kp, vp, thr); };
     const int per = (a4 + kDW - 1) / kDW;
     const int k_lo = w * per, k_hi = (w + 1) * per < a4 ? (w + 1) * per : a4;
     const T* qg = reinterpret_cast<const T*>(A.q) + b * A.q_sb + h * A.q_sh;
@@ -426,8 +448,393 @@ __global__ __launch_bounds__(kDT) void attend_decode_kernel(DecAttnArgs A) {
     }
 }
 
+// ------------------------------------------------------------------------------------------
+// split decode attention (head_dim 64 / 128): the key sequence of each (b, head) in splits of
+// kSplitKeys keys, one workgroup per split; 16 lanes per key (a lane holds head_dim/16
+// consecutive dims, so a key row is one contiguous read), 16 keys per 16-lane group, four in
+// flight.  Each split writes its (max, sum, accumulator) partial; decode_combine_kernel merges.
+// ------------------------------------------------------------------------------------------
+constexpr int kSplitKeys = 256;
+
+// Sum over the 16 lanes of a DPP row, bit-identical in all of them (butterfly: xor 1, xor 2,
+// half-row mirror, row mirror).
+__device__ __forceinline__ float r16_sum_f(float x) {
+    x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0xB1, 0xf, 0xf, true));
+    x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x4E, 0xf, 0xf, true));
+    x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x141, 0xf, 0xf, true));
+    x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x140, 0xf, 0xf, true));
+    return x;
+}
+
+template <int DT, int DPL>
+__device__ __forceinline__ void load_slice(const typename Elem<DT>::T* p, float (&x)[DPL]) {
+    if constexpr (DT == HGA_DTYPE_BF16) {
+        if constexpr (DPL == 8) {
+            const uint4 u = *reinterpret_cast<const uint4*>(p);
+            const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                x[2 * e] = __uint_as_float(w[e] << 16);
+                x[2 * e + 1] = __uint_as_float(w[e] & 0xffff0000u);
+            }
+        } else {
+            const uint2 u = *reinterpret_cast<const uint2*>(p);
+            x[0] = __uint_as_float(u.x << 16);
+            x[1] = __uint_as_float(u.x & 0xffff0000u);
+            x[2] = __uint_as_float(u.y << 16);
+            x[3] = __uint_as_float(u.y & 0xffff0000u);
+        }
+    } else {
+#pragma unroll
+        for (int e = 0; e < DPL; e += 4) {
+            const float4 u = *reinterpret_cast<const float4*>(p + e);
+            x[e] = u.x; x[e + 1] = u.y; x[e + 2] = u.z; x[e + 3] = u.w;
+        }
+    }
+}
+
+template <int DT, int DH>
+__global__ __launch_bounds__(kDT) void attend_decode_split_kernel(DecAttnArgs A, float* part,
+                                                                  int nsplit) {
+    typedef typename Elem<DT>::T T;
+    constexpr int DPL = DH / 16;
+    constexpr int NG = kDT / 16;                     // 16-lane groups per workgroup
+    constexpr int KPG = kSplitKeys / NG;             // keys per group
+    constexpr int U = 4;                             // keys in flight per group
+    __shared__ int sOG[256], sOT[256];
+    __shared__ float sM[NG], sL[NG];
+    __shared__ float sAcc[NG][DH];
+    const int split = blockIdx.x, bh = blockIdx.y, b = bh / A.H, h = bh % A.H;
+    const int kvh = h / (A.H / A.KVH);
+    const int l = lane_id(), j = l & 15, G = (int)(threadIdx.x >> 4);
+    const int Kgw = A.Kg > 0 ? A.Kg : 1;
+    for (int i = threadIdx.x; i < A.Kg; i += kDT) {
+        sOG[i] = A.open_grp[(int64_t)bh * Kgw + i];
+        sOT[i] = A.open_thr[(int64_t)bh * Kgw + i];
+    }
+    __syncthreads();
+    int nopen = 0;
+    for (int i = 0; i < A.Kg; ++i)
+        if (sOG[i] >= 0 && sOT[i] >= 0) nopen = i + 1;
+    DecKeys<T> keys;
+    keys.init(A, b, kvh, sOG, sOT, nopen);
+    const int gk0 = split * kSplitKeys + G * KPG;
+    const T* qg = reinterpret_cast<const T*>(A.q) + b * A.q_sb + h * A.q_sh;
+    for (int row = 0; row < A.L; ++row) {
+        float qv[DPL];
+#pragma unroll
+        for (int e = 0; e < DPL; ++e) qv[e] = Elem<DT>::ld(qg, (int64_t)row * A.q_ss + j * DPL + e);
+        float m_run = -INFINITY, l_run = 0.0f, acc[DPL];
+#pragma unroll
+        for (int e = 0; e < DPL; ++e) acc[e] = 0.0f;
+        for (int i0 = 0; i0 < KPG; i0 += U) {
+            const T* vp[U];
+            float s[U];
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const int k = gk0 + i0 + u;
+                const T* kp = nullptr;
+                vp[u] = nullptr;
+                int thr = kNoRow;
+                if (k < keys.a4) keys.locate(k, kp, vp[u], thr);
+                float d = 0.0f;
+                const bool vis = k < keys.a4 && row >= thr;
+                if (vis) {
+                    float kx[DPL];
+                    load_slice<DT, DPL>(kp + j * DPL, kx);
+#pragma unroll
+                    for (int e = 0; e < DPL; ++e) d = fmaf(qv[e], kx[e], d);
+                }
+                d = r16_sum_f(d);                    // whole group: uniform control flow
+                s[u] = vis ? d * A.scale : -INFINITY;
+                if (!vis) vp[u] = nullptr;
+            }
+            float mx = m_run;
+#pragma unroll
+            for (int u = 0; u < U; ++u) mx = fmaxf(mx, s[u]);
+            const float m_use = mx == -INFINITY ? 0.0f : mx;
+            const float alpha = expf(m_run - m_use);
+            l_run *= alpha;
+#pragma unroll
+            for (int e = 0; e < DPL; ++e) acc[e] *= alpha;
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const float p = expf(s[u] - m_use);
+                l_run += p;
+                if (vp[u]) {
+                    float vx[DPL];
+                    load_slice<DT, DPL>(vp[u] + j * DPL, vx);
+#pragma unroll
+                    for (int e = 0; e < DPL; ++e) acc[e] = fmaf(p, vx[e], acc[e]);
+                }
+            }
+            m_run = mx;
+        }
+        if (j == 0) {
+            sM[G] = m_run;
+            sL[G] = l_run;
+        }
+#pragma unroll
+        for (int e = 0; e < DPL; ++e) sAcc[G][j * DPL + e] = acc[e];
+        __syncthreads();
+        // merge the 16 groups: partial of this split for this row
+        float* pp = part + (((int64_t)bh * A.L + row) * nsplit + split) * (DH + 2);
+        float mt = -INFINITY;
+        for (int g = 0; g < NG; ++g) mt = fmaxf(mt, sM[g]);
+        const float mu = mt == -INFINITY ? 0.0f : mt;
+        for (int d = threadIdx.x; d < DH; d += kDT) {
+            float o = 0.0f;
+            for (int g = 0; g < NG; ++g) o += sAcc[g][d] * expf(sM[g] - mu);
+            pp[2 + d] = o;
+        }
+        if (threadIdx.x == 0) {
+            float lt = 0.0f;
+            for (int g = 0; g < NG; ++g) lt += sL[g] * expf(sM[g] - mu);
+            pp[0] = mt;
+            pp[1] = lt;
+        }
+        __syncthreads();
+    }
+}
+
+// One workgroup per (b, head, row): out = sum_s e^(m_s - M) acc_s / sum_s e^(m_s - M) l_s.
+template <int DT, int DH>
+__global__ __launch_bounds__(128) void decode_combine_kernel(DecAttnArgs A, const float* part,
+                                                             int nsplit) {
+    typedef typename Elem<DT>::T T;
+    const int bhr = blockIdx.x, row = bhr % A.L, bh = bhr / A.L, b = bh / A.H, h = bh % A.H;
+    const float* pp = part + (int64_t)bhr * nsplit * (DH + 2);
+    float mt = -INFINITY;
+    for (int s2 = 0; s2 < nsplit; ++s2) mt = fmaxf(mt, pp[s2 * (DH + 2)]);
+    const float mu = mt == -INFINITY ? 0.0f : mt;
+    float lt = 0.0f;
+    for (int s2 = 0; s2 < nsplit; ++s2) lt += pp[s2 * (DH + 2) + 1] * expf(pp[s2 * (DH + 2)] - mu);
+    const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
+    T* og = reinterpret_cast<T*>(A.out) + b * A.o_sb + h * A.o_sh + (int64_t)row * A.o_ss;
+    for (int d = threadIdx.x; d < DH; d += 128) {
+        float o = 0.0f;
+        for (int s2 = 0; s2 < nsplit; ++s2)
+            o += pp[s2 * (DH + 2) + 2 + d] * expf(pp[s2 * (DH + 2)] - mu);
+        Elem<DT>::st(og, d, o * inv);
+    }
+}
+
+// ------------------------------------------------------------------------------------------
+// decode gather: the opened groups of a step, deduplicated per (batch, KV head), copied from the
+// closed-token record (pinned host memory or device) into a device staging buffer
+// ------------------------------------------------------------------------------------------
+constexpr int kGT = 256;
+
+struct GatherArgs {
+    const int32_t* open_grp;
+    const int32_t* open_thr;
+    const unsigned char* kd;
+    const unsigned char* vd;
+    int64_t d_sb, d_sh, d_ss;          // record strides (elements)
+    unsigned char* stage_k;
+    unsigned char* stage_v;
+    int32_t* staged_grp;               // [B, H, Kg] staging slot of each opened group, -1 if none
+    int32_t* ulist;                    // [B, KVH, U] group id of each staging slot
+    int32_t* ucount;                   // [B, KVH]
+    int B, H, KVH, rep, Kg, NG, U, C, gs, M, D, esz;
+};
+
+// One workgroup per (b, kv head): the valid opened groups of the kv head's rep query heads are
+// marked in an LDS bitmap over group ids [0, NG); a group's staging slot is its rank among the
+// marked ids (prefix popcount), so slots are dense and in ascending group order.
+__global__ __launch_bounds__(kGT) void gather_plan_kernel(GatherArgs A) {
+    extern __shared__ uint32_t sBm[];                  // [NW] bitmap, then [NW] prefix counts
+    __shared__ int sPart[kGT];
+    const int b = blockIdx.x / A.KVH, kvh = blockIdx.x % A.KVH, tid = threadIdx.x;
+    const int NW = (A.NG + 31) / 32;
+    int* sPre = reinterpret_cast<int*>(sBm + NW);
+    for (int i = tid; i < NW; i += kGT) sBm[i] = 0u;
+    __syncthreads();
+    const int Kgw = A.Kg > 0 ? A.Kg : 1, n_ent = A.rep * A.Kg;
+    for (int e = tid; e < n_ent; e += kGT) {
+        const int h = kvh * A.rep + e / A.Kg;
+        const int64_t idx = ((int64_t)b * A.H + h) * Kgw + e % A.Kg;
+        const int g = A.open_grp[idx];
+        if (g >= 0 && g < A.NG && A.open_thr[idx] >= 0) atomicOr(&sBm[g >> 5], 1u << (g & 31));
+    }
+    __syncthreads();
+    // exclusive prefix of the words' popcounts: per-thread ranges, then a serial scan of the
+    // kGT partial sums
+    const int per = (NW + kGT - 1) / kGT;
+    const int w0 = tid * per, w1 = w0 + per < NW ? w0 + per : NW;
+    int part = 0;
+    for (int w = w0; w < w1; ++w) part += __popc(sBm[w]);
+    sPart[tid] = part;
+    __syncthreads();
+    if (tid == 0) {
+        int run = 0;
+        for (int i = 0; i < kGT; ++i) {
+            const int x = sPart[i];
+            sPart[i] = run;
+            run += x;
+        }
+        A.ucount[blockIdx.x] = run;
+    }
+    __syncthreads();
+    {
+        int run = sPart[tid];
+        for (int w = w0; w < w1; ++w) {
+            sPre[w] = run;
+            run += __popc(sBm[w]);
+        }
+    }
+    __syncthreads();
+    int32_t* ul = A.ulist + (int64_t)blockIdx.x * A.U;
+    for (int w = tid; w < NW; w += kGT) {
+        uint32_t bits = sBm[w];
+        int slot = sPre[w];
+        while (bits) {
+            ul[slot++] = 32 * w + __builtin_ctz(bits);
+            bits &= bits - 1u;
+        }
+    }
+    for (int e = tid; e < n_ent; e += kGT) {
+        const int h = kvh * A.rep + e / A.Kg;
+        const int64_t idx = ((int64_t)b * A.H + h) * Kgw + e % A.Kg;
+        const int g = A.open_grp[idx];
+        int slot = -1;
+        if (g >= 0 && g < A.NG && A.open_thr[idx] >= 0)
+            slot = sPre[g >> 5] + __popc(sBm[g >> 5] & ((1u << (g & 31)) - 1u));
+        A.staged_grp[idx] = slot;
+    }
+}
+
+// One workgroup per (staging slot, kv head, b): copies the group's gs K rows and gs V rows
+// (contiguous in a [.., T, D] record) with 16-byte accesses; slots past the count exit.
+__global__ __launch_bounds__(kGT) void gather_copy_kernel(GatherArgs A) {
+    const int u = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
+    const int bk = b * A.KVH + kvh;
+    if (u >= A.ucount[bk]) return;
+    const int g = A.ulist[(int64_t)bk * A.U + u];
+    const int64_t p0 = (int64_t)(g / A.M) * A.C + (int64_t)(g % A.M) * A.gs;
+    const int64_t src = ((int64_t)b * A.d_sb + (int64_t)kvh * A.d_sh + p0 * A.d_ss) * A.esz;
+    const int64_t dst = (((int64_t)bk * A.U + u) * A.gs) * (int64_t)A.D * A.esz;
+    const int vpr = A.D * A.esz / 16;                  // 16-byte pieces per row
+    for (int c = threadIdx.x; c < A.gs * vpr; c += kGT) {
+        const int r = c / vpr, x = (c % vpr) * 16;
+        const int64_t so = src + (int64_t)r * A.d_ss * A.esz + x;
+        const int64_t dO = dst + (int64_t)r * A.D * A.esz + x;
+        *reinterpret_cast<uint4*>(A.stage_k + dO) = *reinterpret_cast<const uint4*>(A.kd + so);
+        *reinterpret_cast<uint4*>(A.stage_v + dO) = *reinterpret_cast<const uint4*>(A.vd + so);
+    }
+}
+
 }  // namespace
 }  // namespace hga
+
+namespace {
+// Splits of the split decode attention: the longest key sequence a head of the block can have
+// (every opened slot valid) in kSplitKeys pieces.
+int decode_splits(const hga_config* cfg, int32_t L, int32_t n_closed, int64_t start_pos,
+                  int32_t Kg) {
+    int f_hi, l_lo;
+    hga::windows(n_closed, cfg->keep_first, cfg->keep_last, &f_hi, &l_lo);
+    const int64_t C = cfg->chunk_size;
+    const int64_t c0 = start_pos - (int64_t)n_closed * C;
+    const int64_t keys = (int64_t)f_hi * C + (int64_t)(n_closed - l_lo) * C +
+                         (int64_t)(Kg > 0 ? Kg : 0) * cfg->group_size + c0 + L;
+    const int64_t n = (keys + hga::kSplitKeys - 1) / hga::kSplitKeys;
+    return (int)(n > 0 ? n : 1);
+}
+}  // namespace
+
+extern "C" int32_t hga_attend_decode_workspace(const hga_config* cfg, int32_t L, int32_t n_closed,
+                                               int64_t start_pos, int32_t Kg, int64_t* bytes) {
+    using namespace hga;
+    int rc = check_config(cfg);
+    if (rc) return rc;
+    HGA_REQUIRE(bytes && L >= 1 && n_closed >= 0 && Kg >= 0, HGA_ERR_ARG,
+                "hga_attend_decode_workspace: bad arguments");
+    const int D = cfg->head_dim;
+    *bytes = (D == 64 || D == 128)
+                 ? 4 * (int64_t)cfg->batch * cfg->heads * L *
+                       decode_splits(cfg, L, n_closed, start_pos, Kg) * (D + 2)
+                 : 0;
+    return HGA_OK;
+}
+
+extern "C" int32_t hga_gather_decode_sizes(const hga_config* cfg, int32_t Kg,
+                                           int32_t* stage_groups, int64_t* stage_bytes,
+                                           int64_t* scratch_bytes) {
+    using namespace hga;
+    int rc = check_config(cfg);
+    if (rc) return rc;
+    HGA_REQUIRE(Kg >= 0 && stage_groups && stage_bytes && scratch_bytes, HGA_ERR_ARG,
+                "hga_gather_decode_sizes: bad arguments");
+    const int rep = cfg->heads / cfg->kv_heads;
+    const int U = rep * (Kg > 0 ? Kg : 1);
+    const int64_t esz = cfg->dtype == HGA_DTYPE_BF16 ? 2 : 4;
+    *stage_groups = U;
+    *stage_bytes = (int64_t)cfg->batch * cfg->kv_heads * U * cfg->group_size * cfg->head_dim * esz;
+    *scratch_bytes = 4 * (int64_t)cfg->batch * cfg->kv_heads * (U + 1);
+    return HGA_OK;
+}
+
+extern "C" int hga_gather_decode(const hga_config* cfg, int32_t n_closed, const int32_t* open_grp,
+                                 const int32_t* open_thr, int32_t Kg, const void* k_record,
+                                 const void* v_record, int64_t d_sb, int64_t d_sh, int64_t d_ss,
+                                 int32_t record_on_host, void* stage_k, void* stage_v,
+                                 int32_t stage_groups, int32_t* staged_grp, void* scratch,
+                                 int64_t scratch_bytes, void* stream) {
+    using namespace hga;
+    int rc = check_config(cfg);
+    if (rc) return rc;
+    HGA_REQUIRE(open_grp && open_thr && k_record && v_record && stage_k && stage_v && staged_grp &&
+                    scratch,
+                HGA_ERR_ARG, "hga_gather_decode: NULL pointer");
+    HGA_REQUIRE(n_closed >= 0 && Kg >= 0, HGA_ERR_ARG, "hga_gather_decode: bad n_closed/Kg");
+    int32_t U = 0;
+    int64_t sbytes = 0, need = 0;
+    hga_gather_decode_sizes(cfg, Kg, &U, &sbytes, &need);
+    // scratch: the slot list at the caller's staging capacity, then the counts
+    need = 4 * (int64_t)cfg->batch * cfg->kv_heads * ((int64_t)stage_groups + 1);
+    HGA_REQUIRE(stage_groups >= U && scratch_bytes >= need, HGA_ERR_ARG,
+                "hga_gather_decode: staging for %d groups and %lld scratch bytes required", U,
+                (long long)need);
+    const int64_t ve = cfg->dtype == HGA_DTYPE_BF16 ? 8 : 4;
+    HGA_REQUIRE(((uintptr_t)k_record | (uintptr_t)v_record | (uintptr_t)stage_k |
+                 (uintptr_t)stage_v) % 16 == 0 && ((d_sb | d_sh | d_ss) % ve) == 0,
+                HGA_ERR_ARG, "hga_gather_decode: 16-byte aligned rows required");
+    GatherArgs a{};
+    a.kd = static_cast<const unsigned char*>(k_record);
+    a.vd = static_cast<const unsigned char*>(v_record);
+    if (record_on_host) {
+        void *dk = nullptr, *dv = nullptr;
+        hipError_t e1 = hipHostGetDevicePointer(&dk, const_cast<void*>(k_record), 0);
+        hipError_t e2 = hipHostGetDevicePointer(&dv, const_cast<void*>(v_record), 0);
+        HGA_REQUIRE(e1 == hipSuccess && e2 == hipSuccess, HGA_ERR_ARG,
+                    "hga_gather_decode: the host record is not pinned device-accessible memory");
+        a.kd = static_cast<const unsigned char*>(dk);
+        a.vd = static_cast<const unsigned char*>(dv);
+    }
+    a.open_grp = open_grp; a.open_thr = open_thr;
+    a.d_sb = d_sb; a.d_sh = d_sh; a.d_ss = d_ss;
+    a.stage_k = static_cast<unsigned char*>(stage_k);
+    a.stage_v = static_cast<unsigned char*>(stage_v);
+    a.staged_grp = staged_grp;
+    a.B = cfg->batch; a.H = cfg->heads; a.KVH = cfg->kv_heads; a.rep = cfg->heads / cfg->kv_heads;
+    a.Kg = Kg; a.C = cfg->chunk_size; a.gs = cfg->group_size; a.M = a.C / a.gs;
+    a.NG = n_closed * a.M; a.U = stage_groups; a.D = cfg->head_dim;
+    a.esz = cfg->dtype == HGA_DTYPE_BF16 ? 2 : 4;
+    a.ulist = static_cast<int32_t*>(scratch);
+    a.ucount = a.ulist + (int64_t)a.B * a.KVH * a.U;
+    const int NW = (a.NG + 31) / 32;
+    const size_t lds = 2 * sizeof(uint32_t) * (size_t)(NW > 0 ? NW : 1);
+    HGA_REQUIRE(lds <= 65536, HGA_ERR_UNSUPPORTED, "hga_gather_decode: %d closed chunks too many",
+                n_closed);
+    hipStream_t st = (hipStream_t)stream;
+    gather_plan_kernel<<<dim3((unsigned)(a.B * a.KVH)), dim3(kGT), lds, st>>>(a);
+    rc = launch_status("hga_gather_decode (plan)");
+    if (rc) return rc;
+    if (Kg == 0 || n_closed == 0) return HGA_OK;
+    gather_copy_kernel<<<dim3((unsigned)a.U, (unsigned)a.KVH, (unsigned)a.B), dim3(kGT), 0, st>>>(a);
+    return launch_status("hga_gather_decode (copy)");
+}
 
 extern "C" int32_t hga_decode_widths(const hga_config* cfg, int32_t n_closed, int32_t* Kc,
                                      int32_t* Kg) {
@@ -526,7 +933,8 @@ extern "C" int hga_attend_decode(const hga_config* cfg, int32_t L, int32_t n_clo
                                  const void* v_record, int64_t d_sb, int64_t d_sh, int64_t d_ss,
                                  int32_t record_on_host, const int32_t* open_grp,
                                  const int32_t* open_thr, int32_t Kg, void* out, int64_t o_sb,
-                                 int64_t o_sh, int64_t o_ss, void* stream) {
+                                 int64_t o_sh, int64_t o_ss, void* workspace,
+                                 int64_t workspace_bytes, void* stream) {
     using namespace hga;
     int rc = check_config(cfg);
     if (rc) return rc;
@@ -573,6 +981,28 @@ extern "C" int hga_attend_decode(const hga_config* cfg, int32_t L, int32_t n_clo
     HGA_REQUIRE(al % 16 == 0 && ((r_sb | r_sh | r_ss | f_sb | f_sh | f_ss | d_sb | d_sh | d_ss) % ve) == 0,
                 HGA_ERR_ARG, "hga_attend_decode: 16-byte aligned key rows required");
     hipStream_t st = (hipStream_t)stream;
+    if (D == 64 || D == 128) {
+        const int nsplit = decode_splits(cfg, L, n_closed, start_pos, Kg);
+        const int64_t need = 4 * (int64_t)a.B * a.H * L * nsplit * (D + 2);
+        HGA_REQUIRE(workspace && workspace_bytes >= need, HGA_ERR_ARG,
+                    "hga_attend_decode: workspace of %lld bytes required (got %lld)",
+                    (long long)need, (long long)workspace_bytes);
+        float* part = static_cast<float*>(workspace);
+        const dim3 g1((unsigned)nsplit, (unsigned)(a.B * a.H)), g2((unsigned)(a.B * a.H * L));
+#define HGA_DS_CASE(DTV, DHV)                                                                    \
+        if (cfg->dtype == DTV && D == DHV) {                                                   \
+            attend_decode_split_kernel<DTV, DHV><<<g1, kDT, 0, st>>>(a, part, nsplit);          \
+            rc = launch_status("hga_attend_decode (split)");                                    \
+            if (rc) return rc;                                                                  \
+            decode_combine_kernel<DTV, DHV><<<g2, 128, 0, st>>>(a, part, nsplit);               \
+            return launch_status("hga_attend_decode (combine)");                                \
+        }
+        HGA_DS_CASE(HGA_DTYPE_BF16, 128)
+        HGA_DS_CASE(HGA_DTYPE_BF16, 64)
+        HGA_DS_CASE(HGA_DTYPE_F32, 128)
+        HGA_DS_CASE(HGA_DTYPE_F32, 64)
+#undef HGA_DS_CASE
+    }
     const unsigned grid = (unsigned)(a.B * a.H);
 #define HGA_DA_CASE(DTV, DHV) \
     if (cfg->dtype == DTV && D == DHV) { attend_decode_kernel<DTV, DHV><<<grid, kDT, 0, st>>>(a); return launch_status("hga_attend_decode"); }

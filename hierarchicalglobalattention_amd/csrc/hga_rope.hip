@@ -1,5 +1,5 @@
 // Rotate-half RoPE applied in fp32 and rounded to the activation dtype
-// (HierarchicalGlobalAttentionRouted.py:156-157, 219-223).  Memory-bound elementwise kernel:
+// (HierarchicalGlobalAttentionRouted.py:156-157, 219-223).  HBM-bound elementwise kernel:
 // each thread owns 4 consecutive dims of the first half and the matching 4 of the second half
 // of one row, so every load/store is an 8-byte (bf16) or 16-byte (fp32) vector access.
 // Built with -ffp-contract=off: x*cos and rot*sin are rounded separately, then added, as torch's
@@ -50,8 +50,12 @@ __global__ __launch_bounds__(256) void rope_kernel(const char* x, int64_t x_sb, 
     const int64_t row = (int64_t)blockIdx.x * rpb + threadIdx.x / tpr;
     if (row >= nrows) return;
     const int d0 = (threadIdx.x % tpr) * 4;
-    const int s = (int)(row % S);
-    const int64_t bx = row / S;
+    // rows in (position, batch, head) order, heads fastest: the heads of one position share
+    // its cos/sin row while it is in cache (head-major order would stream the whole table
+    // once per head)
+    const int64_t BX = nrows / S;
+    const int s = (int)(row / BX);
+    const int64_t bx = row % BX;
     const int h = (int)(bx % X);
     const int64_t b = bx / X;
     constexpr int E = Vec4<DT>::kBytes;

@@ -233,6 +233,56 @@ def route_decode(cfg: HgaConfig, q: torch.Tensor, chunk_k: torch.Tensor, group_k
     return r
 
 
+def gather_decode_sizes(cfg: HgaConfig, Kg: int) -> tuple[int, int, int]:
+    """(stage_groups, stage_bytes, scratch_bytes) of hga_gather_decode."""
+    u, sb, xb = ctypes.c_int32(), ctypes.c_int64(), ctypes.c_int64()
+    check(lib().hga_gather_decode_sizes(ctypes.byref(cfg), Kg, ctypes.byref(u), ctypes.byref(sb),
+                                        ctypes.byref(xb)), "hga_gather_decode_sizes")
+    return u.value, sb.value, xb.value
+
+
+class DecodeStaging:
+    """Device staging for hga_gather_decode, reused across calls (stream-ordered): K/V
+    [B, KVH, U, gs, Dh], staged group slots [B, H, Kg] and the int32 scratch; reallocated only
+    when a call needs more."""
+
+    def __init__(self):
+        self.key = None
+
+    def get(self, cfg: HgaConfig, Kg: int, H: int, dtype, device):
+        U, sbytes, xbytes = gather_decode_sizes(cfg, Kg)
+        B, KVH, gs, D = cfg.batch, cfg.kv_heads, cfg.group_size, cfg.head_dim
+        key = (B, KVH, H, U, gs, D, max(Kg, 1), dtype, device)
+        if self.key != key:
+            self.k = torch.empty((B, KVH, U * gs, D), dtype=dtype, device=device)
+            self.v = torch.empty_like(self.k)
+            self.grp = torch.empty((B, H, max(Kg, 1)), dtype=torch.int32, device=device)
+            self.scratch = torch.empty((xbytes + 3) // 4, dtype=torch.int32, device=device)
+            self.key = key
+        return U, self.k, self.v, self.grp, self.scratch
+
+
+def gather_decode(cfg: HgaConfig, n_closed: int, open_grp: torch.Tensor, open_thr: torch.Tensor,
+                  Kg: int, record_k: torch.Tensor, record_v: torch.Tensor, record_on_host: bool,
+                  staging: DecodeStaging, H: int):
+    """Copies the step's opened groups (deduplicated per KV head) from the record into device
+    staging; returns (stage_k, stage_v, staged_grp): a [B, KVH, U*gs, Dh] record view and the
+    open-group list to pass to attend_decode in place of the record and open_grp."""
+    _dev(open_grp, open_thr)
+    if record_on_host and not record_k.is_pinned():
+        raise ValueError("a host record must be pinned memory")
+    if record_k.stride() != record_v.stride():
+        raise ValueError("K and V of the record must share strides")
+    U, sk, sv, sg, scr = staging.get(cfg, Kg, H, record_k.dtype, open_grp.device)
+    og = open_grp.contiguous()
+    ot = open_thr.contiguous()
+    check(lib().hga_gather_decode(
+        ctypes.byref(cfg), n_closed, _p(og), _p(ot), Kg, _p(record_k), _p(record_v),
+        *_s4(record_k)[:3], 1 if record_on_host else 0, _p(sk), _p(sv), U, _p(sg), _p(scr),
+        scr.numel() * 4, _stream()), "hga_gather_decode")
+    return sk, sv, sg
+
+
 def attend_decode(cfg: HgaConfig, q: torch.Tensor, n_closed: int, start_pos: int,
                   recent_k: torch.Tensor, recent_v: torch.Tensor, ring_chunks: int,
                   first_k, first_v, record_k, record_v, record_on_host: bool,
@@ -259,9 +309,13 @@ def attend_decode(cfg: HgaConfig, q: torch.Tensor, n_closed: int, start_pos: int
             raise ValueError("K and V of a source must share strides")
     og = open_grp.contiguous()
     ot = open_thr.contiguous()
+    nb = ctypes.c_int64()
+    check(lib().hga_attend_decode_workspace(ctypes.byref(cfg), L, n_closed, start_pos, Kg,
+                                            ctypes.byref(nb)), "hga_attend_decode_workspace")
+    ws = torch.empty(max(nb.value, 16), dtype=torch.uint8, device=q.device)
     check(lib().hga_attend_decode(
         ctypes.byref(cfg), L, n_closed, start_pos, _p(q), *_s4(q), _p(recent_k), _p(recent_v),
         *_s4(recent_k), ring_chunks, _p(first_k), _p(first_v), *_s4(first_k), _p(record_k),
         _p(record_v), *_s4(record_k), 1 if record_on_host else 0, _p(og), _p(ot), Kg, _p(out),
-        *_s4(out), _stream()), "hga_attend_decode")
+        *_s4(out), _p(ws), ws.numel(), _stream()), "hga_attend_decode")
     return out

@@ -200,8 +200,10 @@ class VramKVCacheStore(_StoreBase):
 class RamKVCacheStore(_StoreBase):
     """RAM tier (ram_kv_cache_store.py:29-619 semantics): the closed-token record lives in pinned
     host memory; only the summary tables, the first window and a ring holding the last window
-    plus the active chunk live on the GPU.  Opened groups are read from the host record by the
-    decode attention kernel directly over PCIe (zero copy), so only routed groups cross the link.
+    plus the active chunk live on the GPU.  Each decode step gathers its opened groups,
+    deduplicated over the query heads of a KV head, from the host record into a device staging
+    buffer (hga_gather_decode: coalesced 4 KiB group reads over PCIe), and attention reads them
+    there, so only routed groups cross the link, once per KV head.
     The record must be pinned for that (the reference's module uses pageable memory,
     HierarchicalGlobalAttentionRouted.py:239); ``pin_memory`` is accepted for signature
     compatibility.  The reference's optional LRU VRAM banks (``vram_cache_chunks``,
@@ -214,6 +216,7 @@ class RamKVCacheStore(_StoreBase):
                                                      "groups_per_chunk", "batch_size", "dtype",
                                                      "initial_capacity")}
         super().__init__(**kw)
+        self.staging = ops.DecodeStaging()   # shared by all layers (stream-ordered reuse)
 
     def _new_record(self, *shape):
         return torch.zeros(*shape, dtype=self.dtype, pin_memory=True)
@@ -295,7 +298,7 @@ class RamKVCacheStore(_StoreBase):
         st = self.layer(layer)
         return dict(recent_k=st.ring_k, recent_v=st.ring_v, ring_chunks=st.ring_R,
                     first_k=st.first_k, first_v=st.first_v, record_k=st.tok_k,
-                    record_v=st.tok_v, record_on_host=True)
+                    record_v=st.tok_v, record_on_host=True, staging=self.staging)
 
 
 class RoutedKV:
@@ -324,9 +327,17 @@ class RoutedKV:
         if self.chunked:
             return ops.attend_prefill(self.hcfg, q, self.k_rope, self.v, r["open_grp"],
                                       r["open_thr"], r["Kg"])
-        return ops.attend_decode(self.hcfg, q, self.n_closed, self.start_pos,
-                                 open_grp=r["open_grp"], open_thr=r["open_thr"], Kg=r["Kg"],
-                                 **self.sources)
+        src = dict(self.sources)
+        staging = src.pop("staging", None)
+        og = r["open_grp"]
+        if staging is not None:
+            # host record: gather the opened groups into device staging, attend there
+            sk, sv, og = ops.gather_decode(self.hcfg, self.n_closed, og, r["open_thr"], r["Kg"],
+                                           src["record_k"], src["record_v"],
+                                           src["record_on_host"], staging, q.shape[1])
+            src.update(record_k=sk, record_v=sv, record_on_host=False)
+        return ops.attend_decode(self.hcfg, q, self.n_closed, self.start_pos, open_grp=og,
+                                 open_thr=r["open_thr"], Kg=r["Kg"], **src)
 
 
 class ChunkRouter:

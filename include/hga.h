@@ -187,7 +187,40 @@ int hga_attend_decode(const hga_config* cfg, int32_t L, int32_t n_closed, int64_
                       const void* k_record, const void* v_record, int64_t d_sb, int64_t d_sh,
                       int64_t d_ss, int32_t record_on_host, const int32_t* open_grp,
                       const int32_t* open_thr, int32_t Kg, void* out, int64_t o_sb,
-                      int64_t o_sh, int64_t o_ss, void* stream);
+                      int64_t o_sh, int64_t o_ss, void* workspace, int64_t workspace_bytes,
+                      void* stream);
+
+/* Device scratch bytes hga_attend_decode needs (head_dim 64 / 128: the key sequence is split
+ * over workgroups of 256 keys whose fp32 partials [B*H*L, splits, head_dim+2] are merged by a
+ * second kernel; 0 for other head dims).  16-byte aligned, used only by the call's kernels
+ * (stream ordered).  No counterpart in the reference. */
+int32_t hga_attend_decode_workspace(const hga_config* cfg, int32_t L, int32_t n_closed,
+                                    int64_t start_pos, int32_t Kg, int64_t* bytes);
+
+/* Sizes for hga_gather_decode: staging capacity per (batch, KV head) in groups (rep * Kg, the
+ * most distinct groups the rep query heads can open), bytes of each of the K and V staging
+ * buffers ([B, KVH, stage_groups, group_size, head_dim]) and bytes of the int32 scratch. */
+int32_t hga_gather_decode_sizes(const hga_config* cfg, int32_t Kg, int32_t* stage_groups,
+                                int64_t* stage_bytes, int64_t* scratch_bytes);
+
+/*
+ * Decode gather (the store I/O of ram_kv_cache_store.py:_gather_record / gather_tokens,
+ * :560-607, done once per KV head instead of once per query head): the groups opened by
+ * hga_route_decode (open_grp/open_thr [B, H, Kg]) are deduplicated over the rep query heads of
+ * each KV head and copied, in ascending group order, from the closed-token record (pinned host
+ * memory read over PCIe when record_on_host != 0, else device memory; element strides b, kv
+ * head, position) into stage_k / stage_v [B, KVH, stage_groups, group_size, head_dim].
+ * staged_grp [B, H, Kg] receives each opened group's staging slot (-1 for padding / invisible).
+ * Since a slot s occupies positions [s*gs, s*gs + gs) of the staging buffer viewed as a record,
+ * hga_attend_decode with that view (d_sb = KVH*stage_groups*gs*Dh, d_sh = stage_groups*gs*Dh,
+ * d_ss = Dh, record_on_host 0) and open_grp = staged_grp attends exactly as with the record.
+ * scratch: int32[B*KVH*(stage_groups+1)] (slot lists and counts).
+ */
+int hga_gather_decode(const hga_config* cfg, int32_t n_closed, const int32_t* open_grp,
+                      const int32_t* open_thr, int32_t Kg, const void* k_record,
+                      const void* v_record, int64_t d_sb, int64_t d_sh, int64_t d_ss,
+                      int32_t record_on_host, void* stage_k, void* stage_v, int32_t stage_groups,
+                      int32_t* staged_grp, void* scratch, int64_t scratch_bytes, void* stream);
 
 #ifdef __cplusplus
 }

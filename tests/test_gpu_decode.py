@@ -243,7 +243,7 @@ def _ring(k, n_closed, C, kf, kl, R):
 
 @pytest.mark.parametrize("case", ATTN_CASES, ids=lambda c: f"B{c[0]}n{c[10]}c{c[11]}L{c[12]}"
                          f"{'bf16' if c[13] is torch.bfloat16 else 'f32'}")
-@pytest.mark.parametrize("tier", ["vram", "ram"])
+@pytest.mark.parametrize("tier", ["vram", "ram", "gather"])
 def test_attend_decode_vs_oracle(case, tier):
     B, H, KVH, Dh, C, gs, tc, tg, kf, kl, n_closed, c0, L, dt = case
     print(f"[decode] attend {tier} {case}", flush=True)
@@ -276,6 +276,16 @@ def test_attend_decode_vs_oracle(case, tier):
         hv[:, :, :n_closed * C] = v[:, :, :n_closed * C]
         out = ops.attend_decode(cfg, q.to(DEV), n_closed, start, rk.to(DEV), rv.to(DEV), R,
                                 fk.to(DEV), fv.to(DEV), hk, hv, True, og, ot, Kg)
+        if tier == "gather":
+            # opened groups staged in device memory: the same keys in the same order, so the
+            # result equals the zero-copy read bit for bit
+            staged = ops.gather_decode(cfg, n_closed, og, ot, Kg, hk, hv, True,
+                                       ops.DecodeStaging(), H)
+            out_g = ops.attend_decode(cfg, q.to(DEV), n_closed, start, rk.to(DEV), rv.to(DEV),
+                                      R, fk.to(DEV), fv.to(DEV), staged[0], staged[1], False,
+                                      staged[2], ot, Kg)
+            torch.cuda.synchronize()
+            assert torch.equal(out_g, out)
     torch.cuda.synchronize()
     ref = oracle.attend_decode(q.float().numpy(), k.float().numpy(), v.float().numpy(), C, gs,
                                kf, kl, n_closed, start, og.cpu().numpy(), ot.cpu().numpy(),
@@ -286,6 +296,48 @@ def test_attend_decode_vs_oracle(case, tier):
         assert d.max() <= BF16_MAX and d.mean() <= BF16_MEAN, (d.max(), d.mean())
     else:
         assert d.max() <= F32_TOL, d.max()
+
+
+@pytest.mark.parametrize("on_host", [True, False])
+def test_gather_decode_contents(on_host):
+    """Staged groups are the record's groups, one slot per distinct (b, kv head, group) in
+    ascending group order; every opened entry maps to its group's slot, padding to -1."""
+    B, H, KVH, Dh, C, gs, tc, tg, kf, kl = 2, 8, 2, 128, 64, 16, 8, 16, 1, 2
+    n_closed, dt = 40, torch.bfloat16
+    M = C // gs
+    gen = torch.Generator().manual_seed(17)
+    cfg = _cfg(B, H, KVH, Dh, C, gs, tc, tg, kf, kl, dt)
+    q = torch.randn(B, H, 1, Dh, generator=gen).to(dt)
+    ck, gk = _summaries(gen, B, KVH, n_closed, M, Dh, dt)
+    r = ops.route_decode(cfg, q.to(DEV), ck.to(DEV), gk.to(DEV), n_closed)
+    og, ot, Kg = r["open_grp"], r["open_thr"], r["Kg"]
+    k, v = _history(gen, B, KVH, n_closed * C, Dh, dt)
+    if on_host:
+        hk = torch.empty(B, KVH, n_closed * C, Dh, dtype=dt, pin_memory=True)
+        hv = torch.empty_like(hk).pin_memory()
+        hk.copy_(k)
+        hv.copy_(v)
+    else:
+        hk, hv = k.to(DEV), v.to(DEV)
+    sk, sv, sg = ops.gather_decode(cfg, n_closed, og, ot, Kg, hk, hv, on_host,
+                                   ops.DecodeStaging(), H)
+    torch.cuda.synchronize()
+    og_, ot_, sg_ = og.cpu().numpy(), ot.cpu().numpy(), sg.cpu().numpy()
+    sk_, sv_ = sk.cpu(), sv.cpu()
+    rep = H // KVH
+    for b in range(B):
+        for kvh in range(KVH):
+            ids = sorted({int(x) for h in range(kvh * rep, (kvh + 1) * rep)
+                          for x, t in zip(og_[b, h, :Kg], ot_[b, h, :Kg]) if x >= 0 and t >= 0})
+            for slot, grp in enumerate(ids):
+                p0 = (grp // M) * C + (grp % M) * gs
+                assert torch.equal(sk_[b, kvh, slot * gs:(slot + 1) * gs], k[b, kvh, p0:p0 + gs])
+                assert torch.equal(sv_[b, kvh, slot * gs:(slot + 1) * gs], v[b, kvh, p0:p0 + gs])
+            for h in range(kvh * rep, (kvh + 1) * rep):
+                for i in range(Kg):
+                    valid = og_[b, h, i] >= 0 and ot_[b, h, i] >= 0
+                    want = ids.index(int(og_[b, h, i])) if valid else -1
+                    assert sg_[b, h, i] == want
 
 
 def test_attend_decode_rejects_bad_blocks():
