@@ -69,18 +69,22 @@ struct KeySeq {
     }
 };
 
-// Maps a dispatch index to (b, h, n) such that the rep heads of one (b, kv head, n) are
-// consecutive blocks of one XCD (blocks are dispatched round-robin over the 8 XCDs).
-__device__ __forceinline__ void block_coords(int nblk, int B, int H, int N, int* b, int* h,
-                                             int* n) {
+// Maps a dispatch index to (b, h, n).  Blocks are dispatched round-robin over the 8 XCDs, each
+// with its own L2; every XCD takes a contiguous range of logical = ((b*KVH + kvh)*N + n)*rep +
+// h % rep, so an XCD works on one (b, kv head) -- or a chunk range of it -- at a time and the
+// opened groups its in-flight blocks share (same K/V) meet in its L2; the rep heads of one
+// (b, kv head, n) are consecutive blocks (shared windows and own chunk).
+__device__ __forceinline__ void block_coords(int nblk, int B, int H, int KVH, int N, int* b,
+                                             int* h, int* n) {
     const int bid = blockIdx.x, xcd = bid % 8, slot = bid / 8;
     const int q = nblk / 8, r = nblk % 8;
     const int logical = xcd < r ? xcd * (q + 1) + slot : r * (q + 1) + (xcd - r) * q + slot;
-    // logical = ((b * N + n) * H + h): heads innermost (heads of a KV head are contiguous)
-    *h = logical % H;
-    const int bn = logical / H;
-    *n = bn % N;
-    *b = bn / N;
+    const int rep = H / KVH;
+    const int t = logical / rep;
+    *n = t % N;
+    const int bk = t / N;
+    *b = bk / KVH;
+    *h = (bk % KVH) * rep + logical % rep;
 }
 
 __device__ __forceinline__ void setup_keys(const AttnArgs& A, int b, int h, int n, int rows,
@@ -132,7 +136,7 @@ __global__ __launch_bounds__(kAT) void attend_mfma_kernel(AttnArgs A) {
     int* sOT = sOpen + (A.Kg > 0 ? A.Kg : 1);
 
     int b, h, n;
-    block_coords(A.B * A.H * A.N, A.B, A.H, A.N, &b, &h, &n);
+    block_coords(A.B * A.H * A.N, A.B, A.H, A.KVH, A.N, &b, &h, &n);
     const int kvh = h / (A.H / A.KVH);
     int rows = A.S - n * A.C;
     if (rows > A.C) rows = A.C;
@@ -288,7 +292,7 @@ __global__ __launch_bounds__(kVT) void attend_valu_kernel(AttnArgs A) {
     int* sOG = sOpen;
     int* sOT = sOpen + (A.Kg > 0 ? A.Kg : 1);
     int b, h, n;
-    block_coords(A.B * A.H * A.N, A.B, A.H, A.N, &b, &h, &n);
+    block_coords(A.B * A.H * A.N, A.B, A.H, A.KVH, A.N, &b, &h, &n);
     const int kvh = h / (A.H / A.KVH);
     int rows = A.S - n * A.C;
     if (rows > A.C) rows = A.C;
@@ -451,7 +455,7 @@ __global__ __launch_bounds__(kV2Threads) void attend_v2_kernel(AttnArgs A,
     int* sPos = sTab;
     int* sThr = sTab + nb_cap;
     int b, h, n;
-    block_coords(A.B * A.H * A.N, A.B, A.H, A.N, &b, &h, &n);
+    block_coords(A.B * A.H * A.N, A.B, A.H, A.KVH, A.N, &b, &h, &n);
     const int kvh = h / (A.H / A.KVH);
     const int C = A.C, gs = A.gs, M = A.M;
     int rows = A.S - n * C;
