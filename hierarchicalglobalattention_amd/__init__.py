@@ -2,10 +2,13 @@
 the reference's HierarchicalGlobalAttentionRouted / ChunkRouter interfaces."""
 from ._lib import HgaError, build, lib
 from .routed_attention import HierarchicalGlobalAttentionRouted, RMSNorm
+from .qwen_routed_attention import (QwenRoutedAttention, replace_qwen_attention_with_router,
+                                    restore_original_attention)
 from .router import (ChunkPlacementPolicy, ChunkRouter, RamKVCacheStore, RoutedKV, RouterConfig,
                      VramKVCacheStore)
 
 __all__ = [
     "HierarchicalGlobalAttentionRouted", "RMSNorm", "ChunkPlacementPolicy", "ChunkRouter",
     "RoutedKV", "RouterConfig", "VramKVCacheStore", "RamKVCacheStore", "HgaError", "build", "lib",
+    "QwenRoutedAttention", "replace_qwen_attention_with_router", "restore_original_attention",
 ]

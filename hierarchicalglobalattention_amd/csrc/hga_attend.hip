@@ -18,6 +18,8 @@
 // hits.
 // fp32 path (and head_dim 16/32): one wave per query row at a time, VALU dot products, online
 // softmax across the wave.
+#include <algorithm>
+
 #include "hga_common.h"
 
 namespace hga {
@@ -746,9 +748,11 @@ extern "C" int hga_attend_prefill(const hga_config* cfg, int32_t S, const void* 
         const int Sp = (int)vt_keys(cfg, S);
         uint16_t* kbl = (uint16_t*)workspace;
         uint16_t* vbl = kbl + (int64_t)a.B * a.KVH * Sp * D;
-        // 16-key blocks of the longest key sequence, rounded up to whole 2-block tiles
+        // 16-key blocks of the longest key sequence, rounded up to whole 2-block tiles; the
+        // windows of chunk n cover min(kf, n) + (n - l_lo) <= min(kf + kl, N - 1) chunks
         const int bpc = a.C / 16;
-        const int nb_cap = ((a.kf + a.kl + 1) * bpc + Kg * (a.gs / 16) + 3) / 4 * 4;
+        const int64_t wch = std::min<int64_t>((int64_t)a.kf + a.kl, a.N - 1);
+        const int nb_cap = (int)(((wch + 1) * bpc + Kg * (a.gs / 16) + 3) / 4 * 4);
         // block table, then two stages of one tile (K and V of two 16-key blocks)
         const size_t lds2 = sizeof(int) * 2 * (size_t)nb_cap + 2 * 4 * 32 * (size_t)D;
         HGA_REQUIRE(lds2 <= 65536, HGA_ERR_UNSUPPORTED,

@@ -1,5 +1,8 @@
 // Rotate-half RoPE applied in fp32 and rounded to the activation dtype
-// (HierarchicalGlobalAttentionRouted.py:156-157, 219-223).  HBM-bound elementwise kernel:
+// (HierarchicalGlobalAttentionRouted.py:156-157, 219-223), or with every step rounded to the
+// activation dtype (x*cos, rotate_half(x)*sin and their sum, as transformers'
+// apply_rotary_pos_emb computes them on bf16 tensors: qwen_routed_attention.py:176, :80-84).
+// HBM-bound elementwise kernel:
 // each thread owns 4 consecutive dims of the first half and the matching 4 of the second half
 // of one row, so every load/store is an 8-byte (bf16) or 16-byte (fp32) vector access.
 // Built with -ffp-contract=off: x*cos and rot*sin are rounded separately, then added, as torch's
@@ -40,7 +43,7 @@ struct Vec4<HGA_DTYPE_F32> {
     static constexpr int kBytes = 4;
 };
 
-template <int DT>
+template <int DT, bool STEPS>
 __global__ __launch_bounds__(256) void rope_kernel(const char* x, int64_t x_sb, int64_t x_sh,
                                                    int64_t x_ss, char* out, int64_t o_sb,
                                                    int64_t o_sh, int64_t o_ss, const float* cos,
@@ -74,11 +77,17 @@ __global__ __launch_bounds__(256) void rope_kernel(const char* x, int64_t x_sb, 
     const float ss1[4] = {s1.x, s1.y, s1.z, s1.w}, ss2[4] = {s2.x, s2.y, s2.z, s2.w};
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-        const float a = x1[e] * cc1[e];
-        const float r1 = -x2[e] * ss1[e];
+        float a = x1[e] * cc1[e];
+        float r1 = -x2[e] * ss1[e];
+        float c = x2[e] * cc2[e];
+        float r2 = x1[e] * ss2[e];
+        if constexpr (STEPS) {
+            a = round_dt(a, DT);
+            r1 = round_dt(r1, DT);
+            c = round_dt(c, DT);
+            r2 = round_dt(r2, DT);
+        }
         o1[e] = a + r1;
-        const float c = x2[e] * cc2[e];
-        const float r2 = x1[e] * ss2[e];
         o2[e] = c + r2;
     }
     Vec4<DT>::st(orow + d0 * E, o1);
@@ -91,12 +100,13 @@ __global__ __launch_bounds__(256) void rope_kernel(const char* x, int64_t x_sb, 
 extern "C" int hga_rope(const hga_config* cfg, int32_t nheads, int32_t S, const void* x,
                         int64_t x_sb, int64_t x_sh, int64_t x_ss, void* out, int64_t o_sb,
                         int64_t o_sh, int64_t o_ss, const float* cos, const float* sin,
-                        int64_t cos_bstride, void* stream) {
+                        int64_t cos_bstride, int32_t flags, void* stream) {
     using namespace hga;
     int rc = check_config(cfg);
     if (rc) return rc;
     HGA_REQUIRE(x && out && cos && sin, HGA_ERR_ARG, "hga_rope: NULL pointer");
     HGA_REQUIRE(nheads > 0 && S >= 0, HGA_ERR_ARG, "hga_rope: bad nheads/S");
+    HGA_REQUIRE((flags & ~HGA_ROPE_STEPS_IN_DTYPE) == 0, HGA_ERR_ARG, "hga_rope: unknown flags");
     if (S == 0) return HGA_OK;
     const int Dh = cfg->head_dim;
     const int E = cfg->dtype == HGA_DTYPE_BF16 ? 2 : 4;
@@ -109,13 +119,17 @@ extern "C" int hga_rope(const hga_config* cfg, int32_t nheads, int32_t S, const 
     const int64_t nrows = (int64_t)cfg->batch * nheads * S;
     const int64_t grid = (nrows + rpb - 1) / rpb;
     hipStream_t st = (hipStream_t)stream;
-    if (cfg->dtype == HGA_DTYPE_BF16)
-        rope_kernel<HGA_DTYPE_BF16><<<dim3((unsigned)grid), dim3(256), 0, st>>>(
-            (const char*)x, x_sb, x_sh, x_ss, (char*)out, o_sb, o_sh, o_ss, cos, sin,
-            cos_bstride, nheads, S, Dh, nrows);
-    else
-        rope_kernel<HGA_DTYPE_F32><<<dim3((unsigned)grid), dim3(256), 0, st>>>(
-            (const char*)x, x_sb, x_sh, x_ss, (char*)out, o_sb, o_sh, o_ss, cos, sin,
-            cos_bstride, nheads, S, Dh, nrows);
+    const bool steps = (flags & HGA_ROPE_STEPS_IN_DTYPE) != 0;
+    auto launch = [&](auto kern) {
+        kern<<<dim3((unsigned)grid), dim3(256), 0, st>>>((const char*)x, x_sb, x_sh, x_ss,
+                                                         (char*)out, o_sb, o_sh, o_ss, cos, sin,
+                                                         cos_bstride, nheads, S, Dh, nrows);
+    };
+    if (cfg->dtype == HGA_DTYPE_BF16) {
+        if (steps) launch(rope_kernel<HGA_DTYPE_BF16, true>);
+        else launch(rope_kernel<HGA_DTYPE_BF16, false>);
+    } else {
+        launch(rope_kernel<HGA_DTYPE_F32, false>);   // fp32: every step is already fp32
+    }
     return launch_status("hga_rope");
 }

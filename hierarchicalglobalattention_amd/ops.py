@@ -80,9 +80,15 @@ def prefill_widths(cfg: HgaConfig, S: int):
     return n.value, kc.value, kg.value
 
 
+ROPE_STEPS_IN_DTYPE = 1
+
+
 def rope(cfg: HgaConfig, x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor,
-         out: torch.Tensor | None = None) -> torch.Tensor:
-    """Rotate-half RoPE of x [B, X, S, Dh] with fp32 tables cos/sin [S, Dh] or [B, S, Dh]."""
+         out: torch.Tensor | None = None, steps_in_dtype: bool = False) -> torch.Tensor:
+    """Rotate-half RoPE of x [B, X, S, Dh] with tables cos/sin [S, Dh] or [B, S, Dh] (any float
+    dtype; used as fp32).  ``steps_in_dtype`` rounds x*cos, rotate_half(x)*sin and their sum to
+    x's dtype one by one (transformers' apply_rotary_pos_emb on bf16 tensors); otherwise the
+    rotation is computed in fp32 and rounded once."""
     _dev(x, cos, sin)
     B, X, S, D = x.shape
     if out is None:
@@ -93,7 +99,8 @@ def rope(cfg: HgaConfig, x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor,
         raise ValueError(f"rotary table {tuple(cos.shape)} does not cover [{S}, {D}]")
     cb = 0 if cos.dim() == 2 or cos.shape[0] == 1 else S * D
     check(lib().hga_rope(ctypes.byref(cfg), X, S, _p(x), *_s4(x), _p(out), *_s4(out), _p(cos),
-                         _p(sin), cb, _stream()), "hga_rope")
+                         _p(sin), cb, ROPE_STEPS_IN_DTYPE if steps_in_dtype else 0, _stream()),
+          "hga_rope")
     return out
 
 

@@ -494,7 +494,9 @@ class ChunkRouter:
             # routing summaries with the activation-dtype table, store summaries with the fp32
             # table written straight into the store tables (one pass over the keys)
             cf, sf = rotary_for_positions(cfg.theta, D, 0, S, dev)
-            ck, gk = torch.empty_like(st.chunk_k[:, :, :N]), torch.empty_like(st.group_k[:, :, :N])
+            # same strides as the store tables (one stride set for both output pairs)
+            ck = torch.empty_like(st.chunk_k)[:, :, :N]
+            gk = torch.empty_like(st.group_k)[:, :, :N]
             ck, gk, ck_s, gk_s = ops.summarize(hc, k_raw, k_rope, cos_r, sin_r, chunk_k=ck,
                                                group_k=gk, cos_b=cf, sin_b=sf,
                                                chunk_k_b=st.chunk_k[:, :, :N],

@@ -66,14 +66,22 @@ int32_t hga_prefill_widths(const hga_config* cfg, int32_t S, int32_t* N, int32_t
                            int32_t* Kg);
 
 /*
- * Rotate-half RoPE in fp32, rounded to the activation dtype:
- *   out = x*cos + cat(-x2, x1)*sin    (HierarchicalGlobalAttentionRouted.py:156-157, 219-223)
+ * Rotate-half RoPE:
+ *   out = x*cos + cat(-x2, x1)*sin
+ * flags = 0: computed in fp32 and rounded once to the activation dtype
+ *   (HierarchicalGlobalAttentionRouted.py:156-157, 219-223);
+ * flags = HGA_ROPE_STEPS_IN_DTYPE: each product and the sum rounded to the activation dtype,
+ *   as transformers' apply_rotary_pos_emb computes it on bf16 tensors (the Qwen3 drop-in,
+ *   Qwen3LongContext/qwen_routed_attention.py:176, and its DCA twin :80-84).
  * x/out: [B, nheads, S, Dh] views; cos/sin: fp32 [Bc, S, Dh] rows of the rotary table for the
- * block's positions, cos_bstride = 0 (shared) or the batch stride in elements.
+ * block's positions (bf16-valued when the model's table is bf16), cos_bstride = 0 (shared) or
+ * the batch stride in elements.
  */
+#define HGA_ROPE_STEPS_IN_DTYPE 1
 int hga_rope(const hga_config* cfg, int32_t nheads, int32_t S, const void* x, int64_t x_sb,
              int64_t x_sh, int64_t x_ss, void* out, int64_t o_sb, int64_t o_sh, int64_t o_ss,
-             const float* cos, const float* sin, int64_t cos_bstride, void* stream);
+             const float* cos, const float* sin, int64_t cos_bstride, int32_t flags,
+             void* stream);
 
 /*
  * Mixed-RoPE chunk and group key summaries at KV-head granularity

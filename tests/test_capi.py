@@ -52,10 +52,10 @@ def test_errors_reported_without_launch():
     assert lib.hga_prefill_widths(ctypes.byref(cfg), 100, None, None, None) == -2
     cfg.head_dim = 64
     z = ctypes.c_void_p(0)
-    rc = lib.hga_rope(ctypes.byref(cfg), 2, 10, z, 0, 0, 0, z, 0, 0, 0, z, z, 0, z)
+    rc = lib.hga_rope(ctypes.byref(cfg), 2, 10, z, 0, 0, 0, z, 0, 0, 0, z, z, 0, 0, z)
     assert rc == -1 and b"NULL" in lib.hga_last_error()
     with pytest.raises(_lib.HgaError):
-        _lib.check(lib.hga_rope(ctypes.byref(cfg), 2, 10, z, 0, 0, 0, z, 0, 0, 0, z, z, 0, z),
+        _lib.check(lib.hga_rope(ctypes.byref(cfg), 2, 10, z, 0, 0, 0, z, 0, 0, 0, z, z, 0, 0, z),
                    "hga_rope")
 
 
