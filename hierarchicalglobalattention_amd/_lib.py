@@ -54,6 +54,10 @@ SIGNATURES = {
                            _i64, _i32, _vp, _vp, _i64, _i64, _i64, _vp, _vp, _i64, _i64, _i64,
                            _i32, _vp, _vp, _i32, _vp, _i64, _i64, _i64, _vp, _i64, _vp],
                           ctypes.c_int),
+    "hga_attend_decode_dca": ([_CFG, _i32, _i32, _i64, _vp, _vp, _vp, _i64, _i64, _i64, _i32,
+                               _vp, _vp, _i64, _i64, _i64, _i32, _vp, _vp, _i64, _i64, _i64,
+                               _vp, _vp, _i64, _i64, _i64, _i32, _vp, _vp, _vp, _i32, _vp, _i64,
+                               _i64, _i64, _vp, _i64, _vp], ctypes.c_int),
     "hga_attend_decode_workspace": ([_CFG, _i32, _i32, _i64, _i32,
                                      ctypes.POINTER(ctypes.c_int64)], _i32),
     "hga_gather_decode_sizes": ([_CFG, _i32, _I32P, ctypes.POINTER(ctypes.c_int64),

@@ -272,6 +272,12 @@ struct DecAttnArgs {
     int64_t start_pos;
     int B, H, KVH, L, n_closed, C, gs, M, kf, kl, Kg, ring;
     float scale;
+    // Dual Chunk Attention (DCA kernels only): fp32 query rows RoPE'd at the intra, successive and
+    // inter positions (strides q_sb/q_sh/q_ss), the opened groups' own ids for key positions
+    // (the list attention reads may hold staging slots), the DCA chunk length
+    const float* q_dca[3];
+    const int32_t* open_pos;
+    int dca_chunk;
 };
 
 // The key sequence of a decode block for (b, query head): [first window | last window | opened
@@ -281,7 +287,7 @@ template <class T>
 struct DecKeys {
     const T *kr, *vr, *kf, *vf, *kd, *vd;
     int64_t r_ss, f_ss, d_ss, c0;
-    const int *sOG, *sOT;
+    const int *sOG, *sOT, *sOP;
     int a1, a2, a3, a4, C, gs, M, n_closed, l_lo, ring;
 
     __device__ void init(const DecAttnArgs& A, int b, int kvh, const int* og, const int* ot,
@@ -289,7 +295,7 @@ struct DecKeys {
         int f_hi;
         windows(A.n_closed, A.kf, A.kl, &f_hi, &l_lo);
         C = A.C; gs = A.gs; M = A.M; n_closed = A.n_closed; ring = A.ring;
-        sOG = og; sOT = ot;
+        sOG = og; sOT = ot; sOP = og;
         c0 = A.start_pos - (int64_t)A.n_closed * C;
         a1 = f_hi * C;
         a2 = a1 + (A.n_closed - l_lo) * C;
@@ -303,11 +309,13 @@ struct DecKeys {
         vd = reinterpret_cast<const T*>(A.vd) + b * A.d_sb + kvh * A.d_sh;
         r_ss = A.r_ss; f_ss = A.f_ss; d_ss = A.d_ss;
     }
-    __device__ void locate(int k, const T*& kp, const T*& vp, int& thr) const {
+    // kpos: the key's absolute position (opened groups: from sOP, the groups' own ids)
+    __device__ void locate(int k, const T*& kp, const T*& vp, int& thr, int64_t& kpos) const {
         if (k < a1) {
             kp = kf + (int64_t)k * f_ss;
             vp = vf + (int64_t)k * f_ss;
             thr = 0;
+            kpos = k;
             return;
         }
         int64_t pos;
@@ -319,12 +327,15 @@ struct DecKeys {
             if (grp < 0 || grp >= n_closed * M || sOT[g] < 0) {   // padding / invalid id
                 kp = vp = nullptr;
                 thr = kNoRow;
+                kpos = 0;
                 return;
             }
             const int64_t p = (int64_t)(grp / M) * C + (grp % M) * gs + e;
             kp = kd + p * d_ss;
             vp = vd + p * d_ss;
             thr = sOT[g];
+            const int gp = sOP[g];
+            kpos = (int64_t)(gp / M) * C + (gp % M) * gs + e;
             return;
         } else {
             pos = (int64_t)n_closed * C + (k - a3);
@@ -334,23 +345,37 @@ struct DecKeys {
         const int64_t slot = ring > 0 ? ((pos / C) % ring) * C + pos % C : pos;
         kp = kr + slot * r_ss;
         vp = vr + slot * r_ss;
+        kpos = pos;
+    }
+    __device__ void locate(int k, const T*& kp, const T*& vp, int& thr) const {
+        int64_t kpos;
+        locate(k, kp, vp, thr, kpos);
     }
 };
 
-template <int DT, int DH>
+// DCA regime of a key for a query at qpos: 0 same DCA chunk, 1 the one before, 2 older
+// (qwen_routed_attention.py:274-278)
+__device__ __forceinline__ int dca_regime(int64_t kpos, int64_t qpos, int L_c) {
+    const int64_t ck = kpos / L_c, cq = qpos / L_c;
+    return ck == cq ? 0 : (ck == cq - 1 ? 1 : 2);
+}
+
+template <int DT, int DH, bool DCA>
 __global__ __launch_bounds__(kDT) void attend_decode_kernel(DecAttnArgs A) {
     typedef typename Elem<DT>::T T;
     constexpr int DPL = DH / kWave > 0 ? DH / kWave : 1;   // dims per lane
-    __shared__ float sQ[DH];
+    constexpr int NQ = DCA ? 3 : 1;                          // query versions
+    __shared__ float sQv[NQ][DH];
     __shared__ float sM[kDW], sLs[kDW];
     __shared__ float sAcc[kDW][DH];
-    __shared__ int sOG[256], sOT[256];
+    __shared__ int sOG[256], sOT[256], sOP[DCA ? 256 : 1];
     const int bh = blockIdx.x, b = bh / A.H, h = bh % A.H, kvh = h / (A.H / A.KVH);
     const int w = threadIdx.x / kWave, l = lane_id();
     const int Kgw = A.Kg > 0 ? A.Kg : 1;
     for (int i = threadIdx.x; i < A.Kg; i += kDT) {
         sOG[i] = A.open_grp[(int64_t)bh * Kgw + i];
         sOT[i] = A.open_thr[(int64_t)bh * Kgw + i];
+        if constexpr (DCA) sOP[i] = A.open_pos[(int64_t)bh * Kgw + i];
     }
     __syncthreads();
     int nopen = 0;
@@ -358,14 +383,22 @@ __global__ __launch_bounds__(kDT) void attend_decode_kernel(DecAttnArgs A) {
         if (sOG[i] >= 0 && sOT[i] >= 0) nopen = i + 1;
     DecKeys<T> keys;
     keys.init(A, b, kvh, sOG, sOT, nopen);
+    if constexpr (DCA) keys.sOP = sOP;
     const int a4 = keys.a4;
-    auto key = [&](int k, const T*& kp, const T*& vp, int& thr) { keys.locate(k, kp, vp, thr); };
     const int per = (a4 + kDW - 1) / kDW;
     const int k_lo = w * per, k_hi = (w + 1) * per < a4 ? (w + 1) * per : a4;
     const T* qg = reinterpret_cast<const T*>(A.q) + b * A.q_sb + h * A.q_sh;
     T* og = reinterpret_cast<T*>(A.out) + b * A.o_sb + h * A.o_sh;
     for (int row = 0; row < A.L; ++row) {
-        for (int d = threadIdx.x; d < DH; d += kDT) sQ[d] = Elem<DT>::ld(qg, (int64_t)row * A.q_ss + d);
+        for (int d = threadIdx.x; d < DH; d += kDT) {
+            const int64_t o = (int64_t)row * A.q_ss + d;
+            if constexpr (DCA) {
+#pragma unroll
+                for (int r = 0; r < 3; ++r) sQv[r][d] = A.q_dca[r][b * A.q_sb + h * A.q_sh + o];
+            } else {
+                sQv[0][d] = Elem<DT>::ld(qg, o);
+            }
+        }
         __syncthreads();
         float m_run = -INFINITY, l_run = 0.0f, acc[DPL];
 #pragma unroll
@@ -375,7 +408,9 @@ __global__ __launch_bounds__(kDT) void attend_decode_kernel(DecAttnArgs A) {
             const T* kp = nullptr;
             const T* vp = nullptr;
             int thr = kNoRow;
-            if (k < k_hi) key(k, kp, vp, thr);
+            int64_t kpos = 0;
+            if (k < k_hi) keys.locate(k, kp, vp, thr, kpos);
+            const float* sQ = sQv[DCA ? dca_regime(kpos, A.start_pos + row, A.dca_chunk) : 0];
             float s = -INFINITY;
             if (k < k_hi && row >= thr) {
                 float d0 = 0.0f;
@@ -493,7 +528,7 @@ __device__ __forceinline__ void load_slice(const typename Elem<DT>::T* p, float 
     }
 }
 
-template <int DT, int DH>
+template <int DT, int DH, bool DCA>
 __global__ __launch_bounds__(kDT) void attend_decode_split_kernel(DecAttnArgs A, float* part,
                                                                   int nsplit) {
     typedef typename Elem<DT>::T T;
@@ -501,7 +536,8 @@ __global__ __launch_bounds__(kDT) void attend_decode_split_kernel(DecAttnArgs A,
     constexpr int NG = kDT / 16;                     // 16-lane groups per workgroup
     constexpr int KPG = kSplitKeys / NG;             // keys per group
     constexpr int U = 4;                             // keys in flight per group
-    __shared__ int sOG[256], sOT[256];
+    constexpr int NQ = DCA ? 3 : 1;                  // query versions
+    __shared__ int sOG[256], sOT[256], sOP[DCA ? 256 : 1];
     __shared__ float sM[NG], sL[NG];
     __shared__ float sAcc[NG][DH];
     const int split = blockIdx.x, bh = blockIdx.y, b = bh / A.H, h = bh % A.H;
@@ -511,6 +547,7 @@ __global__ __launch_bounds__(kDT) void attend_decode_split_kernel(DecAttnArgs A,
     for (int i = threadIdx.x; i < A.Kg; i += kDT) {
         sOG[i] = A.open_grp[(int64_t)bh * Kgw + i];
         sOT[i] = A.open_thr[(int64_t)bh * Kgw + i];
+        if constexpr (DCA) sOP[i] = A.open_pos[(int64_t)bh * Kgw + i];
     }
     __syncthreads();
     int nopen = 0;
@@ -518,12 +555,21 @@ __global__ __launch_bounds__(kDT) void attend_decode_split_kernel(DecAttnArgs A,
         if (sOG[i] >= 0 && sOT[i] >= 0) nopen = i + 1;
     DecKeys<T> keys;
     keys.init(A, b, kvh, sOG, sOT, nopen);
+    if constexpr (DCA) keys.sOP = sOP;
     const int gk0 = split * kSplitKeys + G * KPG;
     const T* qg = reinterpret_cast<const T*>(A.q) + b * A.q_sb + h * A.q_sh;
     for (int row = 0; row < A.L; ++row) {
-        float qv[DPL];
+        float qvs[NQ][DPL];
 #pragma unroll
-        for (int e = 0; e < DPL; ++e) qv[e] = Elem<DT>::ld(qg, (int64_t)row * A.q_ss + j * DPL + e);
+        for (int e = 0; e < DPL; ++e) {
+            const int64_t o = (int64_t)row * A.q_ss + j * DPL + e;
+            if constexpr (DCA) {
+#pragma unroll
+                for (int r = 0; r < 3; ++r) qvs[r][e] = A.q_dca[r][b * A.q_sb + h * A.q_sh + o];
+            } else {
+                qvs[0][e] = Elem<DT>::ld(qg, o);
+            }
+        }
         float m_run = -INFINITY, l_run = 0.0f, acc[DPL];
 #pragma unroll
         for (int e = 0; e < DPL; ++e) acc[e] = 0.0f;
@@ -536,14 +582,24 @@ __global__ __launch_bounds__(kDT) void attend_decode_split_kernel(DecAttnArgs A,
                 const T* kp = nullptr;
                 vp[u] = nullptr;
                 int thr = kNoRow;
-                if (k < keys.a4) keys.locate(k, kp, vp[u], thr);
+                int64_t kpos = 0;
+                if (k < keys.a4) keys.locate(k, kp, vp[u], thr, kpos);
                 float d = 0.0f;
                 const bool vis = k < keys.a4 && row >= thr;
                 if (vis) {
                     float kx[DPL];
                     load_slice<DT, DPL>(kp + j * DPL, kx);
+                    if constexpr (DCA) {
+                        const int r = dca_regime(kpos, A.start_pos + row, A.dca_chunk);
 #pragma unroll
-                    for (int e = 0; e < DPL; ++e) d = fmaf(qv[e], kx[e], d);
+                        for (int e = 0; e < DPL; ++e) {
+                            const float qe = r == 0 ? qvs[0][e] : (r == 1 ? qvs[1][e] : qvs[2][e]);
+                            d = fmaf(qe, kx[e], d);
+                        }
+                    } else {
+#pragma unroll
+                        for (int e = 0; e < DPL; ++e) d = fmaf(qvs[0][e], kx[e], d);
+                    }
                 }
                 d = r16_sum_f(d);                    // whole group: uniform control flow
                 s[u] = vis ? d * A.scale : -INFINITY;
@@ -924,21 +980,23 @@ extern "C" int hga_route_decode(const hga_config* cfg, int32_t L, int32_t n_clos
     return HGA_ERR_UNSUPPORTED;
 }
 
-extern "C" int hga_attend_decode(const hga_config* cfg, int32_t L, int32_t n_closed,
-                                 int64_t start_pos, const void* q, int64_t q_sb, int64_t q_sh,
-                                 int64_t q_ss, const void* k_recent, const void* v_recent,
-                                 int64_t r_sb, int64_t r_sh, int64_t r_ss, int32_t ring_chunks,
-                                 const void* k_first, const void* v_first, int64_t f_sb,
-                                 int64_t f_sh, int64_t f_ss, const void* k_record,
-                                 const void* v_record, int64_t d_sb, int64_t d_sh, int64_t d_ss,
-                                 int32_t record_on_host, const int32_t* open_grp,
-                                 const int32_t* open_thr, int32_t Kg, void* out, int64_t o_sb,
-                                 int64_t o_sh, int64_t o_ss, void* workspace,
-                                 int64_t workspace_bytes, void* stream) {
-    using namespace hga;
+namespace hga {
+namespace {
+// Body of hga_attend_decode and hga_attend_decode_dca (q_dca == nullptr: plain attention).
+int attend_decode_impl(const hga_config* cfg, int32_t L, int32_t n_closed, int64_t start_pos,
+                       const void* q, int64_t q_sb, int64_t q_sh, int64_t q_ss,
+                       const float* const* q_dca, const int32_t* open_pos, int32_t dca_chunk,
+                       const void* k_recent, const void* v_recent, int64_t r_sb, int64_t r_sh,
+                       int64_t r_ss, int32_t ring_chunks, const void* k_first,
+                       const void* v_first, int64_t f_sb, int64_t f_sh, int64_t f_ss,
+                       const void* k_record, const void* v_record, int64_t d_sb, int64_t d_sh,
+                       int64_t d_ss, int32_t record_on_host, const int32_t* open_grp,
+                       const int32_t* open_thr, int32_t Kg, void* out, int64_t o_sb,
+                       int64_t o_sh, int64_t o_ss, void* workspace, int64_t workspace_bytes,
+                       void* stream) {
     int rc = check_config(cfg);
     if (rc) return rc;
-    HGA_REQUIRE(q && k_recent && v_recent && out && open_grp && open_thr, HGA_ERR_ARG,
+    HGA_REQUIRE((q || q_dca) && k_recent && v_recent && out && open_grp && open_thr, HGA_ERR_ARG,
                 "hga_attend_decode: NULL pointer");
     HGA_REQUIRE(L >= 1 && L <= kMaxL && n_closed >= 0 && Kg >= 0 && Kg <= 256 && ring_chunks >= 0,
                 HGA_ERR_ARG, "hga_attend_decode: bad L/n_closed/Kg/ring");
@@ -953,8 +1011,22 @@ extern "C" int hga_attend_decode(const hga_config* cfg, int32_t L, int32_t n_clo
     HGA_REQUIRE(ring_chunks == 0 || ring_chunks >= n_closed - l_lo + 1, HGA_ERR_ARG,
                 "hga_attend_decode: ring of %d chunks cannot hold the last window + active chunk",
                 ring_chunks);
+    const bool dca = q_dca != nullptr;
+    if (dca) {
+        HGA_REQUIRE(q_dca[0] && q_dca[1] && q_dca[2], HGA_ERR_ARG,
+                    "hga_attend_decode_dca: NULL query version");
+        HGA_REQUIRE(dca_chunk > 0 && dca_chunk % C == 0, HGA_ERR_ARG,
+                    "hga_attend_decode_dca: dca_chunk %d must be a positive multiple of the chunk "
+                    "size %d", dca_chunk, C);
+    }
     DecAttnArgs a{};
-    a.q = q; a.q_sb = q_sb; a.q_sh = q_sh; a.q_ss = q_ss;
+    a.q = q ? q : (dca ? q_dca[0] : nullptr);
+    a.q_sb = q_sb; a.q_sh = q_sh; a.q_ss = q_ss;
+    if (dca) {
+        for (int r = 0; r < 3; ++r) a.q_dca[r] = q_dca[r];
+        a.open_pos = open_pos ? open_pos : open_grp;
+        a.dca_chunk = dca_chunk;
+    }
     a.kr = k_recent; a.vr = v_recent; a.r_sb = r_sb; a.r_sh = r_sh; a.r_ss = r_ss;
     a.kfst = k_first ? k_first : k_recent; a.vfst = v_first ? v_first : v_recent;
     a.f_sb = f_sb; a.f_sh = f_sh; a.f_ss = f_ss;
@@ -991,7 +1063,8 @@ extern "C" int hga_attend_decode(const hga_config* cfg, int32_t L, int32_t n_clo
         const dim3 g1((unsigned)nsplit, (unsigned)(a.B * a.H)), g2((unsigned)(a.B * a.H * L));
 #define HGA_DS_CASE(DTV, DHV)                                                                    \
         if (cfg->dtype == DTV && D == DHV) {                                                   \
-            attend_decode_split_kernel<DTV, DHV><<<g1, kDT, 0, st>>>(a, part, nsplit);          \
+            if (dca) attend_decode_split_kernel<DTV, DHV, true><<<g1, kDT, 0, st>>>(a, part, nsplit); \
+            else attend_decode_split_kernel<DTV, DHV, false><<<g1, kDT, 0, st>>>(a, part, nsplit); \
             rc = launch_status("hga_attend_decode (split)");                                    \
             if (rc) return rc;                                                                  \
             decode_combine_kernel<DTV, DHV><<<g2, 128, 0, st>>>(a, part, nsplit);               \
@@ -1004,8 +1077,12 @@ extern "C" int hga_attend_decode(const hga_config* cfg, int32_t L, int32_t n_clo
 #undef HGA_DS_CASE
     }
     const unsigned grid = (unsigned)(a.B * a.H);
-#define HGA_DA_CASE(DTV, DHV) \
-    if (cfg->dtype == DTV && D == DHV) { attend_decode_kernel<DTV, DHV><<<grid, kDT, 0, st>>>(a); return launch_status("hga_attend_decode"); }
+#define HGA_DA_CASE(DTV, DHV)                                                                    \
+    if (cfg->dtype == DTV && D == DHV) {                                                       \
+        if (dca) attend_decode_kernel<DTV, DHV, true><<<grid, kDT, 0, st>>>(a);                \
+        else attend_decode_kernel<DTV, DHV, false><<<grid, kDT, 0, st>>>(a);                   \
+        return launch_status("hga_attend_decode");                                             \
+    }
     HGA_DA_CASE(HGA_DTYPE_BF16, 128)
     HGA_DA_CASE(HGA_DTYPE_BF16, 64)
     HGA_DA_CASE(HGA_DTYPE_BF16, 32)
@@ -1017,4 +1094,47 @@ extern "C" int hga_attend_decode(const hga_config* cfg, int32_t L, int32_t n_clo
 #undef HGA_DA_CASE
     set_error("hga_attend_decode: unsupported dtype/head_dim");
     return HGA_ERR_UNSUPPORTED;
+}
+}  // namespace
+}  // namespace hga
+
+extern "C" int hga_attend_decode(const hga_config* cfg, int32_t L, int32_t n_closed,
+                                 int64_t start_pos, const void* q, int64_t q_sb, int64_t q_sh,
+                                 int64_t q_ss, const void* k_recent, const void* v_recent,
+                                 int64_t r_sb, int64_t r_sh, int64_t r_ss, int32_t ring_chunks,
+                                 const void* k_first, const void* v_first, int64_t f_sb,
+                                 int64_t f_sh, int64_t f_ss, const void* k_record,
+                                 const void* v_record, int64_t d_sb, int64_t d_sh, int64_t d_ss,
+                                 int32_t record_on_host, const int32_t* open_grp,
+                                 const int32_t* open_thr, int32_t Kg, void* out, int64_t o_sb,
+                                 int64_t o_sh, int64_t o_ss, void* workspace,
+                                 int64_t workspace_bytes, void* stream) {
+    HGA_REQUIRE(q, HGA_ERR_ARG, "hga_attend_decode: NULL pointer");
+    return hga::attend_decode_impl(cfg, L, n_closed, start_pos, q, q_sb, q_sh, q_ss, nullptr,
+                                   nullptr, 0, k_recent, v_recent, r_sb, r_sh, r_ss, ring_chunks,
+                                   k_first, v_first, f_sb, f_sh, f_ss, k_record, v_record, d_sb,
+                                   d_sh, d_ss, record_on_host, open_grp, open_thr, Kg, out, o_sb,
+                                   o_sh, o_ss, workspace, workspace_bytes, stream);
+}
+
+extern "C" int hga_attend_decode_dca(const hga_config* cfg, int32_t L, int32_t n_closed,
+                                     int64_t start_pos, const float* q_intra,
+                                     const float* q_succ, const float* q_inter, int64_t q_sb,
+                                     int64_t q_sh, int64_t q_ss, int32_t dca_chunk,
+                                     const void* k_recent, const void* v_recent, int64_t r_sb,
+                                     int64_t r_sh, int64_t r_ss, int32_t ring_chunks,
+                                     const void* k_first, const void* v_first, int64_t f_sb,
+                                     int64_t f_sh, int64_t f_ss, const void* k_record,
+                                     const void* v_record, int64_t d_sb, int64_t d_sh,
+                                     int64_t d_ss, int32_t record_on_host,
+                                     const int32_t* open_grp, const int32_t* open_pos,
+                                     const int32_t* open_thr, int32_t Kg, void* out, int64_t o_sb,
+                                     int64_t o_sh, int64_t o_ss, void* workspace,
+                                     int64_t workspace_bytes, void* stream) {
+    const float* qd[3] = {q_intra, q_succ, q_inter};
+    return hga::attend_decode_impl(cfg, L, n_closed, start_pos, nullptr, q_sb, q_sh, q_ss, qd,
+                                   open_pos, dca_chunk, k_recent, v_recent, r_sb, r_sh, r_ss,
+                                   ring_chunks, k_first, v_first, f_sb, f_sh, f_ss, k_record,
+                                   v_record, d_sb, d_sh, d_ss, record_on_host, open_grp, open_thr,
+                                   Kg, out, o_sb, o_sh, o_ss, workspace, workspace_bytes, stream);
 }

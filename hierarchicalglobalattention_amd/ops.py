@@ -294,15 +294,21 @@ def attend_decode(cfg: HgaConfig, q: torch.Tensor, n_closed: int, start_pos: int
                   recent_k: torch.Tensor, recent_v: torch.Tensor, ring_chunks: int,
                   first_k, first_v, record_k, record_v, record_on_host: bool,
                   open_grp: torch.Tensor, open_thr: torch.Tensor, Kg: int,
-                  out: torch.Tensor | None = None) -> torch.Tensor:
+                  out: torch.Tensor | None = None, dca: dict | None = None) -> torch.Tensor:
     """Decode attention of q [B,H,L,Dh] (rows at start_pos..start_pos+L-1).  Token sources are
     [B,KVH,T,Dh] views: ``recent`` (positions >= the last window, optionally a ring of
     ring_chunks chunks), ``first`` (the first window) and ``record`` (the closed-token record
-    read for opened groups; a pinned host tensor when record_on_host)."""
+    read for opened groups; a pinned host tensor when record_on_host).
+
+    ``dca`` selects Dual Chunk Attention: q is then the fp32 intra version and ``dca`` holds
+    ``q_succ``/``q_inter`` (fp32, q's shape and strides), ``chunk`` (the DCA chunk length) and
+    ``open_pos`` (the opened groups' own ids when open_grp indexes a staging record, else None);
+    the output has the keys' dtype."""
     _dev(q, recent_k, recent_v, open_grp, open_thr)
     B, H, L, D = q.shape
     if out is None:
-        out = torch.empty((B, H, L, D), dtype=q.dtype, device=q.device)
+        out = torch.empty((B, H, L, D), dtype=recent_k.dtype if dca else q.dtype,
+                          device=q.device)
     if first_k is None:
         first_k, first_v = recent_k, recent_v
     if record_k is None:
@@ -320,9 +326,23 @@ def attend_decode(cfg: HgaConfig, q: torch.Tensor, n_closed: int, start_pos: int
     check(lib().hga_attend_decode_workspace(ctypes.byref(cfg), L, n_closed, start_pos, Kg,
                                             ctypes.byref(nb)), "hga_attend_decode_workspace")
     ws = torch.empty(max(nb.value, 16), dtype=torch.uint8, device=q.device)
-    check(lib().hga_attend_decode(
-        ctypes.byref(cfg), L, n_closed, start_pos, _p(q), *_s4(q), _p(recent_k), _p(recent_v),
-        *_s4(recent_k), ring_chunks, _p(first_k), _p(first_v), *_s4(first_k), _p(record_k),
-        _p(record_v), *_s4(record_k), 1 if record_on_host else 0, _p(og), _p(ot), Kg, _p(out),
-        *_s4(out), _p(ws), ws.numel(), _stream()), "hga_attend_decode")
+    src = (_p(recent_k), _p(recent_v), *_s4(recent_k), ring_chunks, _p(first_k), _p(first_v),
+           *_s4(first_k), _p(record_k), _p(record_v), *_s4(record_k),
+           1 if record_on_host else 0)
+    if dca is None:
+        check(lib().hga_attend_decode(
+            ctypes.byref(cfg), L, n_closed, start_pos, _p(q), *_s4(q), *src, _p(og), _p(ot), Kg,
+            _p(out), *_s4(out), _p(ws), ws.numel(), _stream()), "hga_attend_decode")
+        return out
+    qs, qt = dca["q_succ"], dca["q_inter"]
+    _dev(qs, qt)
+    for t in (q, qs, qt):
+        if t.dtype != torch.float32 or t.stride() != q.stride() or t.shape != q.shape:
+            raise ValueError("DCA query versions must be fp32 views of one shape and strides")
+    op = dca.get("open_pos")
+    op = op.contiguous() if op is not None else None
+    check(lib().hga_attend_decode_dca(
+        ctypes.byref(cfg), L, n_closed, start_pos, _p(q), _p(qs), _p(qt), *_s4(q),
+        int(dca["chunk"]), *src, _p(og), _p(op) if op is not None else None, _p(ot), Kg,
+        _p(out), *_s4(out), _p(ws), ws.numel(), _stream()), "hga_attend_decode_dca")
     return out

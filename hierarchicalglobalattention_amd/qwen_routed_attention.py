@@ -38,6 +38,18 @@ def _rope_theta(config: Any) -> float:
     return float(theta)
 
 
+def _dca_rope(positions: torch.Tensor, head_dim: int, theta: float, device: torch.device,
+              dtype: torch.dtype) -> Tuple[torch.Tensor, torch.Tensor]:
+    """Default-RoPE cos/sin rows [len, Dh] for arbitrary (DCA-remapped) positions: the model's
+    inv_freq = theta**-(2i/Dh) evaluated at the given positions, in ``dtype``
+    (qwen_routed_attention.py:61-77)."""
+    half = head_dim // 2
+    inv = 1.0 / (theta ** (torch.arange(half, device=device, dtype=torch.float32) / half))
+    freqs = positions.to(device=device, dtype=torch.float32).unsqueeze(-1) * inv
+    emb = torch.cat((freqs, freqs), dim=-1)
+    return emb.cos().to(dtype), emb.sin().to(dtype)
+
+
 class QwenRoutedAttention(nn.Module):
     """Replacement for ``Qwen3MoeAttention`` routing through a shared ``ChunkRouter``
     (qwen_routed_attention.py:94-325).  Reuses ``orig``'s ``q_proj/k_proj/v_proj/o_proj`` and
@@ -112,8 +124,7 @@ class QwenRoutedAttention(nn.Module):
         if self.layer_idx == 0 and start_pos == 0:
             router.reset()
         if self.dca_chunk > 0:
-            raise NotImplementedError("Dual Chunk Attention (dca_chunk > 0) is not available in "
-                                      "this build")
+            return self._dca_forward(o, q, k_raw, v, start_pos, router, B, S)
 
         cos, sin = position_embeddings                                       # [B|1, S, Dh]
         cos = cos.reshape(-1, S, Dh)
@@ -128,6 +139,37 @@ class QwenRoutedAttention(nn.Module):
         out_heads = q_rope.new_empty(B, H, S, Dh)
         for routed, lo, hi in segments:
             out_heads[:, :, lo:hi] = routed.attend(q_rope[:, :, lo:hi], use_summaries=False)
+        out = o.o_proj(out_heads.transpose(1, 2).reshape(B, S, H * Dh))
+        return out, None
+
+    def _dca_forward(self, o: nn.Module, q: torch.Tensor, k_raw: torch.Tensor, v: torch.Tensor,
+                     start_pos: int, router: ChunkRouter, B: int,
+                     S: int) -> Tuple[torch.Tensor, Optional[torch.Tensor]]:
+        """Dual Chunk Attention forward (qwen_routed_attention.py:209-242): keys RoPE'd at the
+        intra-chunk position pos % L_c (and stored that way), routing with queries RoPE'd the
+        same way, chunk by chunk; attention per key regime (intra / successive / inter)."""
+        H, Dh = self.num_heads, self.head_dim
+        L_c, ceil, theta = self.dca_chunk, self.dca_ceil, self._cfg.theta
+        dev, dt = q.device, q.dtype
+        hc = router.hcfg(B, dt)
+        pos = torch.arange(start_pos, start_pos + S, device=dev)
+        kcos, ksin = _dca_rope(pos % L_c, Dh, theta, dev, dt)
+        k_dca = ops.rope(hc, k_raw, kcos, ksin, steps_in_dtype=True)
+        q_sel = ops.rope(hc, q, kcos, ksin, steps_in_dtype=True)
+        segments = router.route_query_block(self.layer_idx, q_sel, k_dca, k_raw, v, start_pos,
+                                            return_positions=True)
+        # attention queries in fp32 (:259-266)
+        hf = router.hcfg(B, torch.float32)
+        qf = q.float()
+        qp = pos % L_c
+        versions = []
+        for p_ in (qp, (qp + L_c).clamp(max=ceil), torch.full_like(qp, ceil)):
+            c_, s_ = _dca_rope(p_, Dh, theta, dev, torch.float32)
+            versions.append(ops.rope(hf, qf, c_, s_))
+        out_heads = q.new_empty(B, H, S, Dh)
+        for routed, lo, hi in segments:
+            out_heads[:, :, lo:hi] = routed.attend_dca(*(x_[:, :, lo:hi] for x_ in versions),
+                                                       L_c)
         out = o.o_proj(out_heads.transpose(1, 2).reshape(B, S, H * Dh))
         return out, None
 

@@ -339,6 +339,29 @@ class RoutedKV:
         return ops.attend_decode(self.hcfg, q, self.n_closed, self.start_pos, open_grp=og,
                                  open_thr=r["open_thr"], Kg=r["Kg"], **src)
 
+    def attend_dca(self, q_intra: torch.Tensor, q_succ: torch.Tensor, q_inter: torch.Tensor,
+                   dca_chunk: int) -> torch.Tensor:
+        """Dual Chunk Attention over this block's keys (QwenRoutedAttention._dca_attend,
+        qwen_routed_attention.py:244-283): the fp32 query rows RoPE'd at the intra, successive
+        and inter positions; each key is scored with the version its DCA chunk selects.  Keys
+        are as stored (RoPE'd at pos % dca_chunk by the caller).  Decode-path results only."""
+        if self.chunked:
+            raise ValueError("DCA attends per chunk: route with return_positions=True")
+        r = self.routing
+        src = dict(self.sources)
+        staging = src.pop("staging", None)
+        og, op = r["open_grp"], None
+        if staging is not None:
+            sk, sv, sg = ops.gather_decode(self.hcfg, self.n_closed, og, r["open_thr"], r["Kg"],
+                                           src["record_k"], src["record_v"],
+                                           src["record_on_host"], staging, q_intra.shape[1])
+            src.update(record_k=sk, record_v=sv, record_on_host=False)
+            og, op = sg, og
+        return ops.attend_decode(self.hcfg, q_intra, self.n_closed, self.start_pos, open_grp=og,
+                                 open_thr=r["open_thr"], Kg=r["Kg"],
+                                 dca=dict(q_succ=q_succ, q_inter=q_inter, chunk=dca_chunk,
+                                          open_pos=op), **src)
+
 
 class ChunkRouter:
     """Routing engine over a KV store (chunk_router.py:165-516).  Prefill of a fresh multi-chunk
@@ -377,16 +400,17 @@ class ChunkRouter:
         ([1,1,S,Dh] or [S,Dh]).  Returns [(routed, lo, hi)] segments: one decode segment for a
         block inside one chunk, one chunk-parallel segment for a fresh multi-chunk block, else
         one decode segment per chunk."""
-        if return_positions:
-            raise NotImplementedError("token positions are only used by the DCA attend variant")
         C = self.cfg.chunk_size
         S = q.shape[2]
         first_chunk, last_chunk = start_pos // C, (start_pos + S - 1) // C
-        if start_pos > 0 or first_chunk == last_chunk:
+        # return_positions (the DCA attend variant) takes the per-chunk path, as in the
+        # reference (:503-506); key positions are implicit in the routing lists
+        vectorized = start_pos == 0 and first_chunk != last_chunk and not return_positions
+        if not vectorized:
             self.store.prepare_block(layer, first_chunk, last_chunk)
         if first_chunk == last_chunk:
             return [(self.decode_block(layer, q, k_rope, k_raw, v, start_pos), 0, S)]
-        if start_pos == 0:
+        if vectorized:
             return [(self._prefill(layer, q, k_rope, k_raw, v, cos, sin, populate_store), 0, S)]
         segs, p, done = [], start_pos, 0
         while done < S:

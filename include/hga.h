@@ -198,6 +198,32 @@ int hga_attend_decode(const hga_config* cfg, int32_t L, int32_t n_closed, int64_
                       int64_t o_sh, int64_t o_ss, void* workspace, int64_t workspace_bytes,
                       void* stream);
 
+/*
+ * Dual Chunk Attention decode (QwenRoutedAttention._dca_attend,
+ * Qwen3LongContext/qwen_routed_attention.py:244-283): the same key sequence and visibility as
+ * hga_attend_decode over keys stored RoPE'd at pos % dca_chunk.  Key p is scored against
+ *   q_intra  when p / dca_chunk == (start_pos + l) / dca_chunk,
+ *   q_succ   when it is the DCA chunk before,
+ *   q_inter  otherwise,
+ * the three fp32 [B, H, L, Dh] views (shared strides) of row l RoPE'd at pos % dca_chunk,
+ * min(pos % dca_chunk + dca_chunk, ceil) and ceil.  dca_chunk is a positive multiple of the
+ * chunk size.  open_pos holds the opened groups' own ids when open_grp indexes a staging record
+ * (hga_gather_decode's staged_grp), else NULL (open_grp's ids are the positions).  Same
+ * workspace as hga_attend_decode (hga_attend_decode_workspace).  out in the activation dtype.
+ */
+int hga_attend_decode_dca(const hga_config* cfg, int32_t L, int32_t n_closed,
+                          int64_t start_pos, const float* q_intra, const float* q_succ,
+                          const float* q_inter, int64_t q_sb, int64_t q_sh, int64_t q_ss,
+                          int32_t dca_chunk, const void* k_recent, const void* v_recent,
+                          int64_t r_sb, int64_t r_sh, int64_t r_ss, int32_t ring_chunks,
+                          const void* k_first, const void* v_first, int64_t f_sb, int64_t f_sh,
+                          int64_t f_ss, const void* k_record, const void* v_record,
+                          int64_t d_sb, int64_t d_sh, int64_t d_ss, int32_t record_on_host,
+                          const int32_t* open_grp, const int32_t* open_pos,
+                          const int32_t* open_thr, int32_t Kg, void* out, int64_t o_sb,
+                          int64_t o_sh, int64_t o_ss, void* workspace, int64_t workspace_bytes,
+                          void* stream);
+
 /* Device scratch bytes hga_attend_decode needs (head_dim 64 / 128: the key sequence is split
  * over workgroups of 256 keys whose fp32 partials [B*H*L, splits, head_dim+2] are merged by a
  * second kernel; 0 for other head dims).  16-byte aligned, used only by the call's kernels

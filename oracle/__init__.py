@@ -208,6 +208,27 @@ def attend_decode(q, k_hist, v_hist, C, gs, keep_first, keep_last, n_closed, sta
     return out
 
 
+def attend_decode_dca(q_intra, q_succ, q_inter, k_hist, v_hist, C, gs, keep_first, keep_last,
+                      n_closed, start_pos, open_grp, open_thr, scale, dt, dca_chunk):
+    """Dual Chunk Attention decode (qwen_routed_attention.py:253-283): the three fp32 RoPE'd
+    query versions [B,H,L,Dh]; k_hist holds the DCA-roped keys by absolute position."""
+    q1, p1 = _f(q_intra)
+    q2, p2 = _f(q_succ)
+    q3, p3 = _f(q_inter)
+    k_hist, pk = _f(k_hist)
+    v_hist, pv = _f(v_hist)
+    B, H, L, Dh = q1.shape
+    KVH, T = k_hist.shape[1], k_hist.shape[2]
+    og = np.ascontiguousarray(open_grp, np.int32)
+    ot = np.ascontiguousarray(open_thr, np.int32)
+    out = np.empty_like(q1)
+    lib().orc_attend_decode_dca(p1, p2, p3, pk, pv, ctypes.c_long(T), B, H, KVH, L, Dh, C, gs,
+                                keep_first, keep_last, n_closed, ctypes.c_long(start_pos),
+                                _i(og), _i(ot), og.shape[-1], ctypes.c_float(scale), dt,
+                                dca_chunk, _f(out)[1])
+    return out
+
+
 def prefill(q, k_rope, k_raw, v, cos_tab, sin_tab, *, C, gs, keep_first, keep_last,
             topk_chunks, topk_groups, theta, dt):
     """The whole vectorized prefill path for one block at position 0: summaries (with the

@@ -382,10 +382,12 @@ void orc_route_prefill(const float* q, const float* chunk_k, const float* group_
  * Masked columns in the reference carry -1e4 and vanish in the fp32 softmax; here they are
  * simply absent.  Math in double, result rounded to dt.  q/out [B,H,S,Dh], k/v [B,KVH,S,Dh].
  * ------------------------------------------------------------------------------------------ */
-static void attend_row(const float* qr, const float* kb, const float* vb, const long* keys,
-                       int nk, int Dh, double scale, int dt, float* orow, double* p) {
+static void attend_row_sel(const float* const* qsel, const int* regime, const float* kb,
+                           const float* vb, const long* keys, int nk, int Dh, double scale,
+                           int dt, float* orow, double* p) {
     double mx = -INFINITY;
     for (int j = 0; j < nk; ++j) {
+        const float* qr = qsel[regime ? regime[j] : 0];
         const float* kr = kb + keys[j] * Dh;
         double s = 0.0;
         for (int d = 0; d < Dh; ++d) s += (double)qr[d] * (double)kr[d];
@@ -402,6 +404,12 @@ static void attend_row(const float* qr, const float* kb, const float* vb, const 
         for (int j = 0; j < nk; ++j) acc += p[j] * (double)vb[keys[j] * Dh + d];
         orow[d] = rd((float)(acc / den), dt);
     }
+}
+
+static void attend_row(const float* qr, const float* kb, const float* vb, const long* keys,
+                       int nk, int Dh, double scale, int dt, float* orow, double* p) {
+    const float* qsel[1] = {qr};
+    attend_row_sel(qsel, NULL, kb, vb, keys, nk, Dh, scale, dt, orow, p);
 }
 
 void orc_attend_prefill(const float* q, const float* k, const float* v, int B, int H, int KVH,
@@ -610,10 +618,16 @@ void orc_route_decode(const float* q, const float* chunk_k, const float* group_k
  * opened group with open_thr <= l, and active-chunk tokens n_closed*C + [0, c0 + l] where
  * c0 = start_pos - n_closed*C.  k/v: full token history [B,KVH,T,Dh]; q/out [B,H,L,Dh].
  * ------------------------------------------------------------------------------------------ */
-void orc_attend_decode(const float* q, const float* k, const float* v, long T, int B, int H,
-                       int KVH, int L, int Dh, int C, int gs, int kf, int kl, int n_closed,
-                       long start_pos, const int* open_grp, const int* open_thr, int Kgw,
-                       float scale, int dt, float* out) {
+/* Decode attention over the keys a block of L rows sees (chunk_router.py:333-401).  With
+ * q2/q3 set (Dual Chunk Attention, Qwen3LongContext/qwen_routed_attention.py:253-283), q, q2
+ * and q3 are the rows RoPE'd at the intra, successive and inter positions, and key j is scored
+ * with q when its DCA chunk (position / dca_chunk) equals the row's, with q2 when it is the one
+ * before, else with q3. */
+static void attend_decode_impl(const float* q, const float* q2, const float* q3, const float* k,
+                               const float* v, long T, int B, int H, int KVH, int L, int Dh,
+                               int C, int gs, int kf, int kl, int n_closed, long start_pos,
+                               const int* open_grp, const int* open_thr, int Kgw, float scale,
+                               int dt, int dca_chunk, float* out) {
     const int M = C / gs, rep = H / KVH;
     int f_hi = kf < n_closed ? kf : n_closed;
     if (f_hi < 0) f_hi = 0;
@@ -624,6 +638,7 @@ void orc_attend_decode(const float* q, const float* k, const float* v, long T, i
     }
     const long c0 = start_pos - (long)n_closed * C;
     long* keys = (long*)malloc(sizeof(long) * (T + 16));
+    int* regime = q2 ? (int*)malloc(sizeof(int) * (T + 16)) : NULL;
     double* p = (double*)malloc(sizeof(double) * (T + 16));
     for (int b = 0; b < B; ++b)
         for (int h = 0; h < H; ++h) {
@@ -642,10 +657,36 @@ void orc_attend_decode(const float* q, const float* k, const float* v, long T, i
                         for (int e = 0; e < gs; ++e) keys[nk++] = base + e;
                     }
                 for (long j = 0; j <= c0 + l; ++j) keys[nk++] = (long)n_closed * C + j;
-                attend_row(q + (((long)b * H + h) * L + l) * Dh, kb, vb, keys, nk, Dh,
-                           (double)scale, dt, out + (((long)b * H + h) * L + l) * Dh, p);
+                const long ro = (((long)b * H + h) * L + l) * Dh;
+                const float* qsel[3] = {q + ro, q2 ? q2 + ro : NULL, q3 ? q3 + ro : NULL};
+                if (regime) {
+                    const long cq = (start_pos + l) / dca_chunk;
+                    for (int j = 0; j < nk; ++j) {
+                        const long ck = keys[j] / dca_chunk;
+                        regime[j] = ck == cq ? 0 : (ck == cq - 1 ? 1 : 2);
+                    }
+                }
+                attend_row_sel(qsel, regime, kb, vb, keys, nk, Dh, (double)scale, dt, out + ro, p);
             }
         }
     free(keys);
+    free(regime);
     free(p);
+}
+
+void orc_attend_decode(const float* q, const float* k, const float* v, long T, int B, int H,
+                       int KVH, int L, int Dh, int C, int gs, int kf, int kl, int n_closed,
+                       long start_pos, const int* open_grp, const int* open_thr, int Kgw,
+                       float scale, int dt, float* out) {
+    attend_decode_impl(q, NULL, NULL, k, v, T, B, H, KVH, L, Dh, C, gs, kf, kl, n_closed,
+                       start_pos, open_grp, open_thr, Kgw, scale, dt, 1, out);
+}
+
+void orc_attend_decode_dca(const float* q, const float* q2, const float* q3, const float* k,
+                           const float* v, long T, int B, int H, int KVH, int L, int Dh, int C,
+                           int gs, int kf, int kl, int n_closed, long start_pos,
+                           const int* open_grp, const int* open_thr, int Kgw, float scale,
+                           int dt, int dca_chunk, float* out) {
+    attend_decode_impl(q, q2, q3, k, v, T, B, H, KVH, L, Dh, C, gs, kf, kl, n_closed,
+                       start_pos, open_grp, open_thr, Kgw, scale, dt, dca_chunk, out);
 }
