@@ -464,6 +464,146 @@ __device__ __forceinline__ uint32_t rowgroup_topk(const uint32_t (&kv)[JJ], int 
     return bits;
 }
 
+// ------------------------------------------------------------------------------------------
+// Compacted selection (k <= kCompactK): one or a few counting probes find a threshold T that
+// leaves k < count(key >= T) <= kCap keys in the row; those keys are compacted into a per-row
+// LDS buffer (kCap slots + one discard slot) and sorted by a 32-element bitonic network over the
+// row's 16 lanes (2 keys per lane, element e = 2*seg + r, DPP partner exchanges); the k-th and
+// (k+1)-th largest keys are then read off exactly.  This replaces the full-row search and its
+// certification count.  Rows whose probes do not land within a few steps make the whole wave
+// fall back to the full-row search.
+// ------------------------------------------------------------------------------------------
+constexpr int kCap = 32;         // compacted keys per row
+constexpr int kCmpStride = 34;   // per-row buffer: kCap slots, a discard slot, 8-byte aligned
+constexpr int kCompactK = 16;
+
+template <int CTRL>
+__device__ __forceinline__ uint32_t dppu(uint32_t x) {
+    return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, CTRL, 0xf, 0xf, false);
+}
+// compare-exchange of this lane's x with partner value p: the lower element keeps the minimum
+__device__ __forceinline__ uint32_t cx(uint32_t x, uint32_t p, bool lower) {
+    return lower ? min(x, p) : max(x, p);
+}
+// Ascending bitonic sort of the 32 keys (a = element 2*seg, b = 2*seg + 1) of each 16-lane
+// row: for block sizes 2..32 a flip step (element e against e ^ (size-1), a lane mirror that
+// swaps a and b) then half-cleaners e against e ^ j for j = size/4 .. 1.
+__device__ __forceinline__ void sort32_row(uint32_t& a, uint32_t& b, int seg) {
+    auto inlane = [&]() { const uint32_t lo = min(a, b); b = max(a, b); a = lo; };
+    auto flip = [&](auto pa_fn, int lowbit) {
+        const bool lw = (seg & lowbit) == 0;
+        const uint32_t pa = pa_fn(b), pb = pa_fn(a);
+        a = cx(a, pa, lw);
+        b = cx(b, pb, lw);
+    };
+    auto half = [&](auto p_fn, int lowbit) {
+        const bool lw = (seg & lowbit) == 0;
+        a = cx(a, p_fn(a), lw);
+        b = cx(b, p_fn(b), lw);
+    };
+    auto x1 = [](uint32_t v) { return dppu<0xB1>(v); };     // lane ^ 1 (quad_perm [1,0,3,2])
+    auto x2 = [](uint32_t v) { return dppu<0x4E>(v); };     // lane ^ 2 (quad_perm [2,3,0,1])
+    auto m3 = [](uint32_t v) { return dppu<0x1B>(v); };     // lane ^ 3 (quad_perm [3,2,1,0])
+    auto m7 = [](uint32_t v) { return dppu<0x141>(v); };    // lane ^ 7 (row_half_mirror)
+    auto m15 = [](uint32_t v) { return dppu<0x140>(v); };   // lane ^ 15 (row_mirror)
+    auto x4 = [](uint32_t v) {                              // lane ^ 4 (swizzle, xor mask 4)
+        return (uint32_t)__builtin_amdgcn_ds_swizzle((int)v, 0x101f);
+    };
+    inlane();                                                      // size 2
+    flip(x1, 1); inlane();                                         // size 4
+    flip(m3, 2); half(x1, 1); inlane();                            // size 8
+    flip(m7, 4); half(x2, 2); half(x1, 1); inlane();               // size 16
+    flip(m15, 8); half(x4, 4); half(x2, 2); half(x1, 1); inlane(); // size 32
+}
+
+// k-th and (k+1)-th largest keys of each row (k <= kCompactK) by compaction into rowbuf (this
+// row's kCmpStride-slot LDS buffer).  Returns false (wave-uniform) when some row of the wave
+// found no threshold; the caller then runs the full-row search.  Rows with at most kCap valid
+// candidates (including rows with none) compact all of them.
+template <int JJ>
+__device__ __forceinline__ bool rowgroup_compact(const uint32_t (&kv)[JJ], int k, const RowStats& rs,
+                                                 uint32_t* rowbuf, uint32_t& kth, uint32_t& k1th) {
+    const int nv = rs.nv, seg = lane_id() & 15;
+    bool ok = nv <= kCap;
+    uint32_t T = 1u;                  // threshold: keys >= T are compacted (key 0 = no candidate)
+    int cl = 0;                       // this lane's keys >= T
+    {
+        // probes aim at the middle of (k, kCap]: Gaussian quantile of the row's sample first,
+        // then regula falsi between the probes on either side, or a Newton step on the
+        // Gaussian count density (at most 2 standard deviations) while one side is missing
+        const float rn = __builtin_amdgcn_rcpf((float)(rs.ns > 0 ? rs.ns : 1));
+        const float mu = rs.s1 * rn;
+        const float sd = __builtin_amdgcn_sqrtf(fmaxf(rs.s2 * rn - mu * mu, 0.0f));
+        const float rv = __builtin_amdgcn_rcpf((float)(nv > 0 ? nv : 1));
+        const float target = 0.5f * (float)(k + 1 + kCap);
+        float x = mu + z_upper_fast((target + 0.5f) * rv) * sd;
+        float lf = 0.0f, hf = 0.0f;
+        int clo = -1, chi = -1;
+        for (int it = 0; it < 6 && __ballot(!ok) != 0; ++it) {
+            const uint32_t tx = min(max(okey_fast(x), 1u), 0xfffffffeu);
+            int c_l = 0;
+#pragma unroll
+            for (int i = 0; i < JJ; ++i) c_l += kv[i] >= tx ? 1 : 0;
+            const int c = r16_sum(c_l);
+            if (!ok) {
+                if (c > k && c <= kCap) {
+                    ok = true;
+                    T = tx;
+                    cl = c_l;
+                } else {
+                    if (c > kCap) {
+                        lf = x;
+                        clo = c;
+                    } else {
+                        hf = x;
+                        chi = c;
+                    }
+                    if (clo >= 0 && chi >= 0) {
+                        x = lf + (hf - lf) * ((float)clo - target) * __builtin_amdgcn_rcpf((float)(clo - chi));
+                    } else {
+                        const float z = (x - mu) * __builtin_amdgcn_rcpf(sd > 0.0f ? sd : 1.0f);
+                        const float dens = (float)nv * 0.39894228f * __expf(-0.5f * z * z) *
+                                           __builtin_amdgcn_rcpf(sd > 0.0f ? sd : 1.0f);
+                        const float step = ((float)c - target) * __builtin_amdgcn_rcpf(fmaxf(dens, 1e-30f));
+                        x += fminf(fmaxf(step, -2.0f * sd), 2.0f * sd);
+                    }
+                }
+            }
+        }
+    }
+    if (__ballot(!ok) != 0) return false;
+    if (nv <= kCap) {
+        cl = 0;
+#pragma unroll
+        for (int i = 0; i < JJ; ++i) cl += kv[i] != 0u ? 1 : 0;
+    }
+    // exclusive prefix of the per-lane counts over the row (row_shr with zero fill)
+    int incl = cl;
+    incl += dppi<0x111, 0>(incl);
+    incl += dppi<0x112, 0>(incl);
+    incl += dppi<0x114, 0>(incl);
+    incl += dppi<0x118, 0>(incl);
+    const int cnt = r16_sum(cl);
+    int pos = incl - cl;
+#pragma unroll
+    for (int i = 0; i < JJ; ++i) {
+        const bool in = kv[i] >= T;
+        rowbuf[in ? pos : kCap] = kv[i];
+        pos += in ? 1 : 0;
+    }
+    __builtin_amdgcn_wave_barrier();
+    const uint2 ab = *reinterpret_cast<const uint2*>(rowbuf + 2 * seg);
+    uint32_t a = 2 * seg < cnt ? ab.x : 0u;
+    uint32_t b = 2 * seg + 1 < cnt ? ab.y : 0u;
+    __builtin_amdgcn_wave_barrier();
+    sort32_row(a, b, seg);
+    // ascending order: element kCap - k holds the k-th largest key, kCap - k - 1 the next
+    const int ek = kCap - k, ek1 = ek - 1;
+    kth = r16_umax(seg == (ek >> 1) ? ((ek & 1) ? b : a) : 0u);
+    k1th = r16_umax(seg == (ek1 >> 1) ? ((ek1 & 1) ? b : a) : 0u);
+    return true;
+}
+
 // Row-group requests of block rows [r0, r0+32): lane -> (row rr = 4w + lane/16, seg); row rr's
 // candidate values are sS[rr * stride + c] for c < ncand (-inf = not visible when VIS; without
 // VIS every candidate is visible).  Certified rows raise the pooled key / lower the first row of
@@ -472,7 +612,8 @@ __device__ __forceinline__ uint32_t rowgroup_topk(const uint32_t (&kv)[JJ], int 
 template <int JJ, bool VIS>
 __device__ __forceinline__ void rowgroup_requests(int r0, int brows, int ncand, const float* sS, int stride,
                                   int k, float dsc, const float* sQn, uint32_t* sPk,
-                                  int* sFirst, uint32_t* sBits, int BW, int* sAmb, int* sAmbN) {
+                                  int* sFirst, uint32_t* sBits, int BW, int* sAmb, int* sAmbN,
+                                  uint32_t* sCmp) {
     constexpr int W = JJ < 4 ? JJ : 4;
     constexpr int G = JJ / W;
     const int w = threadIdx.x / kWave, l = lane_id(), seg = l & 15;
@@ -532,17 +673,39 @@ __device__ __forceinline__ void rowgroup_requests(int r0, int brows, int ncand, 
     rs.ns = VIS ? r16_sum(nsl) : (ncand < 16 * W ? ncand : 16 * W);
     rs.s1 = r16_fsum(rs.s1);
     rs.s2 = r16_fsum(rs.s2);
+    const bool open = act && rs.nv > k;
+    bool amb = false;
+    uint32_t bits = 0u;
+    // compacted path: exact k-th / (k+1)-th keys, so certification is one comparison
+    // (members: keys >= the k-th; an equal (k+1)-th is a boundary tie, canonical path)
+    bool compacted = false;
+    if constexpr (JJ >= 2) {
+        if (sCmp != nullptr && k <= kCompactK) {
+            uint32_t kth, k1th;
+            if (rowgroup_compact<JJ>(kv, k, rs, sCmp + rr * kCmpStride, kth, k1th)) {
+                compacted = true;
+                const uint32_t vs = open ? kth : 1u;
+#pragma unroll
+                for (int i = JJ - 1; i >= 0; --i) bits = 2u * bits + (kv[i] >= vs ? 1u : 0u);
+                amb = open && kth == k1th;
+                if (open && !amb && dsc > 0.0f) {
+                    const float delta = dsc * sQn[t];
+                    amb = !(okey_inv(kth) - 2.0f * delta > okey_inv(k1th));
+                }
+            }
+        }
+    }
+    if (!compacted) {
     uint32_t vsep;
     bool tie;
-    const uint32_t bits = rowgroup_topk<JJ>(kv, k, rs, vsep, tie);
+    bits = rowgroup_topk<JJ>(kv, k, rs, vsep, tie);
     // A tie at the boundary goes to the canonical path (equal keys ordered by candidate index
     // there; with MFMA scores such a row is never certifiable anyway).  Certification: k-th and
     // (k+1)-th values at least 2*delta apart.  Rows with at most k candidates have no (k+1)-th.
     // A row that ended with count(>= vsep) == k is certified when no key lies in
     // [value(vsep) - 2 delta, vsep) (one more count); only rows failing that test get the exact
     // k-th / (k+1)-th comparison.
-    const bool open = act && rs.nv > k;
-    bool amb = open && tie;
+    amb = open && tie;
     if (dsc > 0.0f) {
         const float delta = act ? dsc * sQn[t] : 0.0f;
         const uint32_t probe = okey_fast(okey_inv(vsep) - 2.0f * delta);
@@ -562,6 +725,7 @@ __device__ __forceinline__ void rowgroup_requests(int r0, int brows, int ncand, 
             const float ak1 = kk1 == 0u ? -INFINITY : okey_inv(kk1);
             if (unsure) amb = ak1 != -INFINITY && !(ak - 2.0f * delta > ak1);
         }
+    }
     }
     if (amb) {
         if (seg == 0) sAmb[atomicAdd(sAmbN, 1)] = t;
@@ -585,9 +749,9 @@ __device__ __noinline__ void rowgroup_requests_call(int r0, int brows, int ncand
                                                     int stride, int k, float dsc,
                                                     const float* sQn, uint32_t* sPk,
                                                     int* sFirst, uint32_t* sBits, int BW,
-                                                    int* sAmb, int* sAmbN) {
+                                                    int* sAmb, int* sAmbN, uint32_t* sCmp) {
     rowgroup_requests<JJ, VIS>(r0, brows, ncand, sS, stride, k, dsc, sQn, sPk, sFirst, sBits, BW,
-                               sAmb, sAmbN);
+                               sAmb, sAmbN, sCmp);
 }
 
 // Calls f(JTag<JJ>) with the smallest JJ in {1, 2, 4, 8, 12, ..., 32} such that 16*JJ >= n
@@ -624,6 +788,7 @@ void route_stage1_kernel(RouteArgs A) {
     int* sThr = sSel + kMaxSel;                                      // [kMaxSel]
     int* sScal = sThr + kMaxSel;                                     // [8] scalars
     int* sAmb = sScal + 8;                                           // [kRows] ambiguous rows
+    uint32_t* sCmp = reinterpret_cast<uint32_t*>(sAmb + kRows);      // [32][kCmpStride] compaction
 
     const int N = A.N, C = A.C;
     const int n = N - 1 - (int)(blockIdx.x / (A.B * A.H));          // heavy chunks first
@@ -689,10 +854,10 @@ void route_stage1_kernel(RouteArgs A) {
             constexpr int JJ = decltype(jt)::value;
             if constexpr (JJ >= 8)
                 rowgroup_requests_call<JJ, false>(r0, brows, P, sS, SP, kreq, ds1, sQn, sPk,
-                                                  sFirst, sBits, BW, sAmb, &sScal[4]);
+                                                  sFirst, sBits, BW, sAmb, &sScal[4], sCmp);
             else
                 rowgroup_requests<JJ, false>(r0, brows, P, sS, SP, kreq, ds1, sQn, sPk, sFirst,
-                                             sBits, BW, sAmb, &sScal[4]);
+                                             sBits, BW, sAmb, &sScal[4], sCmp);
         });
         __syncthreads();
         // rows the MFMA scores could not certify: canonical re-rank (one row per wave)
@@ -845,7 +1010,7 @@ void route_stage2_kernel(RouteArgs A) {
         dispatch_jj(T2, [&](auto jt) {
             constexpr int JJ = decltype(jt)::value;
             rowgroup_requests<JJ, true>(r0, brows, T2, sS + r0 * SP2, SP2, A.Kgr, ds2, sQn,
-                                        sPk, sFirst, sBits, BW, sAmb, &sScal[4]);
+                                        sPk, sFirst, sBits, BW, sAmb, &sScal[4], nullptr);
         });
     }
     __syncthreads();
@@ -983,7 +1148,8 @@ extern "C" int hga_route_prefill(const hga_config* cfg, int32_t S, const void* q
     a.BW = (a.SPP + 31) / 32;
     const size_t lds1 = sizeof(float) * (size_t)a.SSZ + sizeof(float) * kRows +
                         2 * sizeof(int) * (size_t)a.SPP + sizeof(uint32_t) * (size_t)kRows * a.BW +
-                        sizeof(int) * (2 * kMaxSel + 8 + kRows);
+                        sizeof(int) * (2 * kMaxSel + 8 + kRows) +
+                        sizeof(uint32_t) * kBlk * kCmpStride;
     // stage 2: [64][SP2] scores of all rows, row norms, visibility table, pooled state
     a.SPP2 = T2max + 1;
     a.BW2 = (a.SPP2 + 31) / 32;
