@@ -516,6 +516,48 @@ __device__ __forceinline__ void sort32_row(uint32_t& a, uint32_t& b, int seg) {
     flip(m15, 8); half(x4, 4); half(x2, 2); half(x1, 1); inlane(); // size 32
 }
 
+// Ascending bitonic sort of the 64 keys of each 16-lane row, element e = 4*seg + r held in
+// R[r] (the row-group layout of 64 candidates): in-lane steps pair r with r ^ m; cross-lane
+// steps pair lane seg with seg ^ mh (DPP / swizzle) and register r with r ^ ml.
+template <int M>
+__device__ __forceinline__ void sort_inlane4(uint32_t (&R)[4]) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const int p = r ^ M;
+        if (p > r) {
+            const uint32_t lo = min(R[r], R[p]);
+            R[p] = max(R[r], R[p]);
+            R[r] = lo;
+        }
+    }
+}
+template <int ML, class F>
+__device__ __forceinline__ void sort_cross4(uint32_t (&R)[4], F perm, bool lower) {
+    uint32_t P[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) P[r] = perm(R[r ^ ML]);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) R[r] = cx(R[r], P[r], lower);
+}
+__device__ __forceinline__ void sort64_row(uint32_t (&R)[4], int seg) {
+    auto x1 = [](uint32_t v) { return dppu<0xB1>(v); };
+    auto x2 = [](uint32_t v) { return dppu<0x4E>(v); };
+    auto m3 = [](uint32_t v) { return dppu<0x1B>(v); };
+    auto m7 = [](uint32_t v) { return dppu<0x141>(v); };
+    auto m15 = [](uint32_t v) { return dppu<0x140>(v); };
+    auto x4 = [](uint32_t v) { return (uint32_t)__builtin_amdgcn_ds_swizzle((int)v, 0x101f); };
+    const bool b1 = (seg & 1) == 0, b2 = (seg & 2) == 0, b4 = (seg & 4) == 0, b8 = (seg & 8) == 0;
+    sort_inlane4<1>(R);                                                           // size 2
+    sort_inlane4<3>(R); sort_inlane4<1>(R);                                       // size 4
+    sort_cross4<3>(R, x1, b1); sort_inlane4<2>(R); sort_inlane4<1>(R);            // size 8
+    sort_cross4<3>(R, m3, b2); sort_cross4<0>(R, x1, b1);                         // size 16
+    sort_inlane4<2>(R); sort_inlane4<1>(R);
+    sort_cross4<3>(R, m7, b4); sort_cross4<0>(R, x2, b2); sort_cross4<0>(R, x1, b1); // size 32
+    sort_inlane4<2>(R); sort_inlane4<1>(R);
+    sort_cross4<3>(R, m15, b8); sort_cross4<0>(R, x4, b4); sort_cross4<0>(R, x2, b2); // size 64
+    sort_cross4<0>(R, x1, b1); sort_inlane4<2>(R); sort_inlane4<1>(R);
+}
+
 // k-th and (k+1)-th largest keys of each row (k <= kCompactK) by compaction into rowbuf (this
 // row's kCmpStride-slot LDS buffer).  Returns false (wave-uniform) when some row of the wave
 // found no threshold; the caller then runs the full-row search.  Rows with at most kCap valid
@@ -676,26 +718,39 @@ __device__ __forceinline__ void rowgroup_requests(int r0, int brows, int ncand, 
     const bool open = act && rs.nv > k;
     bool amb = false;
     uint32_t bits = 0u;
-    // compacted path: exact k-th / (k+1)-th keys, so certification is one comparison
-    // (members: keys >= the k-th; an equal (k+1)-th is a boundary tie, canonical path)
-    bool compacted = false;
+    // exact k-th / (k+1)-th keys -- by compaction and a 32-key sort (k <= kCompactK, with a
+    // compaction buffer) or, for rows of at most 64 candidates, by sorting the row's keys in
+    // place -- make certification one comparison (members: keys >= the k-th; an equal (k+1)-th
+    // is a boundary tie, canonical path); otherwise the full-row search
+    bool exact = false;
+    uint32_t kth = 0u, k1th = 0u;
     if constexpr (JJ >= 2) {
-        if (sCmp != nullptr && k <= kCompactK) {
-            uint32_t kth, k1th;
-            if (rowgroup_compact<JJ>(kv, k, rs, sCmp + rr * kCmpStride, kth, k1th)) {
-                compacted = true;
-                const uint32_t vs = open ? kth : 1u;
-#pragma unroll
-                for (int i = JJ - 1; i >= 0; --i) bits = 2u * bits + (kv[i] >= vs ? 1u : 0u);
-                amb = open && kth == k1th;
-                if (open && !amb && dsc > 0.0f) {
-                    const float delta = dsc * sQn[t];
-                    amb = !(okey_inv(kth) - 2.0f * delta > okey_inv(k1th));
-                }
-            }
+        if (sCmp != nullptr && k <= kCompactK)
+            exact = rowgroup_compact<JJ>(kv, k, rs, sCmp + rr * kCmpStride, kth, k1th);
+    }
+    if constexpr (JJ == 4) {
+        if (!exact && k < 64) {
+            uint32_t R[4] = {kv[0], kv[1], kv[2], kv[3]};
+            sort64_row(R, seg);
+            const int ek = 64 - k, ek1 = ek - 1;   // ascending positions of the k-th, (k+1)-th
+            const uint32_t vk = (ek & 3) == 0 ? R[0] : (ek & 3) == 1 ? R[1] : (ek & 3) == 2 ? R[2] : R[3];
+            const uint32_t vk1 = (ek1 & 3) == 0 ? R[0] : (ek1 & 3) == 1 ? R[1] : (ek1 & 3) == 2 ? R[2] : R[3];
+            kth = r16_umax(seg == (ek >> 2) ? vk : 0u);
+            k1th = r16_umax(seg == (ek1 >> 2) ? vk1 : 0u);
+            exact = true;
         }
     }
-    if (!compacted) {
+    if (exact) {
+        const uint32_t vs = open ? kth : 1u;
+#pragma unroll
+        for (int i = JJ - 1; i >= 0; --i) bits = 2u * bits + (kv[i] >= vs ? 1u : 0u);
+        amb = open && kth == k1th;
+        if (open && !amb && dsc > 0.0f) {
+            const float delta = dsc * sQn[t];
+            amb = !(okey_inv(kth) - 2.0f * delta > okey_inv(k1th));
+        }
+    }
+    if (!exact) {
     uint32_t vsep;
     bool tie;
     bits = rowgroup_topk<JJ>(kv, k, rs, vsep, tie);
