@@ -431,16 +431,17 @@ __global__ __launch_bounds__(256) void kv_block_kernel(const uint16_t* __restric
     }
 }
 
-// Direct global->LDS copy of 16 bytes per lane: lane i's 16 bytes at src land at the
-// wave-uniform LDS byte address lds_addr + 16 * i.  Issued as inline assembly so that the compiler,
-// which cannot prove that a copy into one stage does not alias reads of the other, inserts no
-// waits for it; the caller waits (vmcnt) before the barrier that publishes a stage.  M0 holds
-// the LDS address; nothing else in these kernels uses M0.
+// Direct global->LDS copy of 16 bytes per lane: lane i's 16 bytes at sbase + voff land at the
+// wave-uniform LDS byte address lds_addr + 16 * i (sbase wave-uniform in SGPRs, voff the lane's
+// 32-bit byte offset).  Issued as inline assembly so that the compiler, which cannot prove that
+// a copy into one stage does not alias reads of the other, inserts no waits for it; the caller
+// waits (vmcnt) before the barrier that publishes a stage.  M0 holds the LDS address; nothing
+// else in these kernels uses M0.
 #pragma clang diagnostic push
 #pragma clang diagnostic ignored "-Winline-asm"
-__device__ __forceinline__ void lds_copy16(const void* src, uint32_t lds_addr) {
-    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off"
-                 :: "s"(__builtin_amdgcn_readfirstlane(lds_addr)), "v"(src) : "memory", "m0");
+__device__ __forceinline__ void lds_copy16_s(const void* sbase, uint32_t voff, uint32_t lds_addr) {
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2"
+                 :: "s"(lds_addr), "v"(voff), "s"(sbase) : "memory", "m0");
 }
 #pragma clang diagnostic pop
 
@@ -519,18 +520,20 @@ __global__ __launch_bounds__(kV2Threads) void attend_v2_kernel(AttnArgs A,
     // Stage copy of tile t: 16-byte piece p = 128 r + thread; a wave's 64 pieces of one r are
     // consecutive within one block (BB/16 pieces per block), so the LDS side is the wave-uniform
     // base + 16 * lane that the direct load writes.
+    // per-lane byte offsets within a block of this wave's pieces (p0 % (BB/16) takes two values)
+    const uint32_t voff0 = (uint32_t)(16 * ((64 * w) % (BB / 16)) + 16 * l);
+    const uint32_t voff1 = (uint32_t)(16 * ((128 + 64 * w) % (BB / 16)) + 16 * l);
     auto copy_tile = [&](int t, int stg) {
         const int2 p2 = *reinterpret_cast<const int2*>(&sPos[2 * t]);
         const int64_t ba = (int64_t)(__builtin_amdgcn_readfirstlane(p2.x) >> 4) * BB;
         const int64_t bbk = (int64_t)(__builtin_amdgcn_readfirstlane(p2.y) >> 4) * BB;
-        const uint32_t dst = stage_lds + (uint32_t)(stg * STG);
+        const uint32_t dst = __builtin_amdgcn_readfirstlane(stage_lds + (uint32_t)(stg * STG));
 #pragma unroll
         for (int r = 0; r < STG / (16 * kV2Threads); ++r) {
             const int p0 = 128 * r + 64 * w;
             const int region = p0 / (BB / 16);
-            const unsigned char* src = (region < 2 ? kblk : vblk) + ((region & 1) ? bbk : ba) +
-                                       (p0 % (BB / 16)) * 16 + 16 * l;
-            lds_copy16(src, dst + (uint32_t)(16 * p0));
+            const unsigned char* base = (region < 2 ? kblk : vblk) + ((region & 1) ? bbk : ba);
+            lds_copy16_s(base, (p0 % (BB / 16)) < 128 ? voff0 : voff1, dst + (uint32_t)(16 * p0));
         }
     };
     const int kcol = 8 * g;                        // this lane's 8 dims per k-step
@@ -552,12 +555,16 @@ __global__ __launch_bounds__(kV2Threads) void attend_v2_kernel(AttnArgs A,
     const int voff = 2 * BB + 512 * g + 16 * lr;
     const float c2 = A.scale * 1.4426950408889634f;
     // raw scores of a tile (S^T: lane = query row, 16 keys per lane)
+    // (two accumulation chains over even and odd k-steps, so consecutive MFMAs do not wait on
+    // each other's results)
     auto scores_raw = [&](const bf16x8 (&kr)[KS]) {
-        floatx16 sc = {};
+        floatx16 s0 = {}, s1 = {};
 #pragma unroll
-        for (int s = 0; s < KS; ++s)
-            sc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kr[s], qb[s], sc, 0, 0, 0);
-        return sc;
+        for (int s = 0; s < KS; s += 2) {
+            s0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kr[s], qb[s], s0, 0, 0, 0);
+            s1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kr[s + 1], qb[s + 1], s1, 0, 0, 0);
+        }
+        return s0 + s1;
     };
     // Mask tile t's scores to the visible keys.  Opened/window blocks have one first-visible
     // row per block (uniform), so a block is all visible, all hidden, or split at one row for
