@@ -177,3 +177,32 @@ def test_route_exact_ties(hga):
     print("ambiguous rows/pools:", stats.cpu().tolist(), "canonical:", stats_c.cpu().tolist())
     assert (o_r["sel_chunk"] == 2).sum() > 0
     assert stats[0].item() > 0           # the tie path really ran
+
+
+def test_route_many_ties_full_search(hga):
+    """41 copies of one chunk summary in pools of up to ~117 chunks with top-16: a row ranking
+    the copied score among its top 16 has no threshold leaving 17..32 keys (the count jumps by
+    41), so its row group takes the full-row search, and the boundary tie the canonical path;
+    selections must still equal the oracle's."""
+    from hierarchicalglobalattention_amd import ops
+    B, H, KVH, S, Dh, C, gs = 1, 4, 2, 64 * 120, 128, 64, 16
+    print("[prefill] many ties", flush=True)
+    q, k_rope, k_raw, v, cos, sin = _bf16_case(9, B, H, KVH, S, Dh, C, gs, 1, 1, 16, 64, 1e6)
+    dev = torch.device("cuda:0")
+    cfg = _cfg(ops, B=B, H=H, KVH=KVH, Dh=Dh, C=C, gs=gs, kf=1, kl=1, tc=16, tg=64, theta=1e6,
+               dtype=torch.bfloat16)
+    cb, sb = cos.to(torch.bfloat16).float(), sin.to(torch.bfloat16).float()
+    ck, gk = ops.summarize(cfg, k_raw.to(dev), k_rope.to(dev), cb.to(dev), sb.to(dev))
+    ck[:, :, 2] *= 3                   # large norm: the copies rank near the top of many rows
+    for c in range(4, 84, 2):          # chunks 4, 6, .., 82 copy chunk 2
+        ck[:, :, c] = ck[:, :, 2]
+    stats = torch.zeros(4, dtype=torch.int32, device=dev)
+    r = ops.route_prefill(cfg, q.to(dev), ck, gk, stats=stats)
+    rc = ops.route_prefill(cfg, q.to(dev), ck, gk, canonical=True)
+    f = lambda t: t.float().cpu().numpy()
+    o_r = oracle.route_prefill(f(q), f(ck), f(gk), S, C, gs, 1, 1, 16, 64, oracle.attn_scale(Dh))
+    for rr in (r, rc):
+        _cmp_sets(rr, o_r["sel_chunk"], o_r["sel_thr"], "sel_chunk", "sel_thr")
+        _cmp_sets(rr, o_r["open_grp"], o_r["open_thr"], "open_grp", "open_thr")
+    print("ambiguous rows/pools:", stats.cpu().tolist())
+    assert stats[0].item() > 0
