@@ -9,11 +9,12 @@ activation dtype, :176), then the block goes through ``ChunkRouter.route_query_b
 ``RoutedKV.attend`` on the HIP kernels, then ``o_proj``.  ``replace_qwen_attention_with_router``
 / ``restore_original_attention`` do the model surgery (:331-399).
 
-Cache tiers: ``"vram"`` (``VramKVCacheStore``) and ``"ram"`` (``RamKVCacheStore``: the token
-record in pinned host memory, each decode step's opened groups gathered over the host link).
-The reference's RAM-tier tuning knobs (``vram_cache_chunks``, ``vram_summary_chunks``,
-``vram_cache_reserve_gb``) size its VRAM LRU cache, which this build has no use for; they are
-accepted and ignored.  The on-disk tier (``"fs"``) is not part of this build and raises.
+Cache tiers: ``"vram"`` (``VramKVCacheStore``), ``"ram"`` (``RamKVCacheStore``: the token
+record in pinned host memory, each decode step's opened groups gathered over the host link) and
+``"fs"`` (``FsKVCacheStore``: the record in per-layer files under ``fs_cache_dir`` with a
+pinned page cache bounded by ``ram_budget_gb``).  The reference's VRAM-bank knobs
+(``vram_cache_chunks``, ``vram_summary_chunks``, ``vram_cache_reserve_gb``) size VRAM LRU
+caches this build has no use for (summaries stay resident); they are accepted and ignored.
 """
 from __future__ import annotations
 
@@ -23,8 +24,8 @@ import torch
 import torch.nn as nn
 
 from . import ops
-from .router import (ChunkPlacementPolicy, ChunkRouter, RamKVCacheStore, RouterConfig,
-                     VramKVCacheStore)
+from .router import (ChunkPlacementPolicy, ChunkRouter, FsKVCacheStore, RamKVCacheStore,
+                     RouterConfig, VramKVCacheStore)
 
 
 def _rope_theta(config: Any) -> float:
@@ -72,9 +73,6 @@ class QwenRoutedAttention(nn.Module):
         self.chunk_size = chunk_size
         if cache_location not in ("vram", "ram", "fs"):
             raise ValueError(f"unknown cache_location {cache_location!r}")
-        if cache_location == "fs":
-            raise NotImplementedError("the on-disk KV tier (cache_location='fs') is not part of "
-                                      "this build; use 'vram' or 'ram'")
         self.cache_location = cache_location
         self.vram_cache_chunks = vram_cache_chunks
         self.vram_summary_chunks = vram_summary_chunks
@@ -180,6 +178,9 @@ class QwenRoutedAttention(nn.Module):
                       groups_per_chunk=self._cfg.groups_per_chunk, batch_size=B, dtype=dtype)
         if self.cache_location == "vram":
             return VramKVCacheStore(**kwargs)
+        if self.cache_location == "fs":
+            return FsKVCacheStore(ram_budget_gb=self.ram_budget_gb, fs_cache_dir=self.fs_cache_dir,
+                                  num_layers=self.num_layers, **kwargs)
         return RamKVCacheStore(num_layers=self.num_layers, **kwargs)
 
     def _get_router(self, pkv: Any, B: int, dtype: torch.dtype,

@@ -15,8 +15,8 @@ import torch
 import torch.nn as nn
 
 from . import ops
-from .router import (ChunkPlacementPolicy, ChunkRouter, RamKVCacheStore, RouterConfig,
-                     VramKVCacheStore)
+from .router import (ChunkPlacementPolicy, ChunkRouter, FsKVCacheStore, RamKVCacheStore,
+                     RouterConfig, VramKVCacheStore)
 
 
 class RMSNorm(nn.Module):
@@ -129,13 +129,15 @@ class HierarchicalGlobalAttentionRouted(nn.Module):
         return emb.cos(), emb.sin()
 
     def _make_store(self, B: int, dtype, device):
-        """VRAM or pinned-RAM token record (HierarchicalGlobalAttentionRouted.py:223-240)."""
-        if self.cache_location not in ("vram", "ram"):
+        """VRAM, pinned-RAM or on-disk token record (HierarchicalGlobalAttentionRouted.py:223-240)."""
+        cls = {"vram": VramKVCacheStore, "ram": RamKVCacheStore,
+               "fs": FsKVCacheStore}.get(self.cache_location)
+        if cls is None:
             raise ValueError(f"unknown cache_location {self.cache_location!r}")
-        cls = VramKVCacheStore if self.cache_location == "vram" else RamKVCacheStore
+        kw = dict(num_layers=self.num_layers) if cls is FsKVCacheStore else {}
         return cls(compute_device=device, policy=self._policy, kv_heads=self.kv_heads,
                    head_dim=self.head_dim, chunk_size=self.chunk_size,
-                   groups_per_chunk=self._cfg.groups_per_chunk, batch_size=B, dtype=dtype)
+                   groups_per_chunk=self._cfg.groups_per_chunk, batch_size=B, dtype=dtype, **kw)
 
     def _get_router(self, pkv: Any, B: int, dtype, device) -> ChunkRouter:
         holder = pkv if pkv is not None else self

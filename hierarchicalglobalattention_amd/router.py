@@ -9,9 +9,15 @@ is a set of index lists on the GPU rather than materialised K/V + masks, and
 from __future__ import annotations
 
 import math
+import os
+import shutil
+import tempfile
+import weakref
+from collections import OrderedDict
 from dataclasses import dataclass
 from typing import Dict, List, Optional, Tuple
 
+import numpy as np
 import torch
 
 from . import ops
@@ -301,6 +307,208 @@ class RamKVCacheStore(_StoreBase):
                     record_v=st.tok_v, record_on_host=True, staging=self.staging)
 
 
+class _FsLayer:
+    """One layer of the on-disk tier: the layer file and its bounded pinned page cache."""
+
+    def __init__(self, path: str, B: int, KVH: int, C: int, D: int, dtype, ram_cap: int):
+        self.path = path
+        self.fd = os.open(path, os.O_RDWR | os.O_CREAT | os.O_TRUNC, 0o600)
+        self.B, self.KVH, self.C, self.D, self.dtype = B, KVH, C, D, dtype
+        self.esz = torch.tensor([], dtype=dtype).element_size()
+        self.chunk_bytes = B * KVH * C * D * self.esz       # K (or V) of one chunk
+        self.ram_cap = ram_cap
+        self.cap = 0
+        self.cache_k = self.cache_v = None                  # pinned [B, KVH, cap*C, D]
+        self.slot: Dict[int, int] = {}                      # chunk -> cache slot
+        self.lru: "OrderedDict[int, None]" = OrderedDict()
+        self.free: List[int] = []
+        self.bounce = torch.empty((2, B, KVH, C, D), dtype=dtype, pin_memory=True)
+        self.reads = 0
+
+    def close(self) -> None:
+        if self.fd is not None:
+            os.close(self.fd)
+            self.fd = None
+            try:
+                os.unlink(self.path)
+            except OSError:
+                pass
+
+    def write(self, c0: int, kv: torch.Tensor) -> None:
+        """kv: contiguous host tensor [n, 2, B, KVH, C, D] of chunks c0 .. c0+n-1 (K then V)."""
+        mv = memoryview(kv.view(torch.uint8).numpy().reshape(-1))
+        off, n = c0 * 2 * self.chunk_bytes, 0
+        while n < len(mv):
+            n += os.pwrite(self.fd, mv[n:], off + n)
+        if hasattr(os, "posix_fadvise"):   # written once, read rarely: keep the page cache small
+            os.posix_fadvise(self.fd, off, len(mv), os.POSIX_FADV_DONTNEED)
+
+    def _grow(self, need: int) -> None:
+        cap = min(self.ram_cap, max(64, 2 * self.cap, need))
+        shape = (self.B, self.KVH, cap * self.C, self.D)
+        k = torch.empty(shape, dtype=self.dtype, pin_memory=True)
+        v = torch.empty(shape, dtype=self.dtype, pin_memory=True)
+        if self.cap:
+            k[:, :, :self.cap * self.C].copy_(self.cache_k)
+            v[:, :, :self.cap * self.C].copy_(self.cache_v)
+        self.free.extend(range(self.cap, cap))
+        self.cache_k, self.cache_v, self.cap = k, v, cap
+
+    def ensure_resident(self, chunks: List[int]) -> None:
+        """Every chunk of `chunks` in a cache slot; misses are read from the file, evicting the
+        least recently used chunks that `chunks` does not need."""
+        if len(chunks) > self.ram_cap:
+            raise RuntimeError(f"a decode step needs {len(chunks)} distinct chunks, more than the "
+                               f"{self.ram_cap}-chunk RAM cache holds; raise ram_budget_gb")
+        missing = [c for c in chunks if c not in self.slot]
+        if len(self.slot) + len(missing) > self.cap and self.cap < self.ram_cap:
+            self._grow(len(self.slot) + len(missing))
+        need = set(chunks)
+        C = self.C
+        for c in missing:
+            if self.free:
+                s = self.free.pop()
+            else:
+                victim = next(x for x in self.lru if x not in need)
+                del self.lru[victim]
+                s = self.slot.pop(victim)
+            mv = memoryview(self.bounce.view(torch.uint8).numpy().reshape(-1))
+            off, n = c * 2 * self.chunk_bytes, 0
+            while n < len(mv):
+                r = os.preadv(self.fd, [mv[n:]], off + n)
+                if r == 0:
+                    raise EOFError(f"chunk {c} is not on disk ({self.path})")
+                n += r
+            self.cache_k[:, :, s * C:(s + 1) * C].copy_(self.bounce[0])
+            self.cache_v[:, :, s * C:(s + 1) * C].copy_(self.bounce[1])
+            self.slot[c] = s
+            self.reads += 1
+        for c in chunks:
+            self.lru[c] = None
+            self.lru.move_to_end(c)
+
+
+class FsKVCacheStore(RamKVCacheStore):
+    """On-disk tier (fs_kv_cache_store.py:385-818): the closed-token record lives in one file per
+    layer, chunk-major with K and V adjacent -- chunk c at byte offset c * 2 * chunk_bytes, its K
+    [B, KVH, C, Dh] first, then its V (the reference's layout, :50-64) -- and host RAM holds a
+    bounded pinned page cache of chunk slots (LRU).  As in the RAM tier, the GPU keeps the
+    summaries, the first window and a ring of the last window.  A decode step makes the chunks of
+    its opened groups resident (pread of the misses into the cache), maps group ids to cache
+    slots and gathers them into device staging with the RAM tier's kernel.  Closed chunks are
+    written once (immutable), so evicting them from RAM is free.  Files live in a private
+    directory under ``fs_cache_dir`` (default: the system temporary directory), removed on reset
+    and when the store is collected.  ``ram_budget_gb`` bounds the page caches of all
+    ``num_layers`` layers together; ``ram_cache_chunks`` sets the per-layer slot count directly.
+    The reference's VRAM bank knobs are accepted and unused (summaries are always resident)."""
+
+    def __init__(self, *, ram_budget_gb: float = 12.0, fs_cache_dir: Optional[str] = None,
+                 num_layers: int = 0, ram_cache_chunks: Optional[int] = None,
+                 vram_cache_chunks: int = 256, vram_summary_chunks: int = 4096,
+                 vram_cache_reserve_gb: float = 1.5, **kw):
+        super().__init__(num_layers=num_layers, **kw)
+        self.ram_budget_gb = ram_budget_gb
+        self._dir = tempfile.mkdtemp(prefix="hga_kv_", dir=fs_cache_dir)
+        self._finalizer = weakref.finalize(self, shutil.rmtree, self._dir, True)
+        esz = torch.tensor([], dtype=self.dtype).element_size()
+        chunk_kv = 2 * self.B * self.kvh * self.C * self.dh * esz
+        if ram_cache_chunks is None:
+            ram_cache_chunks = int(ram_budget_gb * (1 << 30)) // (max(num_layers, 1) * chunk_kv)
+        self.ram_cap = max(1, int(ram_cache_chunks))
+        self._fs: Dict[int, _FsLayer] = {}
+
+    def fs_layer(self, layer: int) -> _FsLayer:
+        f = self._fs.get(layer)
+        if f is None:
+            f = _FsLayer(os.path.join(self._dir, f"L{layer}.t"), self.B, self.kvh, self.C,
+                         self.dh, self.dtype, self.ram_cap)
+            self._fs[layer] = f
+        return f
+
+    def reset(self) -> None:
+        super().reset()
+        for f in self._fs.values():
+            f.close()
+        self._fs.clear()
+
+    def close(self) -> None:
+        self.reset()
+        self._finalizer()
+
+    def _new_record(self, *shape):   # no host record: the file is the record
+        B, KVH, _, D = shape
+        return torch.empty((B, KVH, 0, D), dtype=self.dtype)
+
+    def _record_len(self, st):
+        return 0
+
+    def close_chunk(self, layer: int, n: int) -> None:
+        """Chunk n left the active slot: write it to the layer file (and, inside the first
+        window, copy it to the device first-window buffer)."""
+        st = self.layer(layer)
+        C = self.C
+        s = self._ring_slot(st, n) * C
+        f = self.fs_layer(layer)
+        f.bounce[0].copy_(st.ring_k[:, :, s:s + C])
+        f.bounce[1].copy_(st.ring_v[:, :, s:s + C])
+        torch.cuda.current_stream(self.compute_device).synchronize()
+        f.write(n, f.bounce.unsqueeze(0))
+        if n < self.policy.keep_first:
+            st.first_k[:, :, n * C:(n + 1) * C] = st.ring_k[:, :, s:s + C]
+            st.first_v[:, :, n * C:(n + 1) * C] = st.ring_v[:, :, s:s + C]
+
+    def seed(self, layer: int, k_rope, v, n_closed: int) -> None:
+        st = self.layer(layer)
+        self._ensure_hot(st)
+        B, KVH, C, D = self.B, self.kvh, self.C, self.dh
+        S = k_rope.shape[2]
+        f = self.fs_layer(layer)
+        for c0 in range(0, n_closed, 256):    # chunk-major K/V blocks, <= 256 chunks per write
+            n = min(256, n_closed - c0)
+            a, e = c0 * C, (c0 + n) * C
+            kc = k_rope[:, :, a:e].reshape(B, KVH, n, C, D).permute(2, 0, 1, 3, 4)
+            vc = v[:, :, a:e].reshape(B, KVH, n, C, D).permute(2, 0, 1, 3, 4)
+            f.write(c0, torch.stack([kc, vc], 1).contiguous().cpu())
+        kf = min(self.policy.keep_first, n_closed)
+        if kf:
+            st.first_k[:, :, :kf * C] = k_rope[:, :, :kf * C]
+            st.first_v[:, :, :kf * C] = v[:, :, :kf * C]
+        lo = self.policy.hot_last_range(n_closed)[0]
+        for c in range((lo), (S + C - 1) // C):
+            a, b = c * C, min(S, (c + 1) * C)
+            s = self._ring_slot(st, c) * C
+            st.ring_k[:, :, s:s + b - a] = k_rope[:, :, a:b]
+            st.ring_v[:, :, s:s + b - a] = v[:, :, a:b]
+
+    def _resolve(self, layer: int, open_grp: torch.Tensor):
+        """Makes the opened groups' chunks resident and maps group ids (chunk*M + m) to cache
+        ids (slot*M + m); returns the mapped list, the cache size in chunks and the cache's K/V
+        tensors (the record the gather reads; growing the cache replaces them)."""
+        M = self.M
+        og = open_grp.cpu().numpy()                    # waits for routing (and earlier gathers)
+        valid = og >= 0
+        chunks = np.unique(og[valid] // M).tolist()
+        f = self.fs_layer(layer)
+        f.ensure_resident(chunks)
+        mapped = np.full(og.shape, -1, dtype=np.int32)
+        if chunks:
+            table = np.full(int(max(chunks)) + 1, -1, dtype=np.int64)
+            for c in chunks:
+                table[c] = f.slot[c]
+            mapped[valid] = (table[og[valid] // M] * M + og[valid] % M).astype(np.int32)
+        return torch.from_numpy(mapped).to(open_grp.device), f.cap, f.cache_k, f.cache_v
+
+    def sources(self, layer: int):
+        st = self.layer(layer)
+        f = self.fs_layer(layer)
+        if f.cache_k is None:
+            f._grow(1)
+        return dict(recent_k=st.ring_k, recent_v=st.ring_v, ring_chunks=st.ring_R,
+                    first_k=st.first_k, first_v=st.first_v, record_k=f.cache_k,
+                    record_v=f.cache_v, record_on_host=True, staging=self.staging,
+                    resolve=lambda og, _l=layer: self._resolve(_l, og))
+
+
 class RoutedKV:
     """Routing result of one block: the index lists the attention kernel reads -- no
     materialised K/V (compare RoutedKV, chunk_router.py:93-162).  ``attend`` computes the exact
@@ -329,12 +537,14 @@ class RoutedKV:
                                       r["open_thr"], r["Kg"])
         src = dict(self.sources)
         staging = src.pop("staging", None)
+        resolve = src.pop("resolve", None)
         og = r["open_grp"]
         if staging is not None:
-            # host record: gather the opened groups into device staging, attend there
-            sk, sv, og = ops.gather_decode(self.hcfg, self.n_closed, og, r["open_thr"], r["Kg"],
-                                           src["record_k"], src["record_v"],
-                                           src["record_on_host"], staging, q.shape[1])
+            # host record (or its page cache): gather the opened groups into device staging
+            og_rec, n_rec, rk, rv = (resolve(og) if resolve is not None else
+                                     (og, self.n_closed, src["record_k"], src["record_v"]))
+            sk, sv, og = ops.gather_decode(self.hcfg, n_rec, og_rec, r["open_thr"], r["Kg"], rk,
+                                           rv, src["record_on_host"], staging, q.shape[1])
             src.update(record_k=sk, record_v=sv, record_on_host=False)
         return ops.attend_decode(self.hcfg, q, self.n_closed, self.start_pos, open_grp=og,
                                  open_thr=r["open_thr"], Kg=r["Kg"], **src)
@@ -350,11 +560,13 @@ class RoutedKV:
         r = self.routing
         src = dict(self.sources)
         staging = src.pop("staging", None)
+        resolve = src.pop("resolve", None)
         og, op = r["open_grp"], None
         if staging is not None:
-            sk, sv, sg = ops.gather_decode(self.hcfg, self.n_closed, og, r["open_thr"], r["Kg"],
-                                           src["record_k"], src["record_v"],
-                                           src["record_on_host"], staging, q_intra.shape[1])
+            og_rec, n_rec, rk, rv = (resolve(og) if resolve is not None else
+                                     (og, self.n_closed, src["record_k"], src["record_v"]))
+            sk, sv, sg = ops.gather_decode(self.hcfg, n_rec, og_rec, r["open_thr"], r["Kg"], rk,
+                                           rv, src["record_on_host"], staging, q_intra.shape[1])
             src.update(record_k=sk, record_v=sv, record_on_host=False)
             og, op = sg, og
         return ops.attend_decode(self.hcfg, q_intra, self.n_closed, self.start_pos, open_grp=og,

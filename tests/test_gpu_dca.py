@@ -117,7 +117,7 @@ def _qwen(realistic):
     return cfg, attn, Qwen3MoeRotaryEmbedding(cfg).to(DEV), shape
 
 
-@pytest.mark.parametrize("loc", ["vram", "ram"])
+@pytest.mark.parametrize("loc", ["vram", "ram", "fs"])
 @pytest.mark.parametrize("realistic", [False, True], ids=["tiny-fp32", "realistic-bf16"])
 @torch.no_grad()
 def test_wrapper_dca_equals_dense(realistic, loc):

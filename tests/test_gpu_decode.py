@@ -93,15 +93,16 @@ def test_module_decode_matches_reference(name, monkeypatch):
         _same_lists(og, g["dec_open"][i])
 
 
-def test_module_ram_store_equals_vram_store():
+@pytest.mark.parametrize("loc", ["ram", "fs"])
+def test_module_host_stores_equal_vram_store(loc):
     meta, g = load_case("mod_decode")
     x = torch.from_numpy(g["x"]).to(DEV)
     a = _run_module(_module(meta, g, "vram"), x, meta["S"], meta["gen"])
-    b = _run_module(_module(meta, g, "ram"), x, meta["S"], meta["gen"])
+    b = _run_module(_module(meta, g, loc), x, meta["S"], meta["gen"])
     np.testing.assert_array_equal(a, b)
 
 
-@pytest.mark.parametrize("loc", ["vram", "ram"])
+@pytest.mark.parametrize("loc", ["vram", "ram", "fs"])
 @pytest.mark.parametrize("block", [3, 11])
 def test_module_multi_token_blocks_vs_oracle(loc, block):
     """Blocks of several tokens over resident context -- inside one chunk, and crossing chunk

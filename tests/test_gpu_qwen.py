@@ -85,7 +85,7 @@ def _qwen_attn(realistic):
     return cfg, attn, rot, S, C, gs, dtype, tol
 
 
-@pytest.mark.parametrize("loc", ["vram", "ram"])
+@pytest.mark.parametrize("loc", ["vram", "ram", "fs"])
 @pytest.mark.parametrize("realistic", [False, True], ids=["tiny-fp32", "realistic-bf16"])
 @torch.no_grad()
 def test_wrapper_equals_qwen_full_coverage(hga, realistic, loc):

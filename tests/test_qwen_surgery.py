@@ -58,8 +58,9 @@ def test_config_and_arguments():
     assert (d.dca_local, d.dca_ceil) == (8, 48)
     with pytest.raises(ValueError):
         QwenRoutedAttention(model.model.layers[0].self_attn, model.config, cache_location="tape")
-    with pytest.raises(NotImplementedError):
-        QwenRoutedAttention(model.model.layers[0].self_attn, model.config, cache_location="fs")
+    f = QwenRoutedAttention(model.model.layers[0].self_attn, model.config, cache_location="fs",
+                            ram_budget_gb=0.5, fs_cache_dir="/tmp")
+    assert (f.cache_location, f.ram_budget_gb, f.fs_cache_dir) == ("fs", 0.5, "/tmp")
 
 
 def test_cpu_forward_raises():
