@@ -537,25 +537,44 @@ __global__ __launch_bounds__(kDT) void attend_decode_split_kernel(DecAttnArgs A,
     constexpr int KPG = kSplitKeys / NG;             // keys per group
     constexpr int U = 4;                             // keys in flight per group
     constexpr int NQ = DCA ? 3 : 1;                  // query versions
+    static_assert(kDT == kSplitKeys, "one thread locates each key of a split");
     __shared__ int sOG[256], sOT[256], sOP[DCA ? 256 : 1];
     __shared__ float sM[NG], sL[NG];
     __shared__ float sAcc[NG][DH];
+    // the split's keys, located once: K and V row addresses, first visible row, position
+    __shared__ unsigned long long sKP[kSplitKeys], sVP[kSplitKeys];
+    __shared__ int sKT[kSplitKeys], sKX[DCA ? kSplitKeys : 1];
+    __shared__ int sNopen;
     const int split = blockIdx.x, bh = blockIdx.y, b = bh / A.H, h = bh % A.H;
     const int kvh = h / (A.H / A.KVH);
     const int l = lane_id(), j = l & 15, G = (int)(threadIdx.x >> 4);
     const int Kgw = A.Kg > 0 ? A.Kg : 1;
+    if (threadIdx.x == 0) sNopen = 0;
+    __syncthreads();
     for (int i = threadIdx.x; i < A.Kg; i += kDT) {
-        sOG[i] = A.open_grp[(int64_t)bh * Kgw + i];
-        sOT[i] = A.open_thr[(int64_t)bh * Kgw + i];
+        const int og = A.open_grp[(int64_t)bh * Kgw + i], ot = A.open_thr[(int64_t)bh * Kgw + i];
+        sOG[i] = og;
+        sOT[i] = ot;
         if constexpr (DCA) sOP[i] = A.open_pos[(int64_t)bh * Kgw + i];
+        if (og >= 0 && ot >= 0) atomicMax(&sNopen, i + 1);   // length of the opened list
     }
     __syncthreads();
-    int nopen = 0;
-    for (int i = 0; i < A.Kg; ++i)
-        if (sOG[i] >= 0 && sOT[i] >= 0) nopen = i + 1;
     DecKeys<T> keys;
-    keys.init(A, b, kvh, sOG, sOT, nopen);
+    keys.init(A, b, kvh, sOG, sOT, sNopen);
     if constexpr (DCA) keys.sOP = sOP;
+    {
+        const int k = split * kSplitKeys + (int)threadIdx.x;
+        const T* kp = nullptr;
+        const T* vp = nullptr;
+        int thr = kNoRow;
+        int64_t kpos = 0;
+        if (k < keys.a4) keys.locate(k, kp, vp, thr, kpos);
+        sKP[threadIdx.x] = (unsigned long long)kp;
+        sVP[threadIdx.x] = (unsigned long long)vp;
+        sKT[threadIdx.x] = k < keys.a4 ? thr : kNoRow;
+        if constexpr (DCA) sKX[threadIdx.x] = (int)kpos;
+    }
+    __syncthreads();
     const int gk0 = split * kSplitKeys + G * KPG;
     const T* qg = reinterpret_cast<const T*>(A.q) + b * A.q_sb + h * A.q_sh;
     for (int row = 0; row < A.L; ++row) {
@@ -578,12 +597,11 @@ __global__ __launch_bounds__(kDT) void attend_decode_split_kernel(DecAttnArgs A,
             float s[U];
 #pragma unroll
             for (int u = 0; u < U; ++u) {
-                const int k = gk0 + i0 + u;
-                const T* kp = nullptr;
-                vp[u] = nullptr;
-                int thr = kNoRow;
-                int64_t kpos = 0;
-                if (k < keys.a4) keys.locate(k, kp, vp[u], thr, kpos);
+                const int k = gk0 + i0 + u, kl = G * KPG + i0 + u;   // kl: key within the split
+                const T* kp = reinterpret_cast<const T*>(sKP[kl]);
+                vp[u] = reinterpret_cast<const T*>(sVP[kl]);
+                const int thr = sKT[kl];
+                const int64_t kpos = DCA ? sKX[kl] : 0;
                 float d = 0.0f;
                 const bool vis = k < keys.a4 && row >= thr;
                 if (vis) {
