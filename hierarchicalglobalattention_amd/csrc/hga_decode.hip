@@ -601,7 +601,8 @@ __global__ __launch_bounds__(kDT) void attend_decode_split_kernel(DecAttnArgs A,
                 const T* kp = reinterpret_cast<const T*>(sKP[kl]);
                 vp[u] = reinterpret_cast<const T*>(sVP[kl]);
                 const int thr = sKT[kl];
-                const int64_t kpos = DCA ? sKX[kl] : 0;
+                int64_t kpos = 0;
+                if constexpr (DCA) kpos = sKX[kl];
                 float d = 0.0f;
                 const bool vis = k < keys.a4 && row >= thr;
                 if (vis) {
