@@ -4,8 +4,11 @@
 //
 // Router: one 256-thread workgroup per (batch, query head).  Decode scores are few (L rows x
 // pool), so they are computed directly with the canonical fp32 FMA chain (no MFMA pre-pass, no
-// certification needed); the wave selections of hga_select.h handle up to 2048 pool chunks
-// (128K-token contexts at C = 64).
+// certification needed).  Stage 1 walks the pool in segments that fit LDS: each row's running
+// top-Kc list and the pooled running list are merged with the next segment's scores by an exact
+// wave top-k (top-k of a union = top-k of the union of the parts' top-k, and the running list
+// holds lower ids than the segment, so ties still go to the lower id), so any pool length is
+// routed exactly as a single pass would.
 //
 // Attention: one 256-thread workgroup per (batch, query head); the key sequence [first window |
 // last window | opened groups | active chunk] is split over the 4 waves, lanes score one key
@@ -22,7 +25,8 @@ namespace {
 constexpr int kDT = 256;            // threads
 constexpr int kDW = kDT / kWave;     // waves
 constexpr int kMaxL = 64;
-constexpr int kDecJ = 32;            // <= 2048 pool candidates
+constexpr int kDecJ = 32;            // wave selections over <= 2048 candidates
+constexpr int kDecSegJ = 32;         // stage-1 segment: <= 64 * kDecSegJ positions
 
 struct DecRouteArgs {
     const void* q;
@@ -33,6 +37,7 @@ struct DecRouteArgs {
     int64_t gk_sb, gk_sh;
     int32_t *mid, *mid_thr, *n_mid, *open_grp, *open_thr, *n_open;
     int B, H, KVH, L, n_closed, M, kf, kl, Kc, Kg, Kgr, SPD;
+    int cap;       // stage-1 positions per segment pass (running list + segment)
     float scale;
 };
 
@@ -83,6 +88,41 @@ __device__ __forceinline__ uint32_t topk_lds(const float* vals, int n, int k) {
     return exact_topk<J>(kv, v, k);
 }
 
+// Running exact top-k: vals[0..off) / ids[0..off) is the list so far (ascending ids), vals[off..n)
+// the next segment's values (ids id0 + i - off, all above the list's).  Leaves the top-k of both
+// (ties -> lower id) in vals[0..k) / ids[0..k) in ascending id order, -inf / -1 past its length.
+// Every value is in registers before the first write back.
+template <int J>
+__device__ __forceinline__ void merge_topk(float* vals, int* ids, int n, int off, int k, int id0) {
+    const int l = lane_id();
+    float v[J];
+    uint32_t kv[J];
+    int id[J];
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+        const int i = l + 64 * j;
+        v[j] = i < n ? vals[i] : -INFINITY;
+        kv[j] = v[j] == -INFINITY ? 0u : okey(v[j]);
+        id[j] = i < off ? ids[i] : id0 + i - off;
+    }
+    const uint32_t mem = exact_topk<J>(kv, v, k);
+    int base = 0;
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+        const bool m = (mem >> j) & 1u;
+        const uint64_t bal = __ballot(m);
+        if (m) {
+            vals[base + lanes_below(bal)] = v[j];
+            ids[base + lanes_below(bal)] = id[j];
+        }
+        base += __popcll(bal);
+    }
+    for (int i = base + l; i < k; i += kWave) {
+        vals[i] = -INFINITY;
+        ids[i] = -1;
+    }
+}
+
 template <int DT, int DH>
 __global__ __launch_bounds__(kDT) void route_decode_kernel(DecRouteArgs A) {
     typedef typename Elem<DT>::T T;
@@ -95,6 +135,8 @@ __global__ __launch_bounds__(kDT) void route_decode_kernel(DecRouteArgs A) {
     int* sSel = sFirst + SPD;                                   // [64] sorted chunk ids
     int* sThr = sSel + 64;                                      // [64] -1 = never visible
     int* sScal = sThr + 64;                                     // [8]
+    int* sRI = sScal + 8;                                       // [L][Kc] rows' running lists
+    int* sPI = sRI + L * (A.Kc > 0 ? A.Kc : 1);                 // [Kc] pooled running list
 
     const int bh = blockIdx.x, b = bh / A.H, h = bh % A.H, kvh = h / (A.H / A.KVH);
     const int w = threadIdx.x / kWave, l = lane_id();
@@ -122,80 +164,94 @@ __global__ __launch_bounds__(kDT) void route_decode_kernel(DecRouteArgs A) {
                 *reinterpret_cast<const uint4*>(qg + (int64_t)r * A.q_ss + d);
         }
     }
-    for (int i = threadIdx.x; i < SPD; i += kDT) sFirst[i] = kNoRow;
     __syncthreads();
+    // ---- stage 1: pool chunks, segment by segment (:219-241) ---------------------------------
+    const int K = A.Kc;
     const T* ckb = reinterpret_cast<const T*>(A.ck) + b * A.ck_sb + kvh * A.ck_sh;
-    for (int idx = threadIdx.x; idx < L * nmid; idx += kDT) {
-        const int r = idx / nmid, i = idx % nmid;
-        sS[r * SPD + i] = cdot<DT, DH>(sQ + r * DH, ckb + (int64_t)(f_hi + i) * DH, scale);
-    }
-    __syncthreads();
-    for (int i = threadIdx.x; i < nmid; i += kDT) {       // pooled over all rows (:227)
-        float m = -INFINITY;
-        for (int r = 0; r < L; ++r) m = fmaxf(m, sS[r * SPD + i]);
-        sPool[i] = m;
-    }
-    __syncthreads();
-    // per-row requests (:230) -> first requesting row
-    dispatch_j<kDecJ>(nmid, [&](auto jt) {
-        constexpr int J = decltype(jt)::value;
-        for (int r = w; r < L; r += kDW) {
-            const uint32_t mem = topk_lds<J>(sS + r * SPD, nmid, A.Kc);
-#pragma unroll
-            for (int j = 0; j < J; ++j)
-                if ((mem >> j) & 1u) atomicMin(&sFirst[l + 64 * j], r);
+    for (int s0 = 0, off = 0; s0 < nmid; off = K) {
+        const int sl = min(A.cap - off, nmid - s0);
+        for (int idx = threadIdx.x; idx < L * sl; idx += kDT) {
+            const int r = idx / sl, i = idx % sl;
+            sS[r * SPD + off + i] = cdot<DT, DH>(sQ + r * DH, ckb + (int64_t)(f_hi + s0 + i) * DH, scale);
         }
-    });
-    __syncthreads();
-    if (w == 0) {
-        dispatch_j<kDecJ>(nmid, [&](auto jt) {
+        __syncthreads();
+        for (int i = threadIdx.x; i < sl; i += kDT) {     // pooled over all rows (:227)
+            float m = -INFINITY;
+            for (int r = 0; r < L; ++r) m = fmaxf(m, sS[r * SPD + off + i]);
+            sPool[off + i] = m;
+        }
+        __syncthreads();
+        // per-row requests (:230) and the pooled selection (:231), as running lists (row L = pool)
+        dispatch_j<kDecSegJ>(off + sl, [&](auto jt) {
             constexpr int J = decltype(jt)::value;
-            uint32_t sel = topk_lds<J>(sPool, nmid, A.Kc);
-            const int prev = A.n_closed - 1;
-            const int ip = (prev >= f_hi && prev < l_lo) ? prev - f_hi : -1;   // (:232-241)
-            if (ip >= 0 && __ballot(((sel >> (ip / 64)) & 1u) && l == ip % 64) == 0) {
-                // evict the last-ranked selected chunk (lowest pooled score, highest id)
-                uint32_t worst = 0xffffffffu;
-#pragma unroll
-                for (int j = 0; j < J; ++j)
-                    if ((sel >> j) & 1u) worst = min(worst, okey(sPool[l + 64 * j]));
-                worst = (uint32_t)wave_reduce_bits((int)worst, [](int a, int c) {
-                    return (int)min((uint32_t)a, (uint32_t)c);
-                });
-                int victim = -1;
-#pragma unroll
-                for (int j = J - 1; j >= 0; --j) {
-                    const uint64_t m = __ballot(((sel >> j) & 1u) && okey(sPool[l + 64 * j]) == worst);
-                    if (victim < 0 && m) victim = 64 * j + 63 - __clzll(m);
-                }
-                if (victim >= 0 && l == victim % 64) sel &= ~(1u << (victim / 64));
-                if (l == ip % 64) sel |= 1u << (ip / 64);
-            }
-            int base = 0, nvis = 0;
-#pragma unroll
-            for (int j = 0; j < J; ++j) {
-                const int i = l + 64 * j;
-                const bool m = (sel >> j) & 1u;
-                const int thr = i == ip ? 0 : (i < nmid && sFirst[i] < kNoRow ? sFirst[i] : -1);
-                const uint64_t bal = __ballot(m);
-                if (m) {
-                    sSel[base + lanes_below(bal)] = f_hi + i;
-                    sThr[base + lanes_below(bal)] = thr;
-                }
-                base += __popcll(bal);
-                const uint64_t vb = __ballot(m && thr >= 0);
-                if (m && thr >= 0 && nvis + lanes_below(vb) < Kcw) {
-                    o_mid[nvis + lanes_below(vb)] = f_hi + i;
-                    o_mth[nvis + lanes_below(vb)] = thr;
-                }
-                nvis += __popcll(vb);
-            }
-            for (int i = nvis + l; i < Kcw; i += kWave) o_mid[i] = o_mth[i] = -1;
-            if (l == 0) {
-                A.n_mid[bh] = nvis;
-                sScal[0] = base;
+            for (int r = w; r <= L; r += kDW) {
+                if (r < L) merge_topk<J>(sS + r * SPD, sRI + r * K, off + sl, off, K, s0);
+                else merge_topk<J>(sPool, sPI, off + sl, off, K, s0);
             }
         });
+        __syncthreads();
+        s0 += sl;
+    }
+    if (w == 0) {
+        // forced previous chunk (:232-241); K <= 64, one list entry per lane
+        const int prev = A.n_closed - 1;
+        const int ip = (prev >= f_hi && prev < l_lo) ? prev - f_hi : -1;
+        const int id = l < K ? sPI[l] : -1;
+        bool m = id >= 0;
+        const bool forced = ip >= 0 && __ballot(m && id == ip) == 0;
+        if (forced) {
+            // evict the last-ranked selected chunk (lowest pooled score, highest id)
+            const uint32_t ok = m ? okey(sPool[l]) : 0xffffffffu;
+            const uint32_t worst = (uint32_t)wave_reduce_bits((int)ok, [](int a, int c) {
+                return (int)min((uint32_t)a, (uint32_t)c);
+            });
+            const uint64_t cand = __ballot(m && ok == worst);
+            if (cand && l == 63 - __clzll(cand)) m = false;
+        }
+        // ip >= 0 only when the last window is empty, so ip is the pool's highest id and goes last
+        const uint64_t bal = __ballot(m);
+        const int nkeep = __popcll(bal);
+        if (m) sSel[lanes_below(bal)] = f_hi + id;
+        if (forced && l == 0) sSel[nkeep] = f_hi + ip;
+        const uint64_t fb = __ballot(m && id == ip);          // ip selected on its own
+        const int fl = fb ? 63 - __clzll(fb) : -1;
+        const int ns = nkeep + (forced ? 1 : 0);
+        if (l == 0) {
+            sScal[0] = ns;
+            sScal[1] = forced ? nkeep : (fl >= 0 ? __popcll(bal & ((1ull << fl) - 1ull)) : -1);
+        }
+        if (l < ns) sFirst[l] = kNoRow;                       // ns <= Kc < SPD
+    }
+    __syncthreads();
+    {
+        // first row whose own top-Kc holds each selected chunk (:230, :243-250)
+        const int ns = sScal[0];
+        for (int idx = threadIdx.x; idx < L * K; idx += kDT) {
+            const int c = sRI[idx];
+            if (c < 0) continue;
+            const int g = f_hi + c;
+            int lo = 0, hi = ns;
+            while (lo < hi) {
+                const int mid = (lo + hi) >> 1;
+                if (sSel[mid] < g) lo = mid + 1;
+                else hi = mid;
+            }
+            if (lo < ns && sSel[lo] == g) atomicMin(&sFirst[lo], idx / K);
+        }
+    }
+    __syncthreads();
+    if (w == 0) {
+        const int ns = sScal[0], fpos = sScal[1];
+        const int thr = l >= ns ? -1 : (l == fpos ? 0 : (sFirst[l] < kNoRow ? sFirst[l] : -1));
+        if (l < ns) sThr[l] = thr;
+        const uint64_t vb = __ballot(l < ns && thr >= 0);
+        if (l < ns && thr >= 0) {
+            o_mid[lanes_below(vb)] = sSel[l];
+            o_mth[lanes_below(vb)] = thr;
+        }
+        const int nvis = __popcll(vb);
+        for (int i = nvis + l; i < Kcw; i += kWave) o_mid[i] = o_mth[i] = -1;
+        if (l == 0) A.n_mid[bh] = nvis;
     }
     __syncthreads();
     const int nsel = sScal[0];
@@ -956,16 +1012,23 @@ extern "C" int hga_route_decode(const hga_config* cfg, int32_t L, int32_t n_clos
     windows(n_closed, a.kf, a.kl, &f_hi, &l_lo);
     const int nmid = l_lo > f_hi ? l_lo - f_hi : 0;
     HGA_REQUIRE(a.Kc <= 64, HGA_ERR_UNSUPPORTED, "hga_route_decode: top-k chunks %d > 64", a.Kc);
-    HGA_REQUIRE(nmid <= kDecJ * 64 && a.Kc * a.M <= kDecJ * 64, HGA_ERR_UNSUPPORTED,
-                "hga_route_decode: pool %d exceeds %d chunks", nmid, kDecJ * 64);
-    const int W = (nmid > a.Kc * a.M ? nmid : a.Kc * a.M) + 1;
-    a.SPD = W | 1;
+    const int T2max = a.Kc * a.M;
+    HGA_REQUIRE(T2max <= kDecJ * 64, HGA_ERR_UNSUPPORTED,
+                "hga_route_decode: %d candidate groups exceed %d", T2max, kDecJ * 64);
+    // LDS: sQ [L][D] | sS [L][SPD] | sPool, sFirst [SPD] | sSel, sThr [64] | sScal [8] |
+    // sRI [L][Kc] | sPI [Kc]; the stage-1 segment pass gets what the SPD columns allow
     const int D = cfg->head_dim;
     const size_t esz = cfg->dtype == HGA_DTYPE_BF16 ? 2 : 4;
-    const size_t lds = sizeof(float) * ((size_t)L * a.SPD + a.SPD) + sizeof(int) * (a.SPD + 128 + 8) +
-                       esz * (size_t)L * D + 16;
-    HGA_REQUIRE(lds <= 163840, HGA_ERR_UNSUPPORTED,
-                "hga_route_decode: %zu bytes of LDS for L=%d x pool %d", lds, L, nmid);
+    const int Kcw = a.Kc > 0 ? a.Kc : 1;
+    const size_t fixed = esz * (size_t)L * D + sizeof(int) * (136 + (size_t)(L + 1) * Kcw) + 16;
+    const int64_t spd_max = ((int64_t)163840 - (int64_t)fixed) / (int64_t)(sizeof(float) * (L + 2));
+    a.cap = (int)(spd_max - 2 < 64 * kDecSegJ ? spd_max - 2 : 64 * kDecSegJ);
+    HGA_REQUIRE(a.cap >= a.Kc + 64 && T2max + 2 <= spd_max, HGA_ERR_UNSUPPORTED,
+                "hga_route_decode: L=%d x head_dim %d x %d groups leave no LDS for the pool", L, D,
+                T2max);
+    const int W = (nmid < a.cap ? nmid : a.cap) > T2max ? (nmid < a.cap ? nmid : a.cap) : T2max;
+    a.SPD = (W + 1) | 1;
+    const size_t lds = fixed + sizeof(float) * (size_t)(L + 2) * a.SPD;
     if (a.Kc > 0) {
         const int64_t ve = esz == 2 ? 8 : 4;
         HGA_REQUIRE(chunk_k && group_k, HGA_ERR_ARG, "hga_route_decode: NULL summaries");

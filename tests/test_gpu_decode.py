@@ -172,6 +172,10 @@ ROUTE_CASES = [
     (1, 4, 2, 64, 64, 16, 4, 64, 0, 0, 9, 2, torch.float32),          # tg > Kc*M, no windows
     (1, 4, 2, 128, 64, 16, 16, 64, 2, 8, 12, 1, torch.bfloat16),      # pool smaller than tc
     (1, 4, 2, 128, 64, 16, 16, 64, 2, 8, 6, 1, torch.bfloat16),       # everything in windows
+    (1, 4, 1, 128, 64, 16, 16, 64, 2, 8, 8191, 1, torch.bfloat16),    # 512K context, 17 segments
+    (1, 4, 2, 128, 64, 16, 16, 64, 2, 8, 2047, 64, torch.bfloat16),   # 128K context, 64-row block
+    (1, 4, 2, 128, 64, 16, 64, 256, 2, 8, 1200, 64, torch.float32),   # Kc 64, fp32: short segments
+    (1, 4, 2, 64, 64, 16, 4, 64, 0, 0, 1300, 2, torch.float32),       # forced previous, long pool
 ]
 
 
@@ -209,6 +213,30 @@ def test_route_decode_exact_ties(L):
                             kf, kl, tc, tg, oracle.attn_scale(Dh))
     for key in ("mid", "mid_thr", "open_grp", "open_thr"):
         _same_lists(r[key].cpu().numpy(), o[key])
+
+
+@pytest.mark.parametrize("L", [1, 64])
+def test_route_decode_periodic_pool(L):
+    """Chunk and group summaries repeat with period 7 over a 1500-chunk pool: every selection
+    boundary is a tie spread over all stage-1 segments, so the running lists must keep the lowest
+    ids of each score class (chunk_router.py:227-231 take torch.topk over the whole pool)."""
+    B, H, KVH, Dh, C, gs, tc, tg, kf, kl, n_closed = 1, 4, 2, 128, 64, 16, 16, 64, 2, 8, 1500
+    M = C // gs
+    print(f"[decode] route periodic L={L}", flush=True)
+    gen = torch.Generator().manual_seed(1234 + L)
+    base_c = torch.randn(B, KVH, 7, Dh, generator=gen)
+    base_g = torch.randn(B, KVH, 7, M, Dh, generator=gen)
+    idx = torch.arange(n_closed) % 7
+    ck, gk = base_c[:, :, idx].to(torch.bfloat16), base_g[:, :, idx].to(torch.bfloat16)
+    q = torch.randn(B, H, L, Dh, generator=gen).to(torch.bfloat16)
+    cfg = _cfg(B, H, KVH, Dh, C, gs, tc, tg, kf, kl, torch.bfloat16)
+    r = ops.route_decode(cfg, q.to(DEV), ck.to(DEV), gk.to(DEV), n_closed)
+    o = oracle.route_decode(q.float().numpy(), ck.float().numpy(), gk.float().numpy(), n_closed,
+                            kf, kl, tc, tg, oracle.attn_scale(Dh))
+    for key in ("mid", "mid_thr", "open_grp", "open_thr"):
+        _same_lists(r[key].cpu().numpy(), o[key])
+    # the pooled top-16 of a period-7 pool is the best class's 16 lowest-id members
+    assert (o["mid"] < oracle.windows(n_closed, kf, kl)[0] + 7 * 16).all()
 
 
 def _history(gen, B, KVH, T, Dh, dt):
