@@ -206,6 +206,66 @@ def attend_prefill_workspace(cfg: HgaConfig, S: int) -> int:
     return n.value
 
 
+def attend_prefill_bwd(cfg: HgaConfig, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
+                       out: torch.Tensor, dout: torch.Tensor, open_grp: torch.Tensor,
+                       open_thr: torch.Tensor, Kg: int):
+    """Gradients (dq [B,H,S,Dh], dk, dv [B,KVH,S,Dh]) of attend_prefill's output `out` for the
+    upstream gradient dout, in q's dtype."""
+    _dev(q, k, v, out, dout, open_grp, open_thr)
+    B, H, S, D = q.shape
+    dq = torch.empty((B, H, S, D), dtype=q.dtype, device=q.device)
+    dk = torch.empty(k.shape, dtype=q.dtype, device=q.device)
+    dv = torch.empty(v.shape, dtype=q.dtype, device=q.device)
+    if dout.stride(-1) != 1:
+        dout = dout.contiguous()
+    og = open_grp.contiguous()
+    ot = open_thr.contiguous()
+    n = ctypes.c_int64()
+    check(lib().hga_attend_prefill_bwd_workspace(ctypes.byref(cfg), S, ctypes.byref(n)),
+          "hga_attend_prefill_bwd_workspace")
+    ws = torch.empty(max(n.value, 16), dtype=torch.uint8, device=q.device)
+    check(lib().hga_attend_prefill_bwd(
+        ctypes.byref(cfg), S, _p(q), *_s4(q), _p(k), *_s4(k), _p(v), *_s4(v), _p(out), *_s4(out),
+        _p(dout), *_s4(dout), _p(og), _p(ot), Kg, _p(dq), *_s4(dq), _p(dk), *_s4(dk), _p(dv),
+        *_s4(dv), _p(ws), n.value, _stream()), "hga_attend_prefill_bwd")
+    return dq, dk, dv
+
+
+class RoutedAttentionFunction(torch.autograd.Function):
+    """attend_prefill with a backward through hga_attend_prefill_bwd (routing lists are
+    constants: the reference's top-k selections carry no gradient)."""
+
+    @staticmethod
+    def forward(ctx, q, k, v, open_grp, open_thr, Kg, cfg):
+        out = attend_prefill(cfg, q, k, v, open_grp, open_thr, Kg)
+        ctx.save_for_backward(q, k, v, out, open_grp, open_thr)
+        ctx.Kg, ctx.cfg = Kg, cfg
+        return out
+
+    @staticmethod
+    def backward(ctx, dout):
+        q, k, v, out, og, ot = ctx.saved_tensors
+        dq, dk, dv = attend_prefill_bwd(ctx.cfg, q, k, v, out, dout, og, ot, ctx.Kg)
+        return dq, dk, dv, None, None, None, None
+
+
+class RopeFunction(torch.autograd.Function):
+    """rope with its transpose as the backward: the rotation by -theta (cos, -sin)."""
+
+    @staticmethod
+    def forward(ctx, cfg, x, cos, sin):
+        ctx.cfg = cfg
+        ctx.save_for_backward(cos, sin)
+        return rope(cfg, x, cos, sin)
+
+    @staticmethod
+    def backward(ctx, g):
+        cos, sin = ctx.saved_tensors
+        if g.stride(-1) != 1:
+            g = g.contiguous()
+        return None, rope(ctx.cfg, g, cos, -sin), None, None
+
+
 def decode_widths(cfg: HgaConfig, n_closed: int):
     kc, kg = ctypes.c_int32(), ctypes.c_int32()
     check(lib().hga_decode_widths(ctypes.byref(cfg), n_closed, ctypes.byref(kc), ctypes.byref(kg)),

@@ -91,14 +91,33 @@ class HierarchicalGlobalAttentionRouted(nn.Module):
         if self.layer_idx == 0 and start_pos == 0:
             router.reset()
         hc = router.hcfg(B, x.dtype)
-        q_rope = ops.rope(hc, q_raw, cos[:, 0], sin[:, 0])
-        k_rope = ops.rope(hc, k_raw, cos[:, 0], sin[:, 0])
+        # training: gradients flow through RoPE and the exact attention (hga_attend_prefill_bwd);
+        # routing runs on detached tensors (top-k selections carry no gradient in the reference)
+        train = torch.is_grad_enabled() and (q_raw.requires_grad or k_raw.requires_grad or
+                                             v.requires_grad)
+        if train:
+            q_rope = ops.RopeFunction.apply(hc, q_raw, cos[:, 0], sin[:, 0])
+            k_rope = ops.RopeFunction.apply(hc, k_raw, cos[:, 0], sin[:, 0])
+        else:
+            q_rope = ops.rope(hc, q_raw, cos[:, 0], sin[:, 0])
+            k_rope = ops.rope(hc, k_raw, cos[:, 0], sin[:, 0])
         cos_r, sin_r = cos[:1].to(x.dtype), sin[:1].to(x.dtype)
-        segments = router.route_query_block(self.layer_idx, q_rope, k_rope, k_raw, v, start_pos,
-                                            cos=cos_r, sin=sin_r)
-        out_heads = q_rope.new_empty(B, H, S, Dh)
-        for routed, lo, hi in segments:
-            out_heads[:, :, lo:hi] = routed.attend(q_rope[:, :, lo:hi], use_summaries=False)
+        with torch.no_grad():
+            segments = router.route_query_block(self.layer_idx, q_rope.detach(), k_rope.detach(),
+                                                k_raw.detach(), v.detach(), start_pos,
+                                                cos=cos_r, sin=sin_r)
+        if train:
+            if len(segments) != 1 or not segments[0][0].chunked:
+                raise NotImplementedError(
+                    "backward is supported for a fresh multi-chunk block (start_pos 0, "
+                    "S > chunk_size); decode blocks run without gradients")
+            r = segments[0][0].routing
+            out_heads = ops.RoutedAttentionFunction.apply(q_rope, k_rope, v, r["open_grp"],
+                                                          r["open_thr"], r["Kg"], hc)
+        else:
+            out_heads = q_rope.new_empty(B, H, S, Dh)
+            for routed, lo, hi in segments:
+                out_heads[:, :, lo:hi] = routed.attend(q_rope[:, :, lo:hi], use_summaries=False)
         out = self.o_proj(out_heads.transpose(1, 2).contiguous().view(B, S, H * Dh))
         return out, {}
 

@@ -148,6 +148,30 @@ int hga_attend_prefill(const hga_config* cfg, int32_t S, const void* q, int64_t 
  * ordered).  No counterpart in the reference, whose attend materialises K/V instead. */
 int32_t hga_attend_prefill_workspace(const hga_config* cfg, int32_t S, int64_t* bytes);
 
+/*
+ * Gradient of hga_attend_prefill for an upstream gradient dout (the reference trains through
+ * the same attention with torch autograd, HierarchicalGlobalAttentionRouted.py:137-177 over the
+ * working set of vectorized.py:404-490; routing carries no gradient).  q/out/dout/dq:
+ * [B, H, S, Dh]; k/v/dk/dv: [B, KVH, S, Dh]; out is hga_attend_prefill's output for the same
+ * inputs and routing.  dk/dv sum the contributions of every query head of a KV head.
+ * chunk_size <= 64.  workspace: hga_attend_prefill_bwd_workspace bytes, 16-byte aligned (fp32
+ * accumulators, cleared by the call's own kernels).
+ */
+int hga_attend_prefill_bwd(const hga_config* cfg, int32_t S, const void* q, int64_t q_sb,
+                           int64_t q_sh, int64_t q_ss, const void* k, int64_t k_sb, int64_t k_sh,
+                           int64_t k_ss, const void* v, int64_t v_sb, int64_t v_sh, int64_t v_ss,
+                           const void* out, int64_t o_sb, int64_t o_sh, int64_t o_ss,
+                           const void* dout, int64_t g_sb, int64_t g_sh, int64_t g_ss,
+                           const int32_t* open_grp, const int32_t* open_thr, int32_t Kg,
+                           void* dq, int64_t dq_sb, int64_t dq_sh, int64_t dq_ss, void* dk,
+                           int64_t dk_sb, int64_t dk_sh, int64_t dk_ss, void* dv, int64_t dv_sb,
+                           int64_t dv_sh, int64_t dv_ss, void* workspace, int64_t workspace_bytes,
+                           void* stream);
+
+/* Device scratch bytes hga_attend_prefill_bwd needs (2*B*KVH*S*Dh fp32).  No counterpart in the
+ * reference, where autograd allocates the gradient buffers. */
+int32_t hga_attend_prefill_bwd_workspace(const hga_config* cfg, int32_t S, int64_t* bytes);
+
 /* Widths of the decode routing outputs with n_closed closed chunks: the routing pool is
  * [f_hi, l_lo) of ChunkPlacementPolicy (chunk_placement_policy.py:27-38), Kc = min(topk_chunks,
  * |pool|), Kg = min(topk_groups, Kc*C/gs)  (chunk_router.py:213-257). */

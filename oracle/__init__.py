@@ -168,6 +168,23 @@ def attend_prefill(q, k, v, C, gs, keep_first, keep_last, open_grp, open_thr, sc
     return out
 
 
+def attend_prefill_bwd(q, k, v, dout, C, gs, keep_first, keep_last, open_grp, open_thr, scale):
+    """Exact (double) gradients (dq, dk, dv) of attend_prefill's attention for upstream dout."""
+    q, pq = _f(q)
+    k, pk = _f(k)
+    v, pv = _f(v)
+    dout, pg = _f(dout)
+    B, H, S, Dh = q.shape
+    KVH = k.shape[1]
+    og = np.ascontiguousarray(open_grp, np.int32)
+    ot = np.ascontiguousarray(open_thr, np.int32)
+    dq, dk, dv = np.empty_like(q), np.empty_like(k), np.empty_like(v)
+    lib().orc_attend_prefill_bwd(pq, pk, pv, pg, B, H, KVH, S, Dh, C, gs, keep_first, keep_last,
+                                 _i(og), _i(ot), og.shape[-1], ctypes.c_float(scale),
+                                 _f(dq)[1], _f(dk)[1], _f(dv)[1])
+    return dq, dk, dv
+
+
 def route_decode(q, chunk_k, group_k, n_closed, keep_first, keep_last, topk_chunks,
                  topk_groups, scale):
     """q [B,H,L,Dh]; chunk_k [B,KVH,cap,Dh]; group_k [B,KVH,cap,M,Dh] (store layout)."""

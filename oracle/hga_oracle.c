@@ -454,6 +454,102 @@ void orc_attend_prefill(const float* q, const float* k, const float* v, int B, i
 }
 
 /* ------------------------------------------------------------------------------------------
+ * Gradient of the prefill attention above (the reference trains through it with torch
+ * autograd: HierarchicalGlobalAttentionRouted.forward, :137-177, over the gathered working set
+ * of vectorized.py:404-490; routing decisions carry no gradient).  Same per-row key set as
+ * orc_attend_prefill; for row i with keys J(i), in double precision:
+ *   p_j = softmax_j(scale q_i.k_j),  dp_j = dout_i.v_j,  D_i = sum_j p_j dp_j,
+ *   ds_j = p_j (dp_j - D_i),  dq_i = scale sum_j ds_j k_j,
+ *   dk_j += scale ds_j q_i,  dv_j += p_j dout_i   (summed over rows and the heads of a KV head).
+ * q, dout, dq [B,H,S,Dh]; k, v, dk, dv [B,KVH,S,Dh]; open lists as orc_attend_prefill.
+ * ------------------------------------------------------------------------------------------ */
+void orc_attend_prefill_bwd(const float* q, const float* k, const float* v, const float* dout,
+                            int B, int H, int KVH, int S, int Dh, int C, int gs, int kf, int kl,
+                            const int* open_grp, const int* open_thr, int Kgw, float scale,
+                            float* dq, float* dk, float* dv) {
+    const int N = (S + C - 1) / C, M = C / gs, rep = H / KVH;
+    long* keys = (long*)malloc(sizeof(long) * ((long)S + 16));
+    double* p = (double*)malloc(sizeof(double) * ((long)S + 16));
+    double* dpv = (double*)malloc(sizeof(double) * ((long)S + 16));
+    double* gq = (double*)malloc(sizeof(double) * (Dh + 1));
+    const long nkv = (long)B * KVH * S * Dh;
+    double* gk = (double*)calloc(nkv + 1, sizeof(double));
+    double* gv = (double*)calloc(nkv + 1, sizeof(double));
+    for (int b = 0; b < B; ++b)
+        for (int h = 0; h < H; ++h) {
+            const int kvh = h / rep;
+            const long kvo = ((long)b * KVH + kvh) * S * Dh;
+            const float* kb = k + kvo;
+            const float* vb = v + kvo;
+            for (int n = 0; n < N; ++n) {
+                int f_hi = kf > 0 ? (n < kf ? n : kf) : 0;
+                int l_lo = n;
+                if (kl > 0) {
+                    int x = n - kl > kf ? n - kl : kf;
+                    l_lo = x < n ? x : n;
+                }
+                const int* og = open_grp + (((long)b * H + h) * N + n) * Kgw;
+                const int* ot = open_thr + (((long)b * H + h) * N + n) * Kgw;
+                int rows = S - n * C < C ? S - n * C : C;
+                for (int t = 0; t < rows; ++t) {
+                    int nk = 0;
+                    for (long i = 0; i < (long)f_hi * C; ++i) keys[nk++] = i;
+                    for (long i = (long)l_lo * C; i < (long)n * C; ++i) keys[nk++] = i;
+                    for (int j = 0; j < Kgw; ++j)
+                        if (og[j] >= 0 && ot[j] >= 0 && ot[j] <= t) {
+                            long base = (long)(og[j] / M) * C + (og[j] % M) * gs;
+                            for (int e = 0; e < gs; ++e) keys[nk++] = base + e;
+                        }
+                    for (int j = 0; j <= t; ++j) keys[nk++] = (long)n * C + j;
+                    const long ro = (((long)b * H + h) * S + (long)n * C + t) * Dh;
+                    const float* qr = q + ro;
+                    const float* gr = dout + ro;
+                    double mx = -INFINITY, den = 0.0, Dsum = 0.0;
+                    for (int j = 0; j < nk; ++j) {
+                        double sdot = 0.0, vdot = 0.0;
+                        for (int d = 0; d < Dh; ++d) {
+                            sdot += (double)qr[d] * (double)kb[keys[j] * Dh + d];
+                            vdot += (double)gr[d] * (double)vb[keys[j] * Dh + d];
+                        }
+                        p[j] = sdot * scale;
+                        dpv[j] = vdot;
+                        if (p[j] > mx) mx = p[j];
+                    }
+                    for (int j = 0; j < nk; ++j) {
+                        p[j] = exp(p[j] - mx);
+                        den += p[j];
+                    }
+                    for (int j = 0; j < nk; ++j) {
+                        p[j] /= den;
+                        Dsum += p[j] * dpv[j];
+                    }
+                    for (int d = 0; d < Dh; ++d) gq[d] = 0.0;
+                    for (int j = 0; j < nk; ++j) {
+                        const double ds = p[j] * (dpv[j] - Dsum);
+                        const long ko = keys[j] * Dh;
+                        for (int d = 0; d < Dh; ++d) {
+                            gq[d] += ds * (double)kb[ko + d];
+                            gk[kvo + ko + d] += (double)scale * ds * (double)qr[d];
+                            gv[kvo + ko + d] += p[j] * (double)gr[d];
+                        }
+                    }
+                    for (int d = 0; d < Dh; ++d) dq[ro + d] = (float)((double)scale * gq[d]);
+                }
+            }
+        }
+    for (long i = 0; i < nkv; ++i) {
+        dk[i] = (float)gk[i];
+        dv[i] = (float)gv[i];
+    }
+    free(keys);
+    free(p);
+    free(dpv);
+    free(gq);
+    free(gk);
+    free(gv);
+}
+
+/* ------------------------------------------------------------------------------------------
  * Decode routing for an L-token block inside the active chunk (ChunkRouter._route_decision,
  * chunk_router.py:187-277).  Window ranges from ChunkPlacementPolicy
  * (chunk_placement_policy.py:27-38): f_hi = min(kf, n_closed), l_lo = min(max(kf,
