@@ -153,8 +153,32 @@ def run_gpu(args):
     rows = torch.clamp(S - n_idx * C, max=C)
     nsel = r_t["n_sel"].long().cpu().sum(dim=(0, 1))             # per chunk, summed over heads
     score_flops = float(2 * D * (c["H"] * B * (rows * pool).sum() + (rows * nsel * M).sum()))
+    bwd = None
+    if not args.no_backward:
+        # training leg: gradient of the routed attention (hga_attend_prefill_bwd) for an upstream
+        # gradient, same block and routing; 5 products per visible (query, key) pair
+        q = ops.rope(hc, q_raw, cos, sin)
+        k_rope = ops.rope(hc, k_raw, cos, sin)
+        out = ops.attend_prefill(hc, q, k_rope, v, r_t["open_grp"], r_t["open_thr"], r_t["Kg"])
+        dout = torch.randn_like(out)
+        args_b = (hc, q, k_rope, v, out, dout, r_t["open_grp"], r_t["open_thr"], r_t["Kg"])
+        ops.attend_prefill_bwd(*args_b)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        reps = 3
+        e0.record()
+        for _ in range(reps):
+            ops.attend_prefill_bwd(*args_b)
+        e1.record()
+        torch.cuda.synchronize()
+        bms = e0.elapsed_time(e1) / reps
+        bflops = 10.0 * c["Dh"] * pairs
+        bwd = {"kernel": "attend_bwd_mfma_kernel<128> (+ accumulator clear and conversion)",
+               "ms": bms, "algorithmic_flops": bflops,
+               "achieved": bflops / (bms * 1e-3) / 1e12, "unit": "TFLOP/s",
+               "frac": bflops / (bms * 1e-3) / 1e12 / MFMA_BF16_PEAK_TFLOPS}
     return dict(ms=ms, stage_ms=st_ms, pairs=pairs, flops=flops, tokens=B * S,
-                route_bytes=route_bytes, score_flops=score_flops)
+                route_bytes=route_bytes, score_flops=score_flops, backward=bwd)
 
 
 def copy_calibration(nbytes: int = 1 << 30, reps: int = 3):
@@ -307,6 +331,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-budget", type=float, default=15.0)
     ap.add_argument("--no-decode", action="store_true", help="skip the decode legs (c4, c5)")
+    ap.add_argument("--no-backward", action="store_true", help="skip the attention backward leg")
     ap.add_argument("--decode-steps", type=int, default=256)
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run only a 1 GiB device copy (scales the HBM byte counters)")
@@ -378,6 +403,7 @@ def main():
                                "frac": attn_tflops / MFMA_BF16_PEAK_TFLOPS,
                                "algorithmic_flops": g["flops"], "visible_qk_pairs": g["pairs"]},
         "decode": dec,
+        "backward": g["backward"],
         "cpu_baseline": cpu,
         "host": {"cpu": platform.processor() or platform.machine(), "torch": torch.__version__},
     }

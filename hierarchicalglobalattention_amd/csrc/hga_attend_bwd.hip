@@ -236,6 +236,271 @@ __global__ __launch_bounds__(kBT) void attend_bwd_valu_kernel(BwdArgs P) {
     }
 }
 
+// ------------------------------------------------------------------------------------------
+// bf16 MFMA kernel: 128 threads, wave w owns query rows 32w..32w+31, 32-key tiles
+// ------------------------------------------------------------------------------------------
+constexpr int kMT = 128;
+constexpr int kMK = 32;                 // keys per tile
+
+template <int DH>
+struct MfmaLds {
+    static constexpr int KSTR = DH + 8;      // sK / sV row stride (bf16 elements)
+    static constexpr int KTSTR = kMK + 4;    // sKt row stride
+    static constexpr int QTSTR = kBR + 8;    // sQt / sGt row stride
+    static constexpr int PSTR = kBR + 8;     // sP / sDS row stride
+    static constexpr size_t bytes = 2 * (2 * (size_t)DH * QTSTR + 2 * (size_t)kMK * KSTR +
+                                         (size_t)DH * KTSTR + 2 * (size_t)kMK * PSTR);
+};
+
+__device__ __forceinline__ bf16x8 ld8(const uint16_t* p) {
+    return __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(p));
+}
+
+// rows [r0, r0 + 2*npairs) of a [rows][DH] bf16 matrix (row stride ss) -> dst[d][row]
+template <int DH, int STR>
+__device__ __forceinline__ void transpose_rows(const uint16_t* src, int64_t ss, int rows,
+                                               uint16_t* dst) {
+    constexpr int CPR = DH / 8;
+    for (int c = threadIdx.x; c < (kBR / 2) * CPR; c += kMT) {
+        const int rp = c / CPR, dg = c % CPR;
+        const int ra = 2 * rp, rb = 2 * rp + 1;
+        uint4 u0 = make_uint4(0u, 0u, 0u, 0u), u1 = u0;
+        if (ra < rows) u0 = *reinterpret_cast<const uint4*>(src + ra * ss + dg * 8);
+        if (rb < rows) u1 = *reinterpret_cast<const uint4*>(src + rb * ss + dg * 8);
+        auto put = [&](int e, uint32_t x0, uint32_t x1) {
+            *reinterpret_cast<uint32_t*>(&dst[(dg * 8 + 2 * e) * STR + ra]) =
+                (x0 & 0xffffu) | (x1 << 16);
+            *reinterpret_cast<uint32_t*>(&dst[(dg * 8 + 2 * e + 1) * STR + ra]) =
+                (x0 >> 16) | (x1 & 0xffff0000u);
+        };
+        put(0, u0.x, u1.x);
+        put(1, u0.y, u1.y);
+        put(2, u0.z, u1.z);
+        put(3, u0.w, u1.w);
+    }
+}
+
+template <int DH>
+__global__ __launch_bounds__(kMT) void attend_bwd_mfma_kernel(BwdArgs P) {
+    typedef MfmaLds<DH> L;
+    constexpr int KS = DH / 16, DB = DH / 32, CPR = DH / 8;
+    const AttnArgs& A = P.a;
+    extern __shared__ __align__(16) uint16_t lds[];
+    uint16_t* sQt = lds;                           // [DH][QTSTR] Q^T of the chunk's rows
+    uint16_t* sGt = sQt + DH * L::QTSTR;           // dO^T
+    uint16_t* sK = sGt + DH * L::QTSTR;            // [kMK][KSTR]
+    uint16_t* sV = sK + kMK * L::KSTR;
+    uint16_t* sKt = sV + kMK * L::KSTR;            // [DH][KTSTR]
+    uint16_t* sP = sKt + DH * L::KTSTR;            // [kMK][PSTR] P^T (bf16)
+    uint16_t* sDS = sP + kMK * L::PSTR;            // dS^T
+    int* sPos = reinterpret_cast<int*>(sDS + kMK * L::PSTR);
+    int* sThr = sPos + kMK;
+    int* sOG = sThr + kMK;
+    int* sOT = sOG + (A.Kg > 0 ? A.Kg : 1);
+
+    int b, h, n;
+    block_coords(A.B * A.H * A.N, A.B, A.H, A.KVH, A.N, &b, &h, &n);
+    const int kvh = h / (A.H / A.KVH);
+    int rows = A.S - n * A.C;
+    if (rows > A.C) rows = A.C;
+    KeySeq ks;
+    setup_keys(A, b, h, n, rows, sOG, sOT, ks, kMT);
+
+    const int w = threadIdx.x / kWave, l = lane_id(), hl = l / 32;
+    const int row = w * 32 + (l % 32);
+    const bool rv = row < rows;
+    const int64_t r0 = (int64_t)n * A.C;
+    const uint16_t* qp = reinterpret_cast<const uint16_t*>(A.q) + b * A.q_sb + h * A.q_sh + r0 * A.q_ss;
+    const uint16_t* op = reinterpret_cast<const uint16_t*>(A.out) + b * A.o_sb + h * A.o_sh + r0 * A.o_ss;
+    const uint16_t* gp = reinterpret_cast<const uint16_t*>(P.dout) + b * P.g_sb + h * P.g_sh + r0 * P.g_ss;
+    const uint16_t* kp = reinterpret_cast<const uint16_t*>(A.k) + b * A.k_sb + kvh * A.k_sh;
+    const uint16_t* vp = reinterpret_cast<const uint16_t*>(A.v) + b * A.v_sb + kvh * A.v_sh;
+
+    // this lane's query row as MFMA B operands (8 dims of each 16-dim step), D_row = dO.O
+    bf16x8 qb[KS], gb[KS];
+    float Dr = 0.0f;
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+        const int col = s * 16 + 8 * hl;
+        uint4 uq = make_uint4(0u, 0u, 0u, 0u), ug = uq, uo = uq;
+        if (rv) {
+            uq = *reinterpret_cast<const uint4*>(qp + row * A.q_ss + col);
+            ug = *reinterpret_cast<const uint4*>(gp + row * P.g_ss + col);
+            uo = *reinterpret_cast<const uint4*>(op + row * A.o_ss + col);
+        }
+        qb[s] = __builtin_bit_cast(bf16x8, uq);
+        gb[s] = __builtin_bit_cast(bf16x8, ug);
+        const uint32_t g4[4] = {ug.x, ug.y, ug.z, ug.w}, o4[4] = {uo.x, uo.y, uo.z, uo.w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            Dr = fmaf(bf16_to_f((uint16_t)(g4[e] & 0xffffu)), bf16_to_f((uint16_t)(o4[e] & 0xffffu)), Dr);
+            Dr = fmaf(bf16_to_f((uint16_t)(g4[e] >> 16)), bf16_to_f((uint16_t)(o4[e] >> 16)), Dr);
+        }
+    }
+    Dr += __shfl_xor(Dr, 32, kWave);
+    transpose_rows<DH, L::QTSTR>(qp, A.q_ss, rows, sQt);
+    transpose_rows<DH, L::QTSTR>(gp, P.g_ss, rows, sGt);
+
+    const float c2 = A.scale * 1.4426950408889634f;
+    const int ntiles = (ks.a4 + kMK - 1) / kMK;
+    auto load_tile = [&](int tile, bool bwd) {
+        if (threadIdx.x < kMK) {
+            int pos, thr;
+            ks.get(tile * kMK + threadIdx.x, pos, thr);
+            sPos[threadIdx.x] = pos;
+            sThr[threadIdx.x] = thr;
+        }
+        __syncthreads();
+        for (int c = threadIdx.x; c < kMK * CPR; c += kMT) {
+            const int kk = c / CPR, dp = c % CPR;
+            const int64_t pos = sPos[kk];
+            *reinterpret_cast<uint4*>(&sK[kk * L::KSTR + dp * 8]) =
+                *reinterpret_cast<const uint4*>(kp + pos * A.k_ss + dp * 8);
+            if (bwd)
+                *reinterpret_cast<uint4*>(&sV[kk * L::KSTR + dp * 8]) =
+                    *reinterpret_cast<const uint4*>(vp + pos * A.v_ss + dp * 8);
+        }
+        if (bwd) {
+            for (int c = threadIdx.x; c < (kMK / 2) * CPR; c += kMT) {
+                const int kp2 = c / CPR, dg = c % CPR;
+                const uint4 u0 = *reinterpret_cast<const uint4*>(kp + (int64_t)sPos[2 * kp2] * A.k_ss + dg * 8);
+                const uint4 u1 = *reinterpret_cast<const uint4*>(kp + (int64_t)sPos[2 * kp2 + 1] * A.k_ss + dg * 8);
+                const uint32_t a0[4] = {u0.x, u0.y, u0.z, u0.w}, a1[4] = {u1.x, u1.y, u1.z, u1.w};
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    *reinterpret_cast<uint32_t*>(&sKt[(dg * 8 + 2 * e) * L::KTSTR + 2 * kp2]) =
+                        (a0[e] & 0xffffu) | (a1[e] << 16);
+                    *reinterpret_cast<uint32_t*>(&sKt[(dg * 8 + 2 * e + 1) * L::KTSTR + 2 * kp2]) =
+                        (a0[e] >> 16) | (a1[e] & 0xffff0000u);
+                }
+            }
+        }
+        __syncthreads();
+    };
+    // S^T (keys x this wave's rows): lane holds keys 8*(i/4) + 4*hl + i%4 of query row `row`
+    auto scores = [&](const uint16_t* sA, const bf16x8 (&bq)[KS]) {
+        floatx16 acc = {};
+#pragma unroll
+        for (int s = 0; s < KS; ++s)
+            acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+                ld8(&sA[(l % 32) * L::KSTR + s * 16 + 8 * hl]), bq[s], acc, 0, 0, 0);
+        return acc;
+    };
+    auto key_of = [&](int i) { return 8 * (i / 4) + 4 * hl + (i % 4); };
+
+    // pass 1: log2-domain softmax statistics of each row
+    float m_run = -INFINITY, l_run = 0.0f;
+    for (int tile = 0; tile < ntiles; ++tile) {
+        load_tile(tile, false);
+        floatx16 sc = scores(sK, qb);
+        float mx = -INFINITY;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            sc[i] = (rv && row >= sThr[key_of(i)]) ? sc[i] * c2 : -INFINITY;
+            mx = fmaxf(mx, sc[i]);
+        }
+        mx = fmaxf(mx, __shfl_xor(mx, 32, kWave));
+        const float m_new = fmaxf(m_run, mx);
+        const float m_use = m_new == -INFINITY ? 0.0f : m_new;
+        float rs = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) rs += exp2f(sc[i] - m_use);
+        rs += __shfl_xor(rs, 32, kWave);
+        l_run = l_run * exp2f(m_run - m_use) + rs;
+        m_run = m_new;
+        __syncthreads();
+    }
+    const float lse = l_run > 0.0f ? m_run + log2f(l_run) : INFINITY;
+
+    // pass 2
+    floatx16 dq[DB];
+#pragma unroll
+    for (int d = 0; d < DB; ++d) dq[d] = floatx16{};
+    float* dkb = P.dk + ((int64_t)b * A.KVH + kvh) * A.S * DH;
+    float* dvb = P.dv + ((int64_t)b * A.KVH + kvh) * A.S * DH;
+    for (int tile = 0; tile < ntiles; ++tile) {
+        load_tile(tile, true);
+        floatx16 sc = scores(sK, qb);
+        const floatx16 dp = scores(sV, gb);
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const int kk = key_of(i);
+            const float p = (rv && row >= sThr[kk]) ? exp2f(sc[i] * c2 - lse) : 0.0f;
+            sc[i] = p * (dp[i] - Dr);                       // dS
+            sP[kk * L::PSTR + row] = f_to_bf16(p);
+            sDS[kk * L::PSTR + row] = f_to_bf16(sc[i]);
+        }
+        bf16x8 dsb[2];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            dsb[0][j] = (__bf16)sc[j];
+            dsb[1][j] = (__bf16)sc[8 + j];
+        }
+        // dQ^T += K^T dS^T: A = K^T rows (dims), k = keys in the order the score MFMA left them
+#pragma unroll
+        for (int st = 0; st < 2; ++st) {
+            const int kb = 16 * st + 4 * hl;
+#pragma unroll
+            for (int d = 0; d < DB; ++d) {
+                const uint16_t* kr = &sKt[(d * 32 + l % 32) * L::KTSTR];
+                const uint2 lo = *reinterpret_cast<const uint2*>(kr + kb);
+                const uint2 hi = *reinterpret_cast<const uint2*>(kr + kb + 8);
+                dq[d] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+                    __builtin_bit_cast(bf16x8, make_uint4(lo.x, lo.y, hi.x, hi.y)), dsb[st], dq[d],
+                    0, 0, 0);
+            }
+        }
+        __syncthreads();
+        // wave 0: dK = dS^T Q, wave 1: dV = P^T dO over the chunk's 64 rows; then scatter
+        {
+            const uint16_t* sA = w == 0 ? sDS : sP;
+            const uint16_t* sB = w == 0 ? sQt : sGt;
+            float* dst = w == 0 ? dkb : dvb;
+            const float mul = w == 0 ? A.scale : 1.0f;
+            // two 32-dim blocks at a time keep the accumulators to 32 registers
+#pragma unroll
+            for (int d0 = 0; d0 < DB; d0 += 2) {
+                floatx16 acc[2] = {floatx16{}, floatx16{}};
+#pragma unroll
+                for (int st = 0; st < kBR / 16; ++st) {
+                    const bf16x8 a = ld8(&sA[(l % 32) * L::PSTR + 16 * st + 8 * hl]);
+#pragma unroll
+                    for (int d = 0; d < 2; ++d)
+                        acc[d] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+                            a, ld8(&sB[((d0 + d) * 32 + l % 32) * L::QTSTR + 16 * st + 8 * hl]),
+                            acc[d], 0, 0, 0);
+                }
+#pragma unroll
+                for (int i = 0; i < 16; ++i) {
+                    const int kk = key_of(i);
+                    if (sThr[kk] < kNever) {
+                        float* o = dst + (int64_t)sPos[kk] * DH + (d0 * 32 + l % 32);
+                        unsafeAtomicAdd(o, acc[0][i] * mul);
+                        unsafeAtomicAdd(o + 32, acc[1][i] * mul);
+                    }
+                }
+            }
+        }
+        __syncthreads();
+    }
+    if (rv) {
+        uint16_t* dqp = reinterpret_cast<uint16_t*>(P.dq) + b * P.dq_sb + h * P.dq_sh +
+                        (r0 + row) * P.dq_ss;
+#pragma unroll
+        for (int d = 0; d < DB; ++d)
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                const int dim = d * 32 + 8 * g + 4 * hl;
+                uint2 u;
+                u.x = (uint32_t)f_to_bf16(dq[d][4 * g] * A.scale) |
+                      ((uint32_t)f_to_bf16(dq[d][4 * g + 1] * A.scale) << 16);
+                u.y = (uint32_t)f_to_bf16(dq[d][4 * g + 2] * A.scale) |
+                      ((uint32_t)f_to_bf16(dq[d][4 * g + 3] * A.scale) << 16);
+                *reinterpret_cast<uint2*>(dqp + dim) = u;
+            }
+    }
+}
+
 }  // namespace
 }  // namespace hga
 
@@ -301,6 +566,27 @@ extern "C" int hga_attend_prefill_bwd(
     const unsigned grid = (unsigned)(a.B * a.H * a.N);
     const size_t open_lds = sizeof(int) * (2 * (size_t)kBK + 2 * (size_t)(Kg > 0 ? Kg : 1));
     bool launched = false;
+    const uintptr_t al = (uintptr_t)q | (uintptr_t)k | (uintptr_t)v | (uintptr_t)out |
+                         (uintptr_t)dout | (uintptr_t)dq;
+    const bool aligned = al % 16 == 0 && ((q_sb | q_sh | q_ss | k_sb | k_sh | k_ss | v_sb | v_sh |
+                                           v_ss | o_sb | o_sh | o_ss | g_sb | g_sh | g_ss | dq_sb |
+                                           dq_sh | dq_ss) % 8) == 0;
+    if (cfg->dtype == HGA_DTYPE_BF16 && (D == 64 || D == 128) && aligned) {
+        const size_t lds = (D == 128 ? MfmaLds<128>::bytes : MfmaLds<64>::bytes) + open_lds;
+        HGA_REQUIRE(lds <= 163840, HGA_ERR_UNSUPPORTED,
+                    "hga_attend_prefill_bwd: %d opened groups too many", Kg);
+        static bool attr = false;
+        if (!attr) {
+            (void)hipFuncSetAttribute((const void*)attend_bwd_mfma_kernel<128>,
+                                      hipFuncAttributeMaxDynamicSharedMemorySize, 163840);
+            (void)hipFuncSetAttribute((const void*)attend_bwd_mfma_kernel<64>,
+                                      hipFuncAttributeMaxDynamicSharedMemorySize, 163840);
+            attr = true;
+        }
+        if (D == 128) attend_bwd_mfma_kernel<128><<<grid, kMT, lds, st>>>(p);
+        else attend_bwd_mfma_kernel<64><<<grid, kMT, lds, st>>>(p);
+        launched = true;
+    }
 #define HGA_BWD_VALU(DTV, DHV)                                                                   \
     if (!launched && cfg->dtype == DTV && D == DHV) {                                            \
         const size_t lds = sizeof(float) * valu_lds_floats<DHV>() + open_lds;                    \
