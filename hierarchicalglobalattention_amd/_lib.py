@@ -52,7 +52,8 @@ SIGNATURES = {
     "hga_attend_prefill_bwd_workspace": ([_CFG, _i32, ctypes.POINTER(ctypes.c_int64)], _i32),
     "hga_decode_widths": ([_CFG, _i32, _I32P, _I32P], _i32),
     "hga_route_decode": ([_CFG, _i32, _i32, _vp, _i64, _i64, _i64, _vp, _i64, _i64, _vp, _i64,
-                          _i64, _vp, _vp, _vp, _vp, _vp, _vp, _vp], ctypes.c_int),
+                          _i64, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _vp], ctypes.c_int),
+    "hga_route_decode_workspace": ([_CFG, _i32, _i32, ctypes.POINTER(ctypes.c_int64)], _i32),
     "hga_attend_decode": ([_CFG, _i32, _i32, _i64, _vp, _i64, _i64, _i64, _vp, _vp, _i64, _i64,
                            _i64, _i32, _vp, _vp, _i64, _i64, _i64, _vp, _vp, _i64, _i64, _i64,
                            _i32, _vp, _vp, _i32, _vp, _i64, _i64, _i64, _vp, _i64, _vp],

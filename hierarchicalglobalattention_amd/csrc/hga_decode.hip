@@ -4,11 +4,13 @@
 //
 // Router: one 256-thread workgroup per (batch, query head).  Decode scores are few (L rows x
 // pool), so they are computed directly with the canonical fp32 FMA chain (no MFMA pre-pass, no
-// certification needed).  Stage 1 walks the pool in segments that fit LDS: each row's running
-// top-Kc list and the pooled running list are merged with the next segment's scores by an exact
-// wave top-k (top-k of a union = top-k of the union of the parts' top-k, and the running list
-// holds lower ids than the segment, so ties still go to the lower id), so any pool length is
-// routed exactly as a single pass would.
+// certification needed).  Stage 1 is split over workgroups: route_decode_part_kernel (grid: pool
+// segments x (batch, head)) scores one segment of the pool for the block's rows and writes the
+// segment's exact top-Kc of every row and of the pooled (max over rows) scores into a workspace;
+// route_decode_kernel merges the segments' lists with one exact wave top-k per list (top-k of a
+// union = top-k of the union of the parts' top-k; segments hold ascending id ranges and their
+// lists are id-sorted, so candidate order is id order and ties still go to the lower id), then
+// forces the previous chunk and runs stage 2.  Any pool length routes exactly as a single pass.
 //
 // Attention: one 256-thread workgroup per (batch, query head); the key sequence [first window |
 // last window | opened groups | active chunk] is split over the 4 waves, lanes score one key
@@ -26,7 +28,7 @@ constexpr int kDT = 256;            // threads
 constexpr int kDW = kDT / kWave;     // waves
 constexpr int kMaxL = 64;
 constexpr int kDecJ = 32;            // wave selections over <= 2048 candidates
-constexpr int kDecSegJ = 32;         // stage-1 segment: <= 64 * kDecSegJ positions
+constexpr int kDecSegJ = 32;         // stage-1 segment: <= 64 * kDecSegJ chunks
 
 struct DecRouteArgs {
     const void* q;
@@ -37,41 +39,13 @@ struct DecRouteArgs {
     int64_t gk_sb, gk_sh;
     int32_t *mid, *mid_thr, *n_mid, *open_grp, *open_thr, *n_open;
     int B, H, KVH, L, n_closed, M, kf, kl, Kc, Kg, Kgr, SPD;
-    int cap;       // stage-1 positions per segment pass (running list + segment)
+    int seg, nseg;  // stage-1 pool segment length and count (one scoring workgroup each)
+    int SPW;        // row stride of the stage-1 scores (the pool length)
+    float* ws;      // workspace: stage-1 scores [B*H][L][SPW]
+    float* wv;      // segments' pooled top-Kc values [B*H][nseg][Kc] (id-sorted, -inf padded)
+    int32_t* wi;    // and their chunk offsets in the pool (-1 padded)
     float scale;
 };
-
-template <int DT, int DH>
-__device__ __forceinline__ float cdot(const typename Elem<DT>::T* q, const typename Elem<DT>::T* k,
-                                      float scale) {
-    // canonical chain: sequential fp32 FMA over d, then * scale, -0 -> +0
-    float acc = 0.0f;
-    if constexpr (DT == HGA_DTYPE_BF16) {
-#pragma unroll 4
-        for (int i = 0; i < DH / 8; ++i) {
-            const uint4 qq = *reinterpret_cast<const uint4*>(q + 8 * i);
-            const uint4 kk = *reinterpret_cast<const uint4*>(k + 8 * i);
-            const uint32_t qw[4] = {qq.x, qq.y, qq.z, qq.w}, kw[4] = {kk.x, kk.y, kk.z, kk.w};
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                acc = fmaf(__uint_as_float(qw[e] << 16), __uint_as_float(kw[e] << 16), acc);
-                acc = fmaf(__uint_as_float(qw[e] & 0xffff0000u), __uint_as_float(kw[e] & 0xffff0000u), acc);
-            }
-        }
-    } else {
-#pragma unroll 4
-        for (int i = 0; i < DH / 4; ++i) {
-            const float4 qq = *reinterpret_cast<const float4*>(q + 4 * i);
-            const float4 kk = *reinterpret_cast<const float4*>(k + 4 * i);
-            acc = fmaf(qq.x, kk.x, acc);
-            acc = fmaf(qq.y, kk.y, acc);
-            acc = fmaf(qq.z, kk.z, acc);
-            acc = fmaf(qq.w, kk.w, acc);
-        }
-    }
-    const float s = acc * scale;
-    return s == 0.0f ? 0.0f : s;
-}
 
 // Wave-wide exact top-k of LDS values vals[0..n) (-inf excluded); returns member bits.
 template <int J>
@@ -88,22 +62,62 @@ __device__ __forceinline__ uint32_t topk_lds(const float* vals, int n, int k) {
     return exact_topk<J>(kv, v, k);
 }
 
-// Running exact top-k: vals[0..off) / ids[0..off) is the list so far (ascending ids), vals[off..n)
-// the next segment's values (ids id0 + i - off, all above the list's).  Leaves the top-k of both
-// (ties -> lower id) in vals[0..k) / ids[0..k) in ascending id order, -inf / -1 past its length.
-// Every value is in registers before the first write back.
+// Canonical scores (sequential fp32 FMA chain over d, then * scale, -0 -> +0) of one key row
+// against the L query rows in LDS; score r goes to out[r * stride] and the max over the rows is
+// returned.  The key row stays in registers and every lane of a wave reads the same query
+// element at a time (LDS broadcast), so a key costs one global read.
+template <int DT, int DH>
+__device__ __forceinline__ float score_key_rows(const typename Elem<DT>::T* sQ, int L,
+                                                const typename Elem<DT>::T* kg, float* out,
+                                                int64_t stride, float scale) {
+    typedef typename Elem<DT>::T T;
+    constexpr int NV = DH * (int)sizeof(T) / 16;
+    uint4 kr[NV];
+#pragma unroll
+    for (int v = 0; v < NV; ++v) kr[v] = reinterpret_cast<const uint4*>(kg)[v];
+    float mx = -INFINITY;
+    for (int r = 0; r < L; ++r) {
+        const uint4* qv = reinterpret_cast<const uint4*>(sQ + r * DH);
+        float acc = 0.0f;
+#pragma unroll
+        for (int v = 0; v < NV; ++v) {
+            const uint4 qq = qv[v], kk = kr[v];
+            if constexpr (DT == HGA_DTYPE_BF16) {
+                const uint32_t qw[4] = {qq.x, qq.y, qq.z, qq.w}, kw[4] = {kk.x, kk.y, kk.z, kk.w};
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    acc = fmaf(__uint_as_float(qw[e] << 16), __uint_as_float(kw[e] << 16), acc);
+                    acc = fmaf(__uint_as_float(qw[e] & 0xffff0000u),
+                               __uint_as_float(kw[e] & 0xffff0000u), acc);
+                }
+            } else {
+                acc = fmaf(__uint_as_float(qq.x), __uint_as_float(kk.x), acc);
+                acc = fmaf(__uint_as_float(qq.y), __uint_as_float(kk.y), acc);
+                acc = fmaf(__uint_as_float(qq.z), __uint_as_float(kk.z), acc);
+                acc = fmaf(__uint_as_float(qq.w), __uint_as_float(kk.w), acc);
+            }
+        }
+        float sc = acc * scale;
+        sc = sc == 0.0f ? 0.0f : sc;
+        out[r * stride] = sc;
+        mx = fmaxf(mx, sc);
+    }
+    return mx;
+}
+
+// Exact top-k (ties -> lower position) of LDS values vals[0..n) (-inf excluded), written in
+// position order to ov/oi (ids id0 + position), -inf / -1 past its length.
 template <int J>
-__device__ __forceinline__ void merge_topk(float* vals, int* ids, int n, int off, int k, int id0) {
+__device__ __forceinline__ void topk_to(const float* vals, int n, int k, int id0, float* ov,
+                                        int32_t* oi) {
     const int l = lane_id();
     float v[J];
     uint32_t kv[J];
-    int id[J];
 #pragma unroll
     for (int j = 0; j < J; ++j) {
         const int i = l + 64 * j;
         v[j] = i < n ? vals[i] : -INFINITY;
         kv[j] = v[j] == -INFINITY ? 0u : okey(v[j]);
-        id[j] = i < off ? ids[i] : id0 + i - off;
     }
     const uint32_t mem = exact_topk<J>(kv, v, k);
     int base = 0;
@@ -112,14 +126,125 @@ __device__ __forceinline__ void merge_topk(float* vals, int* ids, int n, int off
         const bool m = (mem >> j) & 1u;
         const uint64_t bal = __ballot(m);
         if (m) {
-            vals[base + lanes_below(bal)] = v[j];
-            ids[base + lanes_below(bal)] = id[j];
+            ov[base + lanes_below(bal)] = v[j];
+            oi[base + lanes_below(bal)] = id0 + l + 64 * j;
         }
         base += __popcll(bal);
     }
     for (int i = base + l; i < k; i += kWave) {
-        vals[i] = -INFINITY;
-        ids[i] = -1;
+        ov[i] = -INFINITY;
+        oi[i] = -1;
+    }
+}
+
+// Exact top-k of the candidate lists of nseg segments (k entries each, id-sorted, -inf padded,
+// consecutive): position order is id order, so ties go to the lower id.  Writes the values and
+// ids in id order to LDS, -inf / -1 past its length.
+template <int J>
+__device__ __forceinline__ void merge_segments(const float* cv, const int32_t* ci, int n, int k,
+                                               float* dv, int* di) {
+    const int l = lane_id();
+    float v[J];
+    uint32_t kv[J];
+    int id[J];
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+        const int i = l + 64 * j;
+        v[j] = i < n ? cv[i] : -INFINITY;
+        id[j] = i < n ? ci[i] : -1;
+        kv[j] = v[j] == -INFINITY ? 0u : okey(v[j]);
+    }
+    const uint32_t mem = exact_topk<J>(kv, v, k);
+    int base = 0;
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+        const bool m = (mem >> j) & 1u;
+        const uint64_t bal = __ballot(m);
+        if (m) {
+            di[base + lanes_below(bal)] = id[j];
+            dv[base + lanes_below(bal)] = v[j];
+        }
+        base += __popcll(bal);
+    }
+    for (int i = base + l; i < k; i += kWave) {
+        di[i] = -1;
+        dv[i] = -INFINITY;
+    }
+}
+
+// Whether row `row` (values vals[0..n), candidate ids 0..n-1) ranks each of the wave's open
+// candidates (lanes in `open`, lane p holding its value sp and id cp) among its top k: fewer
+// than k candidates larger, or equal with a lower id -- membership in the row's exact top-k
+// under the canonical ranking, without selecting it.  Returns the lanes that are members.
+__device__ __forceinline__ uint64_t ranked_in(const float* vals, int n, uint64_t open, float sp,
+                                              int cp, int k) {
+    constexpr int U = 4;                      // 64-candidate blocks loaded together
+    const int l = lane_id();
+    int cnt = 0;
+    for (int i0 = 0; i0 < n && open; i0 += U * kWave) {
+        float v[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int i = i0 + u * kWave + l;
+            v[u] = i < n ? vals[i] : -INFINITY;   // -inf never ranks above a score
+        }
+        uint64_t m = open;
+        while (m) {
+            const int p = __builtin_ctzll(m);
+            m &= m - 1ull;
+            const float s = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(sp), p));
+            const int c = __builtin_amdgcn_readlane(cp, p);
+            int add = 0;
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const int i = i0 + u * kWave + l;
+                add += (int)__popcll(__ballot(v[u] > s || (v[u] == s && i < c)));
+            }
+            if (l == p) cnt += add;
+        }
+        open &= __ballot(cnt < k);
+    }
+    return open;
+}
+
+// Stage-1 scoring of one pool segment: canonical scores of the block's L rows (to the
+// workspace, row stride SPW), their max over the rows, and the segment's pooled top-Kc
+// (chunk_router.py:219-231).
+template <int DT, int DH>
+__global__ __launch_bounds__(kDT) void route_decode_part_kernel(DecRouteArgs A) {
+    typedef typename Elem<DT>::T T;
+    extern __shared__ __align__(16) unsigned char smem_raw[];
+    const int L = A.L, K = A.Kc;
+    T* sQ = reinterpret_cast<T*>(smem_raw);                     // [L][DH]
+    float* sPool = reinterpret_cast<float*>(sQ + L * DH);       // [seg]
+    const int sg = blockIdx.x, bh = blockIdx.y, b = bh / A.H, h = bh % A.H;
+    const int kvh = h / (A.H / A.KVH);
+    int f_hi, l_lo;
+    windows(A.n_closed, A.kf, A.kl, &f_hi, &l_lo);
+    const int nmid = l_lo > f_hi ? l_lo - f_hi : 0;
+    const int s0 = sg * A.seg, sl = min(A.seg, nmid - s0);   // s0 < nmid (host grid)
+    {
+        constexpr int VE = 16 / (int)sizeof(T);
+        const T* qg = reinterpret_cast<const T*>(A.q) + b * A.q_sb + h * A.q_sh;
+        for (int idx = threadIdx.x; idx < L * (DH / VE); idx += kDT) {
+            const int r = idx / (DH / VE), d = (idx % (DH / VE)) * VE;
+            *reinterpret_cast<uint4*>(sQ + r * DH + d) =
+                *reinterpret_cast<const uint4*>(qg + (int64_t)r * A.q_ss + d);
+        }
+    }
+    __syncthreads();
+    const T* ckb = reinterpret_cast<const T*>(A.ck) + b * A.ck_sb + kvh * A.ck_sh +
+                   (int64_t)(f_hi + s0) * DH;
+    float* srow = A.ws + (int64_t)bh * L * A.SPW + s0;
+    for (int i = threadIdx.x; i < sl; i += kDT)                // pooled over all rows (:227)
+        sPool[i] = score_key_rows<DT, DH>(sQ, L, ckb + (int64_t)i * DH, srow + i, A.SPW, A.scale);
+    __syncthreads();
+    if (threadIdx.x < kWave) {
+        const int64_t o = ((int64_t)bh * A.nseg + sg) * K;
+        dispatch_j<kDecSegJ>(sl, [&](auto jt) {
+            constexpr int J = decltype(jt)::value;
+            topk_to<J>(sPool, sl, K, s0, A.wv + o, A.wi + o);
+        });
     }
 }
 
@@ -129,14 +254,14 @@ __global__ __launch_bounds__(kDT) void route_decode_kernel(DecRouteArgs A) {
     extern __shared__ __align__(16) unsigned char smem_raw[];
     const int SPD = A.SPD, M = A.M, L = A.L;
     T* sQ = reinterpret_cast<T*>(smem_raw);                     // [L][DH]
-    float* sS = reinterpret_cast<float*>(sQ + L * DH);          // [L][SPD]
+    float* sS = reinterpret_cast<float*>(sQ + L * DH);          // [L][SPD] group scores
     float* sPool = sS + L * SPD;                                // [SPD]
-    int* sFirst = reinterpret_cast<int*>(sPool + SPD);          // [SPD]
+    int* sFirst = reinterpret_cast<int*>(sPool + SPD);          // [SPD] first requesting row
     int* sSel = sFirst + SPD;                                   // [64] sorted chunk ids
     int* sThr = sSel + 64;                                      // [64] -1 = never visible
     int* sScal = sThr + 64;                                     // [8]
-    int* sRI = sScal + 8;                                       // [L][Kc] rows' running lists
-    int* sPI = sRI + L * (A.Kc > 0 ? A.Kc : 1);                 // [Kc] pooled running list
+    int* sOp = sScal + 8;                                       // [256] opened candidates
+    int* sPI = sOp + 256;                                       // [Kc] pooled selection ids
 
     const int bh = blockIdx.x, b = bh / A.H, h = bh % A.H, kvh = h / (A.H / A.KVH);
     const int w = threadIdx.x / kWave, l = lane_id();
@@ -155,6 +280,7 @@ __global__ __launch_bounds__(kDT) void route_decode_kernel(DecRouteArgs A) {
         return;
     }
     const float scale = A.scale;
+    const int K = A.Kc;
     {
         constexpr int VE = 16 / (int)sizeof(T);
         const T* qg = reinterpret_cast<const T*>(A.q) + b * A.q_sb + h * A.q_sh;
@@ -164,34 +290,15 @@ __global__ __launch_bounds__(kDT) void route_decode_kernel(DecRouteArgs A) {
                 *reinterpret_cast<const uint4*>(qg + (int64_t)r * A.q_ss + d);
         }
     }
-    __syncthreads();
-    // ---- stage 1: pool chunks, segment by segment (:219-241) ---------------------------------
-    const int K = A.Kc;
-    const T* ckb = reinterpret_cast<const T*>(A.ck) + b * A.ck_sb + kvh * A.ck_sh;
-    for (int s0 = 0, off = 0; s0 < nmid; off = K) {
-        const int sl = min(A.cap - off, nmid - s0);
-        for (int idx = threadIdx.x; idx < L * sl; idx += kDT) {
-            const int r = idx / sl, i = idx % sl;
-            sS[r * SPD + off + i] = cdot<DT, DH>(sQ + r * DH, ckb + (int64_t)(f_hi + s0 + i) * DH, scale);
-        }
-        __syncthreads();
-        for (int i = threadIdx.x; i < sl; i += kDT) {     // pooled over all rows (:227)
-            float m = -INFINITY;
-            for (int r = 0; r < L; ++r) m = fmaxf(m, sS[r * SPD + off + i]);
-            sPool[off + i] = m;
-        }
-        __syncthreads();
-        // per-row requests (:230) and the pooled selection (:231), as running lists (row L = pool)
-        dispatch_j<kDecSegJ>(off + sl, [&](auto jt) {
+    // ---- stage 1: pooled selection = top-Kc of the segments' pooled lists (:227, :231) ------
+    if (w == 0) {
+        const int64_t o = (int64_t)bh * A.nseg * K;
+        dispatch_j<kDecJ>(A.nseg * K, [&](auto jt) {
             constexpr int J = decltype(jt)::value;
-            for (int r = w; r <= L; r += kDW) {
-                if (r < L) merge_topk<J>(sS + r * SPD, sRI + r * K, off + sl, off, K, s0);
-                else merge_topk<J>(sPool, sPI, off + sl, off, K, s0);
-            }
+            merge_segments<J>(A.wv + o, A.wi + o, A.nseg * K, K, sPool, sPI);
         });
-        __syncthreads();
-        s0 += sl;
     }
+    __syncthreads();
     if (w == 0) {
         // forced previous chunk (:232-241); K <= 64, one list entry per lane
         const int prev = A.n_closed - 1;
@@ -220,23 +327,21 @@ __global__ __launch_bounds__(kDT) void route_decode_kernel(DecRouteArgs A) {
             sScal[0] = ns;
             sScal[1] = forced ? nkeep : (fl >= 0 ? __popcll(bal & ((1ull << fl) - 1ull)) : -1);
         }
-        if (l < ns) sFirst[l] = kNoRow;                       // ns <= Kc < SPD
+        // one row: its own top-Kc is the pooled selection, so row 0 requests every selected chunk
+        if (l < ns) sFirst[l] = L == 1 ? 0 : kNoRow;          // ns <= Kc < SPD
     }
     __syncthreads();
-    {
-        // first row whose own top-Kc holds each selected chunk (:230, :243-250)
+    if (L > 1) {
+        // first row whose own top-Kc holds each selected chunk (:230, :243-250), by rank
         const int ns = sScal[0];
-        for (int idx = threadIdx.x; idx < L * K; idx += kDT) {
-            const int c = sRI[idx];
-            if (c < 0) continue;
-            const int g = f_hi + c;
-            int lo = 0, hi = ns;
-            while (lo < hi) {
-                const int mid = (lo + hi) >> 1;
-                if (sSel[mid] < g) lo = mid + 1;
-                else hi = mid;
-            }
-            if (lo < ns && sSel[lo] == g) atomicMin(&sFirst[lo], idx / K);
+        const int c = l < ns ? sSel[l] - f_hi : 0;
+        for (int r = w; r < L; r += kDW) {
+            const float* row = A.ws + ((int64_t)bh * L + r) * A.SPW;
+            const uint64_t open = __ballot(l < ns && sFirst[l] > r);
+            if (!open) continue;
+            const float sp = l < ns ? row[c] : 0.0f;
+            const uint64_t req = ranked_in(row, nmid, open, sp, c, K);
+            if ((req >> l) & 1ull) atomicMin(&sFirst[l], r);
         }
     }
     __syncthreads();
@@ -263,49 +368,65 @@ __global__ __launch_bounds__(kDT) void route_decode_kernel(DecRouteArgs A) {
     }
     // ---- groups of the selected chunks (:256-276) --------------------------------------------
     const T* gkb = reinterpret_cast<const T*>(A.gk) + b * A.gk_sb + kvh * A.gk_sh;
-    for (int idx = threadIdx.x; idx < L * T2; idx += kDT) {
-        const int r = idx / T2, i = idx % T2;
-        sS[r * SPD + i] = cdot<DT, DH>(sQ + r * DH, gkb + ((int64_t)sSel[i / M] * M + i % M) * DH, scale);
-    }
-    for (int i = threadIdx.x; i < T2; i += kDT) sFirst[i] = kNoRow;
-    __syncthreads();
-    for (int i = threadIdx.x; i < T2; i += kDT) {
-        float m = -INFINITY;
-        for (int r = 0; r < L; ++r) m = fmaxf(m, sS[r * SPD + i]);
-        sPool[i] = m;
-    }
-    __syncthreads();
-    dispatch_j<kDecJ>(T2, [&](auto jt) {
-        constexpr int J = decltype(jt)::value;
-        for (int r = w; r < L; r += kDW) {
-            const uint32_t mem = topk_lds<J>(sS + r * SPD, T2, A.Kgr);
-#pragma unroll
-            for (int j = 0; j < J; ++j)
-                if ((mem >> j) & 1u) atomicMin(&sFirst[l + 64 * j], r);
-        }
-    });
+    for (int i = threadIdx.x; i < T2; i += kDT)               // pooled over all rows (:264)
+        sPool[i] = score_key_rows<DT, DH>(sQ, L, gkb + ((int64_t)sSel[i / M] * M + i % M) * DH,
+                                          sS + i, SPD, scale);
     __syncthreads();
     if (w == 0) {
+        // opened = pooled top-Kg (:265), ascending candidate order
         dispatch_j<kDecJ>(T2, [&](auto jt) {
             constexpr int J = decltype(jt)::value;
             const uint32_t op = topk_lds<J>(sPool, T2, A.Kg);
             int base = 0;
 #pragma unroll
             for (int j = 0; j < J; ++j) {
-                const int i = l + 64 * j;
-                int thr = -1;
-                if (((op >> j) & 1u) && sFirst[i] < kNoRow && sThr[i / M] >= 0)
-                    thr = sFirst[i] > sThr[i / M] ? sFirst[i] : sThr[i / M];
-                const uint64_t bal = __ballot(thr >= 0);
-                if (thr >= 0 && base + lanes_below(bal) < Kgw) {
-                    o_og[base + lanes_below(bal)] = sSel[i / M] * M + i % M;
-                    o_ot[base + lanes_below(bal)] = thr;
-                }
+                const bool m = (op >> j) & 1u;
+                const uint64_t bal = __ballot(m);
+                if (m) sOp[base + lanes_below(bal)] = l + 64 * j;
                 base += __popcll(bal);
             }
-            for (int i = base + l; i < Kgw; i += kWave) o_og[i] = o_ot[i] = -1;
-            if (l == 0) A.n_open[bh] = base;
+            if (l == 0) sScal[2] = base;
         });
+    }
+    __syncthreads();
+    const int nop = sScal[2];
+    for (int i = threadIdx.x; i < nop; i += kDT) sFirst[i] = kNoRow;
+    __syncthreads();
+    // each row requests its own top-Kgr groups (:266); first requesting row by rank
+    for (int r = w; r < L; r += kDW) {
+        const float* row = sS + r * SPD;
+        for (int o0 = 0; o0 < nop; o0 += kWave) {
+            const int o = o0 + l;
+            const uint64_t open = __ballot(o < nop && sFirst[o] > r);
+            if (!open) continue;
+            const int c = o < nop ? sOp[o] : 0;
+            const float sp = o < nop ? row[c] : 0.0f;
+            const uint64_t req = ranked_in(row, T2, open, sp, c, A.Kgr);
+            if ((req >> l) & 1ull) atomicMin(&sFirst[o], r);
+        }
+    }
+    __syncthreads();
+    if (w == 0) {
+        // visible from max(first request, parent threshold) (:273-276)
+        int base = 0;
+        for (int o0 = 0; o0 < nop; o0 += kWave) {
+            const int o = o0 + l;
+            int thr = -1, grp = -1;
+            if (o < nop) {
+                const int i = sOp[o];
+                grp = sSel[i / M] * M + i % M;
+                if (sFirst[o] < kNoRow && sThr[i / M] >= 0)
+                    thr = sFirst[o] > sThr[i / M] ? sFirst[o] : sThr[i / M];
+            }
+            const uint64_t bal = __ballot(thr >= 0);
+            if (thr >= 0 && base + lanes_below(bal) < Kgw) {
+                o_og[base + lanes_below(bal)] = grp;
+                o_ot[base + lanes_below(bal)] = thr;
+            }
+            base += __popcll(bal);
+        }
+        for (int i = base + l; i < Kgw; i += kWave) o_og[i] = o_ot[i] = -1;
+        if (l == 0) A.n_open[bh] = base;
     }
 }
 
@@ -984,12 +1105,61 @@ extern "C" int32_t hga_decode_widths(const hga_config* cfg, int32_t n_closed, in
     return HGA_OK;
 }
 
+namespace hga {
+namespace {
+// Stage-1 segmentation of a decode block's pool: segment length, count and the scoring kernel's
+// LDS bytes.  Segments of 128 (L <= 4) or 256 chunks give one workgroup each enough work; longer
+// segments keep the merge's candidates (nseg * Kc) within one wave selection.
+struct DecSeg {
+    int seg, nseg, spd;
+    size_t lds;
+};
+int dec_segments(const hga_config* cfg, int L, int nmid, int Kc, DecSeg* o) {
+    const size_t esz = cfg->dtype == HGA_DTYPE_BF16 ? 2 : 4;
+    const int64_t room = ((int64_t)163840 - 16 - (int64_t)(esz * L * cfg->head_dim)) / 4;
+    const int cap = 64 * kDecJ / (Kc > 0 ? Kc : 1);
+    int seg = L <= 4 ? 128 : 256;
+    if (nmid > (int64_t)seg * cap) seg = (nmid + cap - 1) / cap;
+    HGA_REQUIRE(seg <= 64 * kDecSegJ && seg <= room, HGA_ERR_UNSUPPORTED,
+                "hga_route_decode: pool of %d chunks too long for L=%d x head_dim %d", nmid, L,
+                cfg->head_dim);
+    o->seg = seg;
+    o->nseg = nmid > 0 ? (nmid + seg - 1) / seg : 0;
+    o->spd = nmid < seg ? nmid : seg;
+    o->lds = esz * (size_t)L * cfg->head_dim + sizeof(float) * (size_t)o->spd + 16;
+    return HGA_OK;
+}
+}  // namespace
+}  // namespace hga
+
+extern "C" int hga_route_decode_workspace(const hga_config* cfg, int32_t L, int32_t n_closed,
+                                          int64_t* bytes) {
+    using namespace hga;
+    int rc = check_config(cfg);
+    if (rc) return rc;
+    HGA_REQUIRE(bytes && L >= 1 && L <= kMaxL && n_closed >= 0, HGA_ERR_ARG,
+                "hga_route_decode_workspace: bad L/n_closed/bytes");
+    int f_hi, l_lo, Kc, Kg;
+    windows(n_closed, cfg->keep_first, cfg->keep_last, &f_hi, &l_lo);
+    const int nmid = l_lo > f_hi ? l_lo - f_hi : 0;
+    hga_decode_widths(cfg, n_closed, &Kc, &Kg);
+    DecSeg sg{};
+    if (Kc > 0) {
+        rc = dec_segments(cfg, L, nmid, Kc, &sg);
+        if (rc) return rc;
+    }
+    // stage-1 scores of every row, then per (b, h, segment) Kc pooled values and chunk offsets
+    *bytes = Kc > 0 ? (int64_t)cfg->batch * cfg->heads * ((int64_t)L * nmid * 4 + sg.nseg * Kc * 8)
+                    : 0;
+    return HGA_OK;
+}
+
 extern "C" int hga_route_decode(const hga_config* cfg, int32_t L, int32_t n_closed, const void* q,
                                 int64_t q_sb, int64_t q_sh, int64_t q_ss, const void* chunk_k,
                                 int64_t ck_sb, int64_t ck_sh, const void* group_k, int64_t gk_sb,
                                 int64_t gk_sh, int32_t* mid, int32_t* mid_thr, int32_t* n_mid,
                                 int32_t* open_grp, int32_t* open_thr, int32_t* n_open,
-                                void* stream) {
+                                void* workspace, int64_t workspace_bytes, void* stream) {
     using namespace hga;
     int rc = check_config(cfg);
     if (rc) return rc;
@@ -1015,20 +1185,33 @@ extern "C" int hga_route_decode(const hga_config* cfg, int32_t L, int32_t n_clos
     const int T2max = a.Kc * a.M;
     HGA_REQUIRE(T2max <= kDecJ * 64, HGA_ERR_UNSUPPORTED,
                 "hga_route_decode: %d candidate groups exceed %d", T2max, kDecJ * 64);
-    // LDS: sQ [L][D] | sS [L][SPD] | sPool, sFirst [SPD] | sSel, sThr [64] | sScal [8] |
-    // sRI [L][Kc] | sPI [Kc]; the stage-1 segment pass gets what the SPD columns allow
     const int D = cfg->head_dim;
     const size_t esz = cfg->dtype == HGA_DTYPE_BF16 ? 2 : 4;
+    DecSeg sg{};
+    if (a.Kc > 0) {
+        rc = dec_segments(cfg, L, nmid, a.Kc, &sg);
+        if (rc) return rc;
+        int64_t need = 0;
+        hga_route_decode_workspace(cfg, L, n_closed, &need);
+        HGA_REQUIRE(workspace && workspace_bytes >= need && (uintptr_t)workspace % 4 == 0,
+                    HGA_ERR_ARG, "hga_route_decode: workspace of %lld bytes required (got %lld)",
+                    (long long)need, (long long)workspace_bytes);
+        a.seg = sg.seg;
+        a.nseg = sg.nseg;
+        a.SPW = nmid;
+        a.ws = (float*)workspace;
+        a.wv = a.ws + (int64_t)a.B * a.H * L * nmid;
+        a.wi = (int32_t*)(a.wv + (int64_t)a.B * a.H * sg.nseg * a.Kc);
+    }
+    // merge kernel LDS: sQ [L][D] | sS [L][SPD] | sPool, sFirst [SPD] | sSel, sThr [64] |
+    // sScal [8] | sOp [256] | sPI [Kc]; SPD covers stage 2's candidate groups and the lists
     const int Kcw = a.Kc > 0 ? a.Kc : 1;
-    const size_t fixed = esz * (size_t)L * D + sizeof(int) * (136 + (size_t)(L + 1) * Kcw) + 16;
-    const int64_t spd_max = ((int64_t)163840 - (int64_t)fixed) / (int64_t)(sizeof(float) * (L + 2));
-    a.cap = (int)(spd_max - 2 < 64 * kDecSegJ ? spd_max - 2 : 64 * kDecSegJ);
-    HGA_REQUIRE(a.cap >= a.Kc + 64 && T2max + 2 <= spd_max, HGA_ERR_UNSUPPORTED,
-                "hga_route_decode: L=%d x head_dim %d x %d groups leave no LDS for the pool", L, D,
-                T2max);
-    const int W = (nmid < a.cap ? nmid : a.cap) > T2max ? (nmid < a.cap ? nmid : a.cap) : T2max;
-    a.SPD = (W + 1) | 1;
-    const size_t lds = fixed + sizeof(float) * (size_t)(L + 2) * a.SPD;
+    HGA_REQUIRE(a.Kg <= 256, HGA_ERR_UNSUPPORTED, "hga_route_decode: top-k groups %d > 256", a.Kg);
+    a.SPD = ((T2max > Kcw ? T2max : Kcw) + 1) | 1;
+    const size_t lds = esz * (size_t)L * D + sizeof(int) * (136 + 256 + (size_t)Kcw) + 16 +
+                       sizeof(float) * (size_t)(L + 2) * a.SPD;
+    HGA_REQUIRE(lds <= 163840, HGA_ERR_UNSUPPORTED,
+                "hga_route_decode: L=%d x head_dim %d x %d groups leave no LDS", L, D, T2max);
     if (a.Kc > 0) {
         const int64_t ve = esz == 2 ? 8 : 4;
         HGA_REQUIRE(chunk_k && group_k, HGA_ERR_ARG, "hga_route_decode: NULL summaries");
@@ -1042,9 +1225,17 @@ extern "C" int hga_route_decode(const hga_config* cfg, int32_t L, int32_t n_clos
     if (cfg->dtype == DTV && D == DHV) {                                                        \
         static bool attr = false;                                                               \
         if (!attr) {                                                                            \
-            (void)hipFuncSetAttribute((const void*)route_decode_kernel<DTV, DHV>,                   \
-                                hipFuncAttributeMaxDynamicSharedMemorySize, 163840);            \
+            (void)hipFuncSetAttribute((const void*)route_decode_kernel<DTV, DHV>,               \
+                                      hipFuncAttributeMaxDynamicSharedMemorySize, 163840);      \
+            (void)hipFuncSetAttribute((const void*)route_decode_part_kernel<DTV, DHV>,          \
+                                      hipFuncAttributeMaxDynamicSharedMemorySize, 163840);      \
             attr = true;                                                                        \
+        }                                                                                       \
+        if (a.Kc > 0) {                                                                         \
+            route_decode_part_kernel<DTV, DHV><<<dim3((unsigned)sg.nseg, grid), kDT, sg.lds,   \
+                                                 st>>>(a);                                      \
+            rc = launch_status("hga_route_decode");                                             \
+            if (rc) return rc;                                                                  \
         }                                                                                       \
         route_decode_kernel<DTV, DHV><<<grid, kDT, lds, st>>>(a);                               \
         return launch_status("hga_route_decode");                                               \

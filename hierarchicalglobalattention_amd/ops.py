@@ -291,11 +291,15 @@ def route_decode(cfg: HgaConfig, q: torch.Tensor, chunk_k: torch.Tensor, group_k
     if chunk_k.stride(-1) != 1 or chunk_k.stride(2) != D or group_k.stride(3) != D or \
             group_k.stride(2) != group_k.shape[3] * D:
         raise ValueError("store tables must be chunk-contiguous with a contiguous head dim")
+    nb = ctypes.c_int64()
+    check(lib().hga_route_decode_workspace(ctypes.byref(cfg), L, n_closed, ctypes.byref(nb)),
+          "hga_route_decode_workspace")
+    ws = torch.empty(max(nb.value, 16), dtype=torch.uint8, device=dev)
     check(lib().hga_route_decode(
         ctypes.byref(cfg), L, n_closed, _p(q), *_s4(q), _p(chunk_k), chunk_k.stride(0),
         chunk_k.stride(1), _p(group_k), group_k.stride(0), group_k.stride(1), _p(r["mid"]),
         _p(r["mid_thr"]), _p(r["n_mid"]), _p(r["open_grp"]), _p(r["open_thr"]), _p(r["n_open"]),
-        _stream()), "hga_route_decode")
+        _p(ws), nb.value, _stream()), "hga_route_decode")
     r["Kc"], r["Kg"] = Kc, Kg
     return r
 

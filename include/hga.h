@@ -190,12 +190,20 @@ int32_t hga_decode_widths(const hga_config* cfg, int32_t n_closed, int32_t* Kc, 
  * Outputs (int32, ascending ids, -1 padded, widths from hga_decode_widths, >= 1):
  *   mid, mid_thr [B, H, Kc]  routed chunks visible to some row; n_mid [B, H]
  *   open_grp, open_thr [B, H, Kg]  opened groups (chunk*M + group) visible to some row; n_open
+ * workspace: hga_route_decode_workspace bytes (the pool's segments' candidate lists), 4-byte
+ * aligned, used only by the call's kernels.  Any pool length; L <= 64, topk_chunks <= 64.
  */
 int hga_route_decode(const hga_config* cfg, int32_t L, int32_t n_closed, const void* q,
                      int64_t q_sb, int64_t q_sh, int64_t q_ss, const void* chunk_k,
                      int64_t ck_sb, int64_t ck_sh, const void* group_k, int64_t gk_sb,
                      int64_t gk_sh, int32_t* mid, int32_t* mid_thr, int32_t* n_mid,
-                     int32_t* open_grp, int32_t* open_thr, int32_t* n_open, void* stream);
+                     int32_t* open_grp, int32_t* open_thr, int32_t* n_open, void* workspace,
+                     int64_t workspace_bytes, void* stream);
+
+/* Device scratch bytes hga_route_decode needs for an L-row block after n_closed chunks.  No
+ * counterpart in the reference, whose router keeps its scores in torch temporaries. */
+int32_t hga_route_decode_workspace(const hga_config* cfg, int32_t L, int32_t n_closed,
+                                   int64_t* bytes);
 
 /*
  * Decode attention (decode_block's assembly, chunk_router.py:333-401, attended flat as in
