@@ -850,6 +850,161 @@ __global__ __launch_bounds__(kDT) void attend_decode_split_kernel(DecAttnArgs A,
 }
 
 // One workgroup per (b, head, row): out = sum_s e^(m_s - M) acc_s / sum_s e^(m_s - M) l_s.
+// Multi-row blocks, bf16 head_dim 64/128: the split's keys are located once, staged 32 at a time
+// in LDS (K row-major, V transposed) and scored for all the block's rows at once with
+// v_mfma_f32_32x32x16_bf16 -- S^T = K Q^T leaves one query row per lane (wave w: rows
+// 32w..32w+31), O^T = V^T P^T -- with the online softmax per row in base 2.  Writes the same
+// per-split partials as attend_decode_split_kernel (natural-log maximum, sum, accumulator).
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float floatx16_t __attribute__((ext_vector_type(16)));
+constexpr int kDMT = 128;   // threads: two waves of 32 rows
+constexpr int kDMK = 32;    // keys per tile
+
+template <int DH>
+__global__ __launch_bounds__(kDMT) void attend_decode_mfma_kernel(DecAttnArgs A, float* part,
+                                                                  int nsplit) {
+    typedef uint16_t T;
+    constexpr int KS = DH / 16, DB = DH / 32, CPR = DH / 8;
+    constexpr int KSTR = DH + 8, VSTR = kDMK + 4;
+    __shared__ __align__(16) uint16_t sK[kDMK * KSTR];
+    __shared__ __align__(16) uint16_t sVt[DH * VSTR];
+    __shared__ int sOG[256], sOT[256];
+    __shared__ unsigned long long sKP[kSplitKeys], sVP[kSplitKeys];
+    __shared__ int sKT[kSplitKeys];
+    __shared__ int sNopen;
+    const int split = blockIdx.x, bh = blockIdx.y, b = bh / A.H, h = bh % A.H;
+    const int kvh = h / (A.H / A.KVH);
+    const int w = threadIdx.x / kWave, l = lane_id(), hl = l / 32;
+    const int row = w * 32 + (l % 32);
+    const int Kgw = A.Kg > 0 ? A.Kg : 1;
+    if (threadIdx.x == 0) sNopen = 0;
+    __syncthreads();
+    for (int i = threadIdx.x; i < A.Kg; i += kDMT) {
+        const int og = A.open_grp[(int64_t)bh * Kgw + i], ot = A.open_thr[(int64_t)bh * Kgw + i];
+        sOG[i] = og;
+        sOT[i] = ot;
+        if (og >= 0 && ot >= 0) atomicMax(&sNopen, i + 1);   // length of the opened list
+    }
+    __syncthreads();
+    DecKeys<T> keys;
+    keys.init(A, b, kvh, sOG, sOT, sNopen);
+    for (int t = threadIdx.x; t < kSplitKeys; t += kDMT) {
+        const int k = split * kSplitKeys + t;
+        const T* kp = nullptr;
+        const T* vp = nullptr;
+        int thr = kNoRow;
+        if (k < keys.a4) keys.locate(k, kp, vp, thr);
+        sKP[t] = (unsigned long long)kp;
+        sVP[t] = (unsigned long long)vp;
+        sKT[t] = kp ? thr : kNoRow;
+    }
+    // this lane's query row as MFMA B operands (8 dims of each 16-dim step)
+    const T* qg = reinterpret_cast<const T*>(A.q) + b * A.q_sb + h * A.q_sh;
+    bf16x8_t qb[KS];
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+        uint4 u = make_uint4(0u, 0u, 0u, 0u);
+        if (row < A.L) u = *reinterpret_cast<const uint4*>(qg + (int64_t)row * A.q_ss + s * 16 + 8 * hl);
+        qb[s] = __builtin_bit_cast(bf16x8_t, u);
+    }
+    __syncthreads();
+    floatx16_t acc[DB];
+#pragma unroll
+    for (int d = 0; d < DB; ++d) acc[d] = floatx16_t{};
+    float m_run = -INFINITY, l_run = 0.0f;
+    const float c2 = A.scale * 1.4426950408889634f;
+    const int nk = min(kSplitKeys, keys.a4 - split * kSplitKeys);
+    for (int t0 = 0; t0 < nk; t0 += kDMK) {
+        const uint4 z = make_uint4(0u, 0u, 0u, 0u);
+        for (int c = threadIdx.x; c < kDMK * CPR; c += kDMT) {
+            const int kk = c / CPR, dp = c % CPR;
+            const T* kp = reinterpret_cast<const T*>(sKP[t0 + kk]);
+            *reinterpret_cast<uint4*>(&sK[kk * KSTR + dp * 8]) =
+                kp ? *reinterpret_cast<const uint4*>(kp + dp * 8) : z;
+        }
+        for (int c = threadIdx.x; c < (kDMK / 2) * CPR; c += kDMT) {
+            const int kp2 = c / CPR, dg = c % CPR;
+            const T* v0 = reinterpret_cast<const T*>(sVP[t0 + 2 * kp2]);
+            const T* v1 = reinterpret_cast<const T*>(sVP[t0 + 2 * kp2 + 1]);
+            const uint4 u0 = v0 ? *reinterpret_cast<const uint4*>(v0 + dg * 8) : z;
+            const uint4 u1 = v1 ? *reinterpret_cast<const uint4*>(v1 + dg * 8) : z;
+            auto put = [&](int e, uint32_t x0, uint32_t x1) {
+                *reinterpret_cast<uint32_t*>(&sVt[(dg * 8 + 2 * e) * VSTR + 2 * kp2]) =
+                    (x0 & 0xffffu) | (x1 << 16);
+                *reinterpret_cast<uint32_t*>(&sVt[(dg * 8 + 2 * e + 1) * VSTR + 2 * kp2]) =
+                    (x0 >> 16) | (x1 & 0xffff0000u);
+            };
+            put(0, u0.x, u1.x);
+            put(1, u0.y, u1.y);
+            put(2, u0.z, u1.z);
+            put(3, u0.w, u1.w);
+        }
+        __syncthreads();
+        floatx16_t sc = {};
+#pragma unroll
+        for (int s = 0; s < KS; ++s)
+            sc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+                __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const uint4*>(
+                                                 &sK[(l % 32) * KSTR + s * 16 + 8 * hl])),
+                qb[s], sc, 0, 0, 0);
+        float mx = -INFINITY;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const int kk = 8 * (i / 4) + 4 * hl + (i % 4);
+            sc[i] = (row < A.L && t0 + kk < nk && row >= sKT[t0 + kk]) ? sc[i] * c2 : -INFINITY;
+            mx = fmaxf(mx, sc[i]);
+        }
+        mx = fmaxf(mx, __shfl_xor(mx, 32, kWave));
+        const float m_new = fmaxf(m_run, mx);
+        const float m_use = m_new == -INFINITY ? 0.0f : m_new;
+        const float alpha = exp2f(m_run - m_use);
+        float rs = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            sc[i] = exp2f(sc[i] - m_use);
+            rs += sc[i];
+        }
+        rs += __shfl_xor(rs, 32, kWave);
+        l_run = l_run * alpha + rs;
+        m_run = m_new;
+#pragma unroll
+        for (int d = 0; d < DB; ++d)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) acc[d][i] *= alpha;
+        bf16x8_t pb[2];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            pb[0][j] = (__bf16)sc[j];
+            pb[1][j] = (__bf16)sc[8 + j];
+        }
+#pragma unroll
+        for (int st = 0; st < 2; ++st) {
+            const int kb = 16 * st + 4 * hl;
+#pragma unroll
+            for (int d = 0; d < DB; ++d) {
+                const uint16_t* vr = &sVt[(d * 32 + l % 32) * VSTR];
+                const uint2 lo = *reinterpret_cast<const uint2*>(vr + kb);
+                const uint2 hi = *reinterpret_cast<const uint2*>(vr + kb + 8);
+                acc[d] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+                    __builtin_bit_cast(bf16x8_t, make_uint4(lo.x, lo.y, hi.x, hi.y)), pb[st],
+                    acc[d], 0, 0, 0);
+            }
+        }
+        __syncthreads();
+    }
+    if (row < A.L) {
+        float* pp = part + (((int64_t)bh * A.L + row) * nsplit + split) * (DH + 2);
+        if (hl == 0) {
+            pp[0] = m_run == -INFINITY ? -INFINITY : m_run * 0.6931471805599453f;
+            pp[1] = l_run;
+        }
+#pragma unroll
+        for (int d = 0; d < DB; ++d)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) pp[2 + d * 32 + 8 * (i / 4) + 4 * hl + (i % 4)] = acc[d][i];
+    }
+}
+
 template <int DT, int DH>
 __global__ __launch_bounds__(128) void decode_combine_kernel(DecAttnArgs A, const float* part,
                                                              int nsplit) {
@@ -1334,9 +1489,14 @@ int attend_decode_impl(const hga_config* cfg, int32_t L, int32_t n_closed, int64
                     (long long)need, (long long)workspace_bytes);
         float* part = static_cast<float*>(workspace);
         const dim3 g1((unsigned)nsplit, (unsigned)(a.B * a.H)), g2((unsigned)(a.B * a.H * L));
+        // blocks of 8+ rows (bf16, aligned query rows): the MFMA split kernel
+        const bool mfma = cfg->dtype == HGA_DTYPE_BF16 && !dca && L >= 8 &&
+                          (uintptr_t)q % 16 == 0 && ((q_sb | q_sh | q_ss) % 8) == 0;
 #define HGA_DS_CASE(DTV, DHV)                                                                    \
         if (cfg->dtype == DTV && D == DHV) {                                                   \
-            if (dca) attend_decode_split_kernel<DTV, DHV, true><<<g1, kDT, 0, st>>>(a, part, nsplit); \
+            if (mfma && DTV == HGA_DTYPE_BF16)                                                  \
+                attend_decode_mfma_kernel<DHV><<<g1, kDMT, 0, st>>>(a, part, nsplit);           \
+            else if (dca) attend_decode_split_kernel<DTV, DHV, true><<<g1, kDT, 0, st>>>(a, part, nsplit); \
             else attend_decode_split_kernel<DTV, DHV, false><<<g1, kDT, 0, st>>>(a, part, nsplit); \
             rc = launch_status("hga_attend_decode (split)");                                    \
             if (rc) return rc;                                                                  \

@@ -254,6 +254,10 @@ ATTN_CASES = [
     (2, 4, 2, 64, 32, 8, 5, 9, 1, 3, 17, 30, 2, torch.float32),
     (1, 4, 2, 64, 64, 16, 4, 64, 0, 0, 9, 0, 2, torch.float32),
     (1, 4, 2, 32, 16, 4, 3, 5, 1, 1, 0, 5, 3, torch.float32),         # nothing closed yet
+    # blocks of 8+ bf16 rows take the MFMA split kernel
+    (1, 8, 2, 128, 64, 16, 16, 64, 2, 8, 200, 0, 64, torch.bfloat16),  # a whole 64-row chunk
+    (2, 4, 2, 64, 32, 8, 5, 9, 1, 3, 40, 7, 20, torch.bfloat16),       # 20 rows from c0 7
+    (1, 4, 1, 128, 64, 16, 16, 64, 2, 8, 3, 16, 48, torch.bfloat16),   # few closed chunks
 ]
 
 
