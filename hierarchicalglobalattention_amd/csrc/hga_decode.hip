@@ -63,47 +63,106 @@ __device__ __forceinline__ uint32_t topk_lds(const float* vals, int n, int k) {
 }
 
 // Canonical scores (sequential fp32 FMA chain over d, then * scale, -0 -> +0) of one key row
-// against the L query rows in LDS; score r goes to out[r * stride] and the max over the rows is
-// returned.  The key row stays in registers and every lane of a wave reads the same query
-// element at a time (LDS broadcast), so a key costs one global read.
+// against query rows [r0, r1) held in LDS as fp32; score r goes to out[r * stride] and the max
+// over those rows is returned.  The key row is widened to fp32 once and kept in registers (bf16
+// widening is exact), every lane of a wave reads the same query element at a time (LDS
+// broadcast), and four rows' chains are interleaved (each keeps its own order).
+__device__ __forceinline__ float fin_score(float acc, float scale) {
+    const float sc = acc * scale;
+    return sc == 0.0f ? 0.0f : sc;
+}
 template <int DT, int DH>
-__device__ __forceinline__ float score_key_rows(const typename Elem<DT>::T* sQ, int L,
+__device__ __forceinline__ float score_key_rows(const float* sQ, int r0, int r1,
                                                 const typename Elem<DT>::T* kg, float* out,
                                                 int64_t stride, float scale) {
-    typedef typename Elem<DT>::T T;
-    constexpr int NV = DH * (int)sizeof(T) / 16;
-    uint4 kr[NV];
+    float kf[DH];
+    if constexpr (DT == HGA_DTYPE_BF16) {
 #pragma unroll
-    for (int v = 0; v < NV; ++v) kr[v] = reinterpret_cast<const uint4*>(kg)[v];
-    float mx = -INFINITY;
-    for (int r = 0; r < L; ++r) {
-        const uint4* qv = reinterpret_cast<const uint4*>(sQ + r * DH);
-        float acc = 0.0f;
+        for (int v = 0; v < DH / 8; ++v) {
+            const uint4 u = reinterpret_cast<const uint4*>(kg)[v];
+            const uint32_t w4[4] = {u.x, u.y, u.z, u.w};
 #pragma unroll
-        for (int v = 0; v < NV; ++v) {
-            const uint4 qq = qv[v], kk = kr[v];
-            if constexpr (DT == HGA_DTYPE_BF16) {
-                const uint32_t qw[4] = {qq.x, qq.y, qq.z, qq.w}, kw[4] = {kk.x, kk.y, kk.z, kk.w};
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    acc = fmaf(__uint_as_float(qw[e] << 16), __uint_as_float(kw[e] << 16), acc);
-                    acc = fmaf(__uint_as_float(qw[e] & 0xffff0000u),
-                               __uint_as_float(kw[e] & 0xffff0000u), acc);
-                }
-            } else {
-                acc = fmaf(__uint_as_float(qq.x), __uint_as_float(kk.x), acc);
-                acc = fmaf(__uint_as_float(qq.y), __uint_as_float(kk.y), acc);
-                acc = fmaf(__uint_as_float(qq.z), __uint_as_float(kk.z), acc);
-                acc = fmaf(__uint_as_float(qq.w), __uint_as_float(kk.w), acc);
+            for (int e = 0; e < 4; ++e) {
+                kf[8 * v + 2 * e] = __uint_as_float(w4[e] << 16);
+                kf[8 * v + 2 * e + 1] = __uint_as_float(w4[e] & 0xffff0000u);
             }
         }
-        float sc = acc * scale;
-        sc = sc == 0.0f ? 0.0f : sc;
+    } else {
+#pragma unroll
+        for (int v = 0; v < DH / 4; ++v) {
+            const float4 f = reinterpret_cast<const float4*>(kg)[v];
+            kf[4 * v] = f.x;
+            kf[4 * v + 1] = f.y;
+            kf[4 * v + 2] = f.z;
+            kf[4 * v + 3] = f.w;
+        }
+    }
+    float mx = -INFINITY;
+    int r = r0;
+    for (; r + 4 <= r1; r += 4) {
+        const float4* q0 = reinterpret_cast<const float4*>(sQ + r * DH);
+        constexpr int NV = DH / 4;
+        float a0 = 0.0f, a1 = 0.0f, a2 = 0.0f, a3 = 0.0f;
+#pragma unroll
+        for (int v = 0; v < NV; ++v) {
+            const float4 x0 = q0[v], x1 = q0[NV + v], x2 = q0[2 * NV + v], x3 = q0[3 * NV + v];
+            a0 = fmaf(x0.x, kf[4 * v], a0);
+            a1 = fmaf(x1.x, kf[4 * v], a1);
+            a2 = fmaf(x2.x, kf[4 * v], a2);
+            a3 = fmaf(x3.x, kf[4 * v], a3);
+            a0 = fmaf(x0.y, kf[4 * v + 1], a0);
+            a1 = fmaf(x1.y, kf[4 * v + 1], a1);
+            a2 = fmaf(x2.y, kf[4 * v + 1], a2);
+            a3 = fmaf(x3.y, kf[4 * v + 1], a3);
+            a0 = fmaf(x0.z, kf[4 * v + 2], a0);
+            a1 = fmaf(x1.z, kf[4 * v + 2], a1);
+            a2 = fmaf(x2.z, kf[4 * v + 2], a2);
+            a3 = fmaf(x3.z, kf[4 * v + 2], a3);
+            a0 = fmaf(x0.w, kf[4 * v + 3], a0);
+            a1 = fmaf(x1.w, kf[4 * v + 3], a1);
+            a2 = fmaf(x2.w, kf[4 * v + 3], a2);
+            a3 = fmaf(x3.w, kf[4 * v + 3], a3);
+        }
+        const float s0 = fin_score(a0, scale), s1 = fin_score(a1, scale);
+        const float s2 = fin_score(a2, scale), s3 = fin_score(a3, scale);
+        out[r * stride] = s0;
+        out[(r + 1) * stride] = s1;
+        out[(r + 2) * stride] = s2;
+        out[(r + 3) * stride] = s3;
+        mx = fmaxf(mx, fmaxf(fmaxf(s0, s1), fmaxf(s2, s3)));
+    }
+    for (; r < r1; ++r) {
+        const float4* qv = reinterpret_cast<const float4*>(sQ + r * DH);
+        float acc = 0.0f;
+#pragma unroll
+        for (int v = 0; v < DH / 4; ++v) {
+            const float4 x = qv[v];
+            acc = fmaf(x.x, kf[4 * v], acc);
+            acc = fmaf(x.y, kf[4 * v + 1], acc);
+            acc = fmaf(x.z, kf[4 * v + 2], acc);
+            acc = fmaf(x.w, kf[4 * v + 3], acc);
+        }
+        const float sc = fin_score(acc, scale);
         out[r * stride] = sc;
         mx = fmaxf(mx, sc);
     }
     return mx;
 }
+
+// Query rows [L][DH] of (b, h) into LDS as fp32 (exact widening of bf16).
+template <int DT, int DH>
+__device__ __forceinline__ void load_q_f32(const DecRouteArgs& A, int b, int h, float* sQ,
+                                           int nthreads) {
+    typedef typename Elem<DT>::T T;
+    const T* qg = reinterpret_cast<const T*>(A.q) + b * A.q_sb + h * A.q_sh;
+    for (int idx = threadIdx.x; idx < A.L * DH; idx += nthreads) {
+        const int r = idx / DH, d = idx % DH;
+        sQ[idx] = Elem<DT>::ld(qg, (int64_t)r * A.q_ss + d);
+    }
+}
+
+// Row groups of the scoring loops: blocks of 16+ rows split a key's rows over 4 thread groups.
+__host__ __device__ __forceinline__ int score_row_groups(int L) { return L >= 16 ? 4 : 1; }
 
 // Exact top-k (ties -> lower position) of LDS values vals[0..n) (-inf excluded), written in
 // position order to ov/oi (ids id0 + position), -inf / -1 past its length.
@@ -215,29 +274,32 @@ __global__ __launch_bounds__(kDT) void route_decode_part_kernel(DecRouteArgs A) 
     typedef typename Elem<DT>::T T;
     extern __shared__ __align__(16) unsigned char smem_raw[];
     const int L = A.L, K = A.Kc;
-    T* sQ = reinterpret_cast<T*>(smem_raw);                     // [L][DH]
-    float* sPool = reinterpret_cast<float*>(sQ + L * DH);       // [seg]
+    float* sQ = reinterpret_cast<float*>(smem_raw);             // [L][DH] fp32
+    float* sPool = sQ + L * DH;                                 // [RG][seg] partial maxima
     const int sg = blockIdx.x, bh = blockIdx.y, b = bh / A.H, h = bh % A.H;
     const int kvh = h / (A.H / A.KVH);
     int f_hi, l_lo;
     windows(A.n_closed, A.kf, A.kl, &f_hi, &l_lo);
     const int nmid = l_lo > f_hi ? l_lo - f_hi : 0;
     const int s0 = sg * A.seg, sl = min(A.seg, nmid - s0);   // s0 < nmid (host grid)
-    {
-        constexpr int VE = 16 / (int)sizeof(T);
-        const T* qg = reinterpret_cast<const T*>(A.q) + b * A.q_sb + h * A.q_sh;
-        for (int idx = threadIdx.x; idx < L * (DH / VE); idx += kDT) {
-            const int r = idx / (DH / VE), d = (idx % (DH / VE)) * VE;
-            *reinterpret_cast<uint4*>(sQ + r * DH + d) =
-                *reinterpret_cast<const uint4*>(qg + (int64_t)r * A.q_ss + d);
-        }
-    }
+    load_q_f32<DT, DH>(A, b, h, sQ, kDT);
     __syncthreads();
     const T* ckb = reinterpret_cast<const T*>(A.ck) + b * A.ck_sb + kvh * A.ck_sh +
                    (int64_t)(f_hi + s0) * DH;
     float* srow = A.ws + (int64_t)bh * L * A.SPW + s0;
-    for (int i = threadIdx.x; i < sl; i += kDT)                // pooled over all rows (:227)
-        sPool[i] = score_key_rows<DT, DH>(sQ, L, ckb + (int64_t)i * DH, srow + i, A.SPW, A.scale);
+    {
+        const int RG = score_row_groups(L), KP = kDT / RG, rg = threadIdx.x / KP;
+        const int rpg = (L + RG - 1) / RG, r0 = min(L, rg * rpg), r1 = min(L, r0 + rpg);
+        for (int i = threadIdx.x % KP; i < sl; i += KP)
+            sPool[rg * A.seg + i] = score_key_rows<DT, DH>(sQ, r0, r1, ckb + (int64_t)i * DH,
+                                                           srow + i, A.SPW, A.scale);
+        __syncthreads();
+        for (int i = threadIdx.x; i < sl; i += kDT) {          // pooled over all rows (:227)
+            float m = sPool[i];
+            for (int g = 1; g < RG; ++g) m = fmaxf(m, sPool[g * A.seg + i]);
+            sPool[i] = m;
+        }
+    }
     __syncthreads();
     if (threadIdx.x < kWave) {
         const int64_t o = ((int64_t)bh * A.nseg + sg) * K;
@@ -253,8 +315,8 @@ __global__ __launch_bounds__(kDT) void route_decode_kernel(DecRouteArgs A) {
     typedef typename Elem<DT>::T T;
     extern __shared__ __align__(16) unsigned char smem_raw[];
     const int SPD = A.SPD, M = A.M, L = A.L;
-    T* sQ = reinterpret_cast<T*>(smem_raw);                     // [L][DH]
-    float* sS = reinterpret_cast<float*>(sQ + L * DH);          // [L][SPD] group scores
+    float* sQ = reinterpret_cast<float*>(smem_raw);             // [L][DH] fp32
+    float* sS = sQ + L * DH;                                    // [L][SPD] group scores
     float* sPool = sS + L * SPD;                                // [SPD]
     int* sFirst = reinterpret_cast<int*>(sPool + SPD);          // [SPD] first requesting row
     int* sSel = sFirst + SPD;                                   // [64] sorted chunk ids
@@ -281,15 +343,7 @@ __global__ __launch_bounds__(kDT) void route_decode_kernel(DecRouteArgs A) {
     }
     const float scale = A.scale;
     const int K = A.Kc;
-    {
-        constexpr int VE = 16 / (int)sizeof(T);
-        const T* qg = reinterpret_cast<const T*>(A.q) + b * A.q_sb + h * A.q_sh;
-        for (int idx = threadIdx.x; idx < L * (DH / VE); idx += kDT) {
-            const int r = idx / (DH / VE), d = (idx % (DH / VE)) * VE;
-            *reinterpret_cast<uint4*>(sQ + r * DH + d) =
-                *reinterpret_cast<const uint4*>(qg + (int64_t)r * A.q_ss + d);
-        }
-    }
+    load_q_f32<DT, DH>(A, b, h, sQ, kDT);
     // ---- stage 1: pooled selection = top-Kc of the segments' pooled lists (:227, :231) ------
     if (w == 0) {
         const int64_t o = (int64_t)bh * A.nseg * K;
@@ -368,9 +422,19 @@ __global__ __launch_bounds__(kDT) void route_decode_kernel(DecRouteArgs A) {
     }
     // ---- groups of the selected chunks (:256-276) --------------------------------------------
     const T* gkb = reinterpret_cast<const T*>(A.gk) + b * A.gk_sb + kvh * A.gk_sh;
-    for (int i = threadIdx.x; i < T2; i += kDT)               // pooled over all rows (:264)
-        sPool[i] = score_key_rows<DT, DH>(sQ, L, gkb + ((int64_t)sSel[i / M] * M + i % M) * DH,
-                                          sS + i, SPD, scale);
+    {
+        const int RG = score_row_groups(L), KP = kDT / RG, rg = threadIdx.x / KP;
+        const int rpg = (L + RG - 1) / RG, r0 = min(L, rg * rpg), r1 = min(L, r0 + rpg);
+        for (int i = threadIdx.x % KP; i < T2; i += KP)
+            score_key_rows<DT, DH>(sQ, r0, r1, gkb + ((int64_t)sSel[i / M] * M + i % M) * DH,
+                                   sS + i, SPD, scale);
+    }
+    __syncthreads();
+    for (int i = threadIdx.x; i < T2; i += kDT) {             // pooled over all rows (:264)
+        float m = -INFINITY;
+        for (int r = 0; r < L; ++r) m = fmaxf(m, sS[r * SPD + i]);
+        sPool[i] = m;
+    }
     __syncthreads();
     if (w == 0) {
         // opened = pooled top-Kg (:265), ascending candidate order
@@ -1263,25 +1327,27 @@ extern "C" int32_t hga_decode_widths(const hga_config* cfg, int32_t n_closed, in
 namespace hga {
 namespace {
 // Stage-1 segmentation of a decode block's pool: segment length, count and the scoring kernel's
-// LDS bytes.  Segments of 128 (L <= 4) or 256 chunks give one workgroup each enough work; longer
-// segments keep the merge's candidates (nseg * Kc) within one wave selection.
+// LDS bytes.  Segments of 128 (L <= 4), 256 (L < 16) or 64 chunks (L >= 16: 4 row groups per
+// key) give each workgroup's 256 threads work; longer segments keep the merge's candidates
+// (nseg * Kc) within one wave selection.
 struct DecSeg {
     int seg, nseg, spd;
     size_t lds;
 };
 int dec_segments(const hga_config* cfg, int L, int nmid, int Kc, DecSeg* o) {
-    const size_t esz = cfg->dtype == HGA_DTYPE_BF16 ? 2 : 4;
-    const int64_t room = ((int64_t)163840 - 16 - (int64_t)(esz * L * cfg->head_dim)) / 4;
+    const int64_t room =
+        ((int64_t)163840 - 16 - (int64_t)(4 * L * cfg->head_dim)) / (4 * score_row_groups(L));
     const int cap = 64 * kDecJ / (Kc > 0 ? Kc : 1);
-    int seg = L <= 4 ? 128 : 256;
+    const int RG = score_row_groups(L);
+    int seg = RG == 4 ? 64 : (L <= 4 ? 128 : 256);
     if (nmid > (int64_t)seg * cap) seg = (nmid + cap - 1) / cap;
     HGA_REQUIRE(seg <= 64 * kDecSegJ && seg <= room, HGA_ERR_UNSUPPORTED,
                 "hga_route_decode: pool of %d chunks too long for L=%d x head_dim %d", nmid, L,
                 cfg->head_dim);
     o->seg = seg;
     o->nseg = nmid > 0 ? (nmid + seg - 1) / seg : 0;
-    o->spd = nmid < seg ? nmid : seg;
-    o->lds = esz * (size_t)L * cfg->head_dim + sizeof(float) * (size_t)o->spd + 16;
+    o->spd = seg;   // [row groups][seg] partial maxima
+    o->lds = sizeof(float) * ((size_t)L * cfg->head_dim + (size_t)RG * seg) + 16;
     return HGA_OK;
 }
 }  // namespace
@@ -1363,8 +1429,8 @@ extern "C" int hga_route_decode(const hga_config* cfg, int32_t L, int32_t n_clos
     const int Kcw = a.Kc > 0 ? a.Kc : 1;
     HGA_REQUIRE(a.Kg <= 256, HGA_ERR_UNSUPPORTED, "hga_route_decode: top-k groups %d > 256", a.Kg);
     a.SPD = ((T2max > Kcw ? T2max : Kcw) + 1) | 1;
-    const size_t lds = esz * (size_t)L * D + sizeof(int) * (136 + 256 + (size_t)Kcw) + 16 +
-                       sizeof(float) * (size_t)(L + 2) * a.SPD;
+    const size_t lds = sizeof(float) * (size_t)L * D + sizeof(int) * (136 + 256 + (size_t)Kcw) +
+                       16 + sizeof(float) * (size_t)(L + 2) * a.SPD;
     HGA_REQUIRE(lds <= 163840, HGA_ERR_UNSUPPORTED,
                 "hga_route_decode: L=%d x head_dim %d x %d groups leave no LDS", L, D, T2max);
     if (a.Kc > 0) {
