@@ -199,10 +199,11 @@ def _rms(x):
     return x * torch.rsqrt(x.pow(2).mean(-1, keepdim=True) + 1e-6)
 
 
-def run_decode(*, ctx, B, tc, tg, tier, steps, warmup, needles=False, seed=0):
-    """Decode of `steps + warmup` one-token steps per sequence after a seeded c3-style context of
-    `ctx` tokens.  A step is one decode_block (token write, decode routing, chunk close when the
-    active chunk fills) plus the routed attention over its working set, for all B sequences.
+def run_decode(*, ctx, B, tc, tg, tier, steps, warmup, needles=False, seed=0, block=1):
+    """Decode of `steps + warmup` steps of `block` tokens per sequence after a seeded c3-style
+    context of `ctx` tokens (block 64: the Qwen chat's 64-token prompt blocks).  A step is one
+    decode_block (token writes, decode routing, chunk close when the active chunk fills) plus the
+    routed attention over its working set, for all B sequences.
     tier "ram": the closed-token record is pinned host memory (the GPU keeps summaries, the
     first window and a ring of last-window chunks); "vram": everything in HBM.  needles: KV heads
     0-1 of every sequence get 4 chunks of keys scaled x8 at seeded random chunk ids."""
@@ -213,7 +214,7 @@ def run_decode(*, ctx, B, tc, tg, tier, steps, warmup, needles=False, seed=0):
     c = DEC_CFG
     dev = torch.device("cuda:0")
     H, KVH, Dh, C = c["H"], c["KVH"], c["Dh"], c["C"]
-    T = ctx + warmup + steps
+    T = ctx + (warmup + steps) * block
     g = torch.Generator(device=dev).manual_seed(seed)
     k_raw = _rms(torch.randn(B, KVH, T, Dh, device=dev, generator=g)).to(torch.bfloat16)
     if needles:
@@ -223,7 +224,8 @@ def run_decode(*, ctx, B, tc, tg, tier, steps, warmup, needles=False, seed=0):
                 for n in torch.randperm(ctx // C, generator=gc)[:4].tolist():
                     k_raw[b, kvh, n * C:(n + 1) * C] *= 8
     v = torch.randn(B, KVH, T, Dh, device=dev, generator=g).to(torch.bfloat16)
-    q_raw = _rms(torch.randn(B, H, warmup + steps, Dh, device=dev, generator=g)).to(torch.bfloat16)
+    q_raw = _rms(torch.randn(B, H, (warmup + steps) * block, Dh, device=dev,
+                             generator=g)).to(torch.bfloat16)
     rcfg = RouterConfig(nhead=H, kv_heads=KVH, head_dim=Dh, chunk_size=C, group_size=c["gs"],
                         topk_chunks=tc, topk_groups=tg, theta=c["theta"])
     pol = ChunkPlacementPolicy(keep_first=c["kf"], keep_last=c["kl"], first_token_level=True)
@@ -242,9 +244,9 @@ def run_decode(*, ctx, B, tc, tg, tier, steps, warmup, needles=False, seed=0):
     stats = dict(open_groups=0, open_groups_union=0, samples=0)
 
     def step(i, timed):
-        p = ctx + i
-        sl = slice(p, p + 1)
-        qi = q[:, :, i:i + 1]
+        p = ctx + i * block
+        sl = slice(p, p + block)
+        qi = q[:, :, i * block:(i + 1) * block]
         if timed is not None:
             timed[0].record()
         routed = router.decode_block(0, qi, k_rope[:, :, sl], k_raw[:, :, sl], v[:, :, sl], p)
@@ -291,8 +293,9 @@ def run_decode(*, ctx, B, tc, tg, tier, steps, warmup, needles=False, seed=0):
     ns = max(stats["samples"], 1)
     grp_bytes = c["gs"] * Dh * 2 * 2          # K and V of one 16-token group, bf16
     rd = stats["open_groups"] / ns * grp_bytes
-    return dict(ctx=ctx, batch=B, topk_chunks=tc, topk_groups=tg, tier=tier, steps=steps,
-                ms_per_step=ms, us_per_step_layer=ms * 1e3, tokens_per_s=B / (ms * 1e-3),
+    return dict(ctx=ctx, batch=B, block=block, topk_chunks=tc, topk_groups=tg, tier=tier,
+                steps=steps, ms_per_step=ms, us_per_step_layer=ms * 1e3,
+                tokens_per_s=B * block / (ms * 1e-3),
                 device_ms=dict(decode_block=route_ms, attention=attn_ms),
                 opened_group_bytes_per_step=rd,
                 opened_group_bytes_per_step_dedup=stats["open_groups_union"] / ns * grp_bytes,
@@ -371,6 +374,8 @@ def main():
                                       warmup=8),
             "c5_b64_64k_vram": run_decode(ctx=65536, B=64, tc=32, tg=128, tier="vram",
                                           steps=max(ds // 8, 4), warmup=4, needles=True),
+            "c4_32k_ram_64token_blocks": run_decode(ctx=32768, B=1, tc=16, tg=64, tier="ram",
+                                                    steps=max(ds // 8, 4), warmup=4, block=64),
         }
         torch.cuda.empty_cache()
     cpu = None

@@ -290,9 +290,10 @@ __global__ __launch_bounds__(kDT) void route_decode_part_kernel(DecRouteArgs A) 
     {
         const int RG = score_row_groups(L), KP = kDT / RG, rg = threadIdx.x / KP;
         const int rpg = (L + RG - 1) / RG, r0 = min(L, rg * rpg), r1 = min(L, r0 + rpg);
+        // a one-row block needs only the pooled score (its rows request the whole selection)
         for (int i = threadIdx.x % KP; i < sl; i += KP)
-            sPool[rg * A.seg + i] = score_key_rows<DT, DH>(sQ, r0, r1, ckb + (int64_t)i * DH,
-                                                           srow + i, A.SPW, A.scale);
+            sPool[rg * A.seg + i] = score_key_rows<DT, DH>(
+                sQ, r0, r1, ckb + (int64_t)i * DH, L == 1 ? sPool + i : srow + i, A.SPW, A.scale);
         __syncthreads();
         for (int i = threadIdx.x; i < sl; i += kDT) {          // pooled over all rows (:227)
             float m = sPool[i];
@@ -1327,9 +1328,10 @@ extern "C" int32_t hga_decode_widths(const hga_config* cfg, int32_t n_closed, in
 namespace hga {
 namespace {
 // Stage-1 segmentation of a decode block's pool: segment length, count and the scoring kernel's
-// LDS bytes.  Segments of 128 (L <= 4), 256 (L < 16) or 64 chunks (L >= 16: 4 row groups per
-// key) give each workgroup's 256 threads work; longer segments keep the merge's candidates
-// (nseg * Kc) within one wave selection.
+// LDS bytes.  Segments of at least 128 (L <= 4), 256 (L < 16) or 64 chunks (L >= 16: 4 row
+// groups per key) give each workgroup's 256 threads work; longer segments where the grid already
+// has about 1024 workgroups, or to keep the merge's candidates (nseg * Kc) within one wave
+// selection.
 struct DecSeg {
     int seg, nseg, spd;
     size_t lds;
@@ -1340,6 +1342,14 @@ int dec_segments(const hga_config* cfg, int L, int nmid, int Kc, DecSeg* o) {
     const int cap = 64 * kDecJ / (Kc > 0 ? Kc : 1);
     const int RG = score_row_groups(L);
     int seg = RG == 4 ? 64 : (L <= 4 ? 128 : 256);
+    // split a pool only as far as the grid needs: about 1024 scoring workgroups in all
+    const int64_t heads = (int64_t)cfg->batch * cfg->heads;
+    const int64_t want = heads >= 1024 ? 1 : (1024 + heads - 1) / heads;
+    if (nmid > seg * want) {
+        seg = (int)((nmid + want - 1) / want);
+        if (seg > 64 * kDecSegJ) seg = 64 * kDecSegJ;
+        if (seg > room) seg = (int)room;
+    }
     if (nmid > (int64_t)seg * cap) seg = (nmid + cap - 1) / cap;
     HGA_REQUIRE(seg <= 64 * kDecSegJ && seg <= room, HGA_ERR_UNSUPPORTED,
                 "hga_route_decode: pool of %d chunks too long for L=%d x head_dim %d", nmid, L,
