@@ -159,16 +159,19 @@ def run_gpu(args):
         # gradient, same block and routing; 5 products per visible (query, key) pair
         q = ops.rope(hc, q_raw, cos, sin)
         k_rope = ops.rope(hc, k_raw, cos, sin)
-        out = ops.attend_prefill(hc, q, k_rope, v, r_t["open_grp"], r_t["open_thr"], r_t["Kg"])
+        # as in training: the forward keeps each row's log-sum-exp for the backward
+        lse = torch.empty(B, c["H"], S, dtype=torch.float32, device=dev)
+        out = ops.attend_prefill(hc, q, k_rope, v, r_t["open_grp"], r_t["open_thr"], r_t["Kg"],
+                                 lse=lse)
         dout = torch.randn_like(out)
         args_b = (hc, q, k_rope, v, out, dout, r_t["open_grp"], r_t["open_thr"], r_t["Kg"])
-        ops.attend_prefill_bwd(*args_b)
+        ops.attend_prefill_bwd(*args_b, lse=lse)
         torch.cuda.synchronize()
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         reps = 3
         e0.record()
         for _ in range(reps):
-            ops.attend_prefill_bwd(*args_b)
+            ops.attend_prefill_bwd(*args_b, lse=lse)
         e1.record()
         torch.cuda.synchronize()
         bms = e0.elapsed_time(e1) / reps

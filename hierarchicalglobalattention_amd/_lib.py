@@ -44,10 +44,10 @@ SIGNATURES = {
     "hga_route_prefill": ([_CFG, _i32, _vp, _i64, _i64, _i64, _vp, _i64, _i64, _vp, _i64, _i64,
                            _vp, _vp, _vp, _vp, _vp, _vp, _i32, _vp, _vp], ctypes.c_int),
     "hga_attend_prefill": ([_CFG, _i32, _vp, _i64, _i64, _i64, _vp, _i64, _i64, _i64, _vp,
-                            _i64, _i64, _i64, _vp, _vp, _i32, _vp, _i64, _i64, _i64, _vp, _i64,
-                            _vp], ctypes.c_int),
+                            _i64, _i64, _i64, _vp, _vp, _i32, _vp, _i64, _i64, _i64, _vp, _vp,
+                            _i64, _vp], ctypes.c_int),
     "hga_attend_prefill_workspace": ([_CFG, _i32, ctypes.POINTER(ctypes.c_int64)], _i32),
-    "hga_attend_prefill_bwd": ([_CFG, _i32] + [_vp, _i64, _i64, _i64] * 5 + [_vp, _vp, _i32] +
+    "hga_attend_prefill_bwd": ([_CFG, _i32] + [_vp, _i64, _i64, _i64] * 5 + [_vp, _vp, _vp, _i32] +
                                [_vp, _i64, _i64, _i64] * 3 + [_vp, _i64, _vp], ctypes.c_int),
     "hga_attend_prefill_bwd_workspace": ([_CFG, _i32, ctypes.POINTER(ctypes.c_int64)], _i32),
     "hga_decode_widths": ([_CFG, _i32, _I32P, _I32P], _i32),

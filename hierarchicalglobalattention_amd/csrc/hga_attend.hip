@@ -172,6 +172,8 @@ __global__ __launch_bounds__(kAT) void attend_mfma_kernel(AttnArgs A) {
         __syncthreads();
     }
     if (wave_active && row < rows) {
+        if (A.lse && l < 32)                // both half-waves hold the row
+            A.lse[((int64_t)b * A.H + h) * A.S + (int64_t)A.C * n + row] = m_run + log2f(l_run);
         const float inv = l_run > 0.0f ? 1.0f / l_run : 0.0f;
         uint16_t* op = reinterpret_cast<uint16_t*>(A.out) + b * A.o_sb + h * A.o_sh +
                        ((int64_t)A.C * n + row) * A.o_ss;
@@ -257,6 +259,9 @@ __global__ __launch_bounds__(kVT) void attend_valu_kernel(AttnArgs A) {
             }
         }
         T* op = reinterpret_cast<T*>(A.out) + b * A.o_sb + h * A.o_sh;
+        if (A.lse && l == 0)
+            A.lse[((int64_t)b * A.H + h) * A.S + (int64_t)A.C * n + t] =
+                (m_run + logf(l_run)) * 1.4426950408889634f;
         const float inv = l_run > 0.0f ? 1.0f / l_run : 0.0f;
 #pragma unroll
         for (int e = 0; e < DPL; ++e) {
@@ -359,7 +364,7 @@ __device__ __forceinline__ void lds_copy16_s(const void* sbase, uint32_t voff, u
 constexpr float kRescaleLog2 = 8.0f;   // a row's softmax reference may trail its max by 2^8
 constexpr int kV2Threads = 128;        // two waves: rows 0-31 and 32-63 of a query chunk
 
-template <int DH>
+template <int DH, bool LSE>
 __global__ __launch_bounds__(kV2Threads) void attend_v2_kernel(AttnArgs A,
                                                                const uint16_t* __restrict__ kbl,
                                                                const uint16_t* __restrict__ vbl,
@@ -576,6 +581,8 @@ __global__ __launch_bounds__(kV2Threads) void attend_v2_kernel(AttnArgs A,
     }
     const float lt = l_run + __shfl_xor(l_run, 32, kWave);
     if (row >= rows) return;
+    if constexpr (LSE)
+        if (g == 0) A.lse[((int64_t)b * A.H + h) * A.S + (int64_t)C * n + row] = m_ref * c2 + log2f(lt);
     const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
     uint16_t* op = reinterpret_cast<uint16_t*>(A.out) + b * A.o_sb + h * A.o_sh +
                    ((int64_t)C * n + row) * A.o_ss;
@@ -626,7 +633,7 @@ extern "C" int hga_attend_prefill(const hga_config* cfg, int32_t S, const void* 
                                   int64_t k_sh, int64_t k_ss, const void* v, int64_t v_sb,
                                   int64_t v_sh, int64_t v_ss, const int32_t* open_grp,
                                   const int32_t* open_thr, int32_t Kg, void* out, int64_t o_sb,
-                                  int64_t o_sh, int64_t o_ss, void* workspace,
+                                  int64_t o_sh, int64_t o_ss, float* lse, void* workspace,
                                   int64_t workspace_bytes, void* stream) {
     using namespace hga;
     int rc = check_config(cfg);
@@ -644,7 +651,7 @@ extern "C" int hga_attend_prefill(const hga_config* cfg, int32_t S, const void* 
     a.B = cfg->batch; a.H = cfg->heads; a.KVH = cfg->kv_heads; a.S = S;
     a.C = cfg->chunk_size; a.gs = cfg->group_size; a.M = a.C / a.gs;
     a.N = (S + a.C - 1) / a.C; a.kf = cfg->keep_first; a.kl = cfg->keep_last;
-    a.Kg = Kg; a.scale = cfg->scale;
+    a.Kg = Kg; a.scale = cfg->scale; a.lse = lse;
     int nN, nKc, nKg;
     hga_prefill_widths(cfg, S, &nN, &nKc, &nKg);
     HGA_REQUIRE(Kg == nKg, HGA_ERR_ARG, "hga_attend_prefill: Kg %d != routing width %d", Kg, nKg);
@@ -680,12 +687,14 @@ extern "C" int hga_attend_prefill(const hga_config* cfg, int32_t S, const void* 
             kv_block_kernel<128><<<tg, 256, 0, st>>>((const uint16_t*)k, k_sb, k_sh, k_ss,
                                                      (const uint16_t*)v, v_sb, v_sh, v_ss, kbl,
                                                      vbl, S, Sp, a.KVH);
-            attend_v2_kernel<128><<<grid, kV2Threads, lds2, st>>>(a, kbl, vbl, Sp, nb_cap);
+            if (lse) attend_v2_kernel<128, true><<<grid, kV2Threads, lds2, st>>>(a, kbl, vbl, Sp, nb_cap);
+            else attend_v2_kernel<128, false><<<grid, kV2Threads, lds2, st>>>(a, kbl, vbl, Sp, nb_cap);
         } else {
             kv_block_kernel<64><<<tg, 256, 0, st>>>((const uint16_t*)k, k_sb, k_sh, k_ss,
                                                     (const uint16_t*)v, v_sb, v_sh, v_ss, kbl,
                                                     vbl, S, Sp, a.KVH);
-            attend_v2_kernel<64><<<grid, kV2Threads, lds2, st>>>(a, kbl, vbl, Sp, nb_cap);
+            if (lse) attend_v2_kernel<64, true><<<grid, kV2Threads, lds2, st>>>(a, kbl, vbl, Sp, nb_cap);
+            else attend_v2_kernel<64, false><<<grid, kV2Threads, lds2, st>>>(a, kbl, vbl, Sp, nb_cap);
         }
         return launch_status("hga_attend_prefill");
     }

@@ -152,9 +152,9 @@ __global__ __launch_bounds__(kBT) void attend_bwd_valu_kernel(BwdArgs P) {
         }
     };
 
-    // pass 1: log2-domain softmax statistics of each row
+    // pass 1: log2-domain softmax statistics of each row (the forward's, when it kept them)
     float m = -INFINITY, lsum = 0.0f;
-    for (int tile = 0; tile < ntiles; ++tile) {
+    for (int tile = 0; tile < (A.lse ? 0 : ntiles); ++tile) {
         load_tile(tile, false);
         float s[8];
         dots(sQ, sK, s);
@@ -178,7 +178,8 @@ __global__ __launch_bounds__(kBT) void attend_bwd_valu_kernel(BwdArgs P) {
         }
         __syncthreads();
     }
-    const float lse = lsum > 0.0f ? m + log2f(lsum) : INFINITY;
+    const float lse = A.lse ? (r < rows ? A.lse[((int64_t)b * A.H + h) * A.S + r0 + r] : INFINITY)
+                            : (lsum > 0.0f ? m + log2f(lsum) : INFINITY);
     const float Dr = sD[r];
 
     // pass 2
@@ -388,9 +389,9 @@ __global__ __launch_bounds__(kMT) void attend_bwd_mfma_kernel(BwdArgs P) {
     };
     auto key_of = [&](int i) { return 8 * (i / 4) + 4 * hl + (i % 4); };
 
-    // pass 1: log2-domain softmax statistics of each row
+    // pass 1: log2-domain softmax statistics of each row (the forward's, when it kept them)
     float m_run = -INFINITY, l_run = 0.0f;
-    for (int tile = 0; tile < ntiles; ++tile) {
+    for (int tile = 0; tile < (A.lse ? 0 : ntiles); ++tile) {
         load_tile(tile, false);
         floatx16 sc = scores(sK, qb);
         float mx = -INFINITY;
@@ -410,7 +411,8 @@ __global__ __launch_bounds__(kMT) void attend_bwd_mfma_kernel(BwdArgs P) {
         m_run = m_new;
         __syncthreads();
     }
-    const float lse = l_run > 0.0f ? m_run + log2f(l_run) : INFINITY;
+    const float lse = A.lse ? (rv ? A.lse[((int64_t)b * A.H + h) * A.S + r0 + row] : INFINITY)
+                            : (l_run > 0.0f ? m_run + log2f(l_run) : INFINITY);
 
     // pass 2
     floatx16 dq[DB];
@@ -519,8 +521,8 @@ extern "C" int hga_attend_prefill_bwd(
     const hga_config* cfg, int32_t S, const void* q, int64_t q_sb, int64_t q_sh, int64_t q_ss,
     const void* k, int64_t k_sb, int64_t k_sh, int64_t k_ss, const void* v, int64_t v_sb,
     int64_t v_sh, int64_t v_ss, const void* out, int64_t o_sb, int64_t o_sh, int64_t o_ss,
-    const void* dout, int64_t g_sb, int64_t g_sh, int64_t g_ss, const int32_t* open_grp,
-    const int32_t* open_thr, int32_t Kg, void* dq, int64_t dq_sb, int64_t dq_sh, int64_t dq_ss,
+    const void* dout, int64_t g_sb, int64_t g_sh, int64_t g_ss, const float* lse,
+    const int32_t* open_grp, const int32_t* open_thr, int32_t Kg, void* dq, int64_t dq_sb, int64_t dq_sh, int64_t dq_ss,
     void* dk, int64_t dk_sb, int64_t dk_sh, int64_t dk_ss, void* dv, int64_t dv_sb,
     int64_t dv_sh, int64_t dv_ss, void* workspace, int64_t workspace_bytes, void* stream) {
     using namespace hga;
@@ -552,7 +554,7 @@ extern "C" int hga_attend_prefill_bwd(
     a.B = cfg->batch; a.H = cfg->heads; a.KVH = cfg->kv_heads; a.S = S;
     a.C = cfg->chunk_size; a.gs = cfg->group_size; a.M = a.C / a.gs;
     a.N = (S + a.C - 1) / a.C; a.kf = cfg->keep_first; a.kl = cfg->keep_last;
-    a.Kg = Kg; a.scale = cfg->scale;
+    a.Kg = Kg; a.scale = cfg->scale; a.lse = const_cast<float*>(lse);
     p.dout = dout; p.g_sb = g_sb; p.g_sh = g_sh; p.g_ss = g_ss;
     p.dq = dq; p.dq_sb = dq_sb; p.dq_sh = dq_sh; p.dq_ss = dq_ss;
     const int D = cfg->head_dim;

@@ -27,6 +27,9 @@ struct AttnArgs {
     const int32_t* open_thr;
     int B, H, KVH, S, N, C, gs, M, kf, kl, Kg;
     float scale;
+    // NULL or [B, H, S]: each row's log-sum-exp of its scores times scale*log2(e), in log2 units
+    // (written by the forward kernels, read by the backward instead of recomputing it)
+    float* lse;
 };
 
 struct KeySeq {

@@ -181,10 +181,12 @@ def route_prefill(cfg: HgaConfig, q: torch.Tensor, chunk_k: torch.Tensor,
 
 def attend_prefill(cfg: HgaConfig, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
                    open_grp: torch.Tensor, open_thr: torch.Tensor, Kg: int,
-                   out: torch.Tensor | None = None) -> torch.Tensor:
+                   out: torch.Tensor | None = None,
+                   lse: torch.Tensor | None = None) -> torch.Tensor:
     """Exact attention of q [B,H,S,Dh] over the routed working set (RoPE'd k and v
-    [B,KVH,S,Dh]); returns out [B,H,S,Dh] in q's dtype."""
-    _dev(q, k, v, open_grp, open_thr)
+    [B,KVH,S,Dh]); returns out [B,H,S,Dh] in q's dtype.  lse: optional fp32 [B,H,S] that
+    receives each row's log-sum-exp (log2 units of scale*log2(e) scores) for the backward."""
+    _dev(q, k, v, open_grp, open_thr, lse)
     B, H, S, D = q.shape
     if out is None:
         out = torch.empty((B, H, S, D), dtype=q.dtype, device=q.device)
@@ -194,7 +196,7 @@ def attend_prefill(cfg: HgaConfig, q: torch.Tensor, k: torch.Tensor, v: torch.Te
     wbuf = torch.empty(max(ws, 16), dtype=torch.uint8, device=q.device) if ws else None
     check(lib().hga_attend_prefill(
         ctypes.byref(cfg), S, _p(q), *_s4(q), _p(k), *_s4(k), _p(v), *_s4(v), _p(og), _p(ot),
-        Kg, _p(out), *_s4(out), _p(wbuf), ws, _stream()), "hga_attend_prefill")
+        Kg, _p(out), *_s4(out), _p(lse), _p(wbuf), ws, _stream()), "hga_attend_prefill")
     return out
 
 
@@ -208,10 +210,11 @@ def attend_prefill_workspace(cfg: HgaConfig, S: int) -> int:
 
 def attend_prefill_bwd(cfg: HgaConfig, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
                        out: torch.Tensor, dout: torch.Tensor, open_grp: torch.Tensor,
-                       open_thr: torch.Tensor, Kg: int):
+                       open_thr: torch.Tensor, Kg: int, lse: torch.Tensor | None = None):
     """Gradients (dq [B,H,S,Dh], dk, dv [B,KVH,S,Dh]) of attend_prefill's output `out` for the
-    upstream gradient dout, in q's dtype."""
-    _dev(q, k, v, out, dout, open_grp, open_thr)
+    upstream gradient dout, in q's dtype; lse: attend_prefill's lse output for the same call
+    (optional: recomputed when absent)."""
+    _dev(q, k, v, out, dout, open_grp, open_thr, lse)
     B, H, S, D = q.shape
     dq = torch.empty((B, H, S, D), dtype=q.dtype, device=q.device)
     dk = torch.empty(k.shape, dtype=q.dtype, device=q.device)
@@ -226,7 +229,8 @@ def attend_prefill_bwd(cfg: HgaConfig, q: torch.Tensor, k: torch.Tensor, v: torc
     ws = torch.empty(max(n.value, 16), dtype=torch.uint8, device=q.device)
     check(lib().hga_attend_prefill_bwd(
         ctypes.byref(cfg), S, _p(q), *_s4(q), _p(k), *_s4(k), _p(v), *_s4(v), _p(out), *_s4(out),
-        _p(dout), *_s4(dout), _p(og), _p(ot), Kg, _p(dq), *_s4(dq), _p(dk), *_s4(dk), _p(dv),
+        _p(dout), *_s4(dout), _p(lse), _p(og), _p(ot), Kg, _p(dq), *_s4(dq), _p(dk), *_s4(dk),
+        _p(dv),
         *_s4(dv), _p(ws), n.value, _stream()), "hga_attend_prefill_bwd")
     return dq, dk, dv
 
@@ -237,15 +241,17 @@ class RoutedAttentionFunction(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, q, k, v, open_grp, open_thr, Kg, cfg):
-        out = attend_prefill(cfg, q, k, v, open_grp, open_thr, Kg)
-        ctx.save_for_backward(q, k, v, out, open_grp, open_thr)
+        B, H, S, _ = q.shape
+        lse = torch.empty((B, H, S), dtype=torch.float32, device=q.device)
+        out = attend_prefill(cfg, q, k, v, open_grp, open_thr, Kg, lse=lse)
+        ctx.save_for_backward(q, k, v, out, open_grp, open_thr, lse)
         ctx.Kg, ctx.cfg = Kg, cfg
         return out
 
     @staticmethod
     def backward(ctx, dout):
-        q, k, v, out, og, ot = ctx.saved_tensors
-        dq, dk, dv = attend_prefill_bwd(ctx.cfg, q, k, v, out, dout, og, ot, ctx.Kg)
+        q, k, v, out, og, ot, lse = ctx.saved_tensors
+        dq, dk, dv = attend_prefill_bwd(ctx.cfg, q, k, v, out, dout, og, ot, ctx.Kg, lse=lse)
         return dq, dk, dv, None, None, None, None
 
 

@@ -133,12 +133,14 @@ int hga_route_prefill(const hga_config* cfg, int32_t S, const void* q, int64_t q
  * keep_first and keep_last windows, and every opened group with open_thr <= t.
  * q/out: [B, H, S, Dh]; k/v: [B, KVH, S, Dh] (RoPE'd keys).  open_grp/open_thr as written by
  * hga_route_prefill (width Kg; Kg = 0 with 1-element arrays when routing is off).
+ * lse: NULL, or fp32 [B, H, S] receiving each row's log-sum-exp of its scores times
+ * scale*log2(e) (log2 units), which hga_attend_prefill_bwd can take instead of recomputing it.
  */
 int hga_attend_prefill(const hga_config* cfg, int32_t S, const void* q, int64_t q_sb,
                        int64_t q_sh, int64_t q_ss, const void* k, int64_t k_sb, int64_t k_sh,
                        int64_t k_ss, const void* v, int64_t v_sb, int64_t v_sh, int64_t v_ss,
                        const int32_t* open_grp, const int32_t* open_thr, int32_t Kg, void* out,
-                       int64_t o_sb, int64_t o_sh, int64_t o_ss, void* workspace,
+                       int64_t o_sb, int64_t o_sh, int64_t o_ss, float* lse, void* workspace,
                        int64_t workspace_bytes, void* stream);
 
 /* Device scratch bytes hga_attend_prefill needs for a block of S tokens (16-key blocked copies
@@ -153,7 +155,9 @@ int32_t hga_attend_prefill_workspace(const hga_config* cfg, int32_t S, int64_t* 
  * the same attention with torch autograd, HierarchicalGlobalAttentionRouted.py:137-177 over the
  * working set of vectorized.py:404-490; routing carries no gradient).  q/out/dout/dq:
  * [B, H, S, Dh]; k/v/dk/dv: [B, KVH, S, Dh]; out is hga_attend_prefill's output for the same
- * inputs and routing.  dk/dv sum the contributions of every query head of a KV head.
+ * inputs and routing, lse NULL or hga_attend_prefill's lse output for them (then the rows'
+ * softmax statistics are not recomputed).  dk/dv sum the contributions of every query head of a
+ * KV head.
  * chunk_size <= 64.  workspace: hga_attend_prefill_bwd_workspace bytes, 16-byte aligned (fp32
  * accumulators, cleared by the call's own kernels).
  */
@@ -162,7 +166,8 @@ int hga_attend_prefill_bwd(const hga_config* cfg, int32_t S, const void* q, int6
                            int64_t k_ss, const void* v, int64_t v_sb, int64_t v_sh, int64_t v_ss,
                            const void* out, int64_t o_sb, int64_t o_sh, int64_t o_ss,
                            const void* dout, int64_t g_sb, int64_t g_sh, int64_t g_ss,
-                           const int32_t* open_grp, const int32_t* open_thr, int32_t Kg,
+                           const float* lse, const int32_t* open_grp, const int32_t* open_thr,
+                           int32_t Kg,
                            void* dq, int64_t dq_sb, int64_t dq_sh, int64_t dq_ss, void* dk,
                            int64_t dk_sb, int64_t dk_sh, int64_t dk_ss, void* dv, int64_t dv_sb,
                            int64_t dv_sh, int64_t dv_ss, void* workspace, int64_t workspace_bytes,

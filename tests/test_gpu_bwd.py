@@ -3,7 +3,9 @@ through the drop-in module.
 
 * ops level: dq, dk, dv against the oracle's exact gradient (itself pinned to torch float64
   autograd of the masked dense attention, test_oracle_bwd.py) on random routing lists: opened
-  groups visible from a later row or never, ragged tails, GQA head sums, routing off.
+  groups visible from a later row or never, ragged tails, GQA head sums, routing off -- with the
+  rows' softmax statistics recomputed and taken from the forward (whose lse output is checked
+  against float64 log-sum-exp for each forward kernel).
   Tolerances: fp32 1e-4 and bf16 2e-2 max / 1e-2 mean abs error, relative to the gradient's
   largest magnitude when that exceeds 1.
 * module level: HierarchicalGlobalAttentionRouted forward + backward (RoPE transpose, routed
@@ -55,9 +57,10 @@ BWD_CASES = [
 @pytest.mark.parametrize("case", BWD_CASES, ids=lambda c: f"S{c[3]}D{c[4]}C{c[5]}gs{c[6]}"
                          f"{'bf16' if c[9] is torch.bfloat16 else 'f32'}")
 @pytest.mark.parametrize("Kg", [0, 6])
-def test_attend_prefill_bwd_vs_oracle(case, Kg):
+@pytest.mark.parametrize("keep_lse", [False, True], ids=["recompute", "fwd-lse"])
+def test_attend_prefill_bwd_vs_oracle(case, Kg, keep_lse):
     B, H, KVH, S, Dh, C, gs, kf, kl, dt = case
-    print(f"[bwd] ops {case} Kg={Kg}", flush=True)
+    print(f"[bwd] ops {case} Kg={Kg} lse={keep_lse}", flush=True)
     rng = np.random.default_rng(S + Dh + Kg)
     bf = oracle.bf16_round if dt is torch.bfloat16 else (lambda x: x)
     q = bf(rng.standard_normal((B, H, S, Dh)).astype(np.float32))
@@ -71,8 +74,9 @@ def test_attend_prefill_bwd_vs_oracle(case, Kg):
     T = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(DEV, dt)
     I = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(DEV)
     qd, kd, vd, gd = T(q), T(k), T(v), T(dout)
-    out = ops.attend_prefill(cfg, qd, kd, vd, I(og), I(ot), Kgc)
-    dq, dk, dv = ops.attend_prefill_bwd(cfg, qd, kd, vd, out, gd, I(og), I(ot), Kgc)
+    lse = torch.empty(B, H, S, device=DEV) if keep_lse else None
+    out = ops.attend_prefill(cfg, qd, kd, vd, I(og), I(ot), Kgc, lse=lse)
+    dq, dk, dv = ops.attend_prefill_bwd(cfg, qd, kd, vd, out, gd, I(og), I(ot), Kgc, lse=lse)
     torch.cuda.synchronize()
     ro = oracle.attend_prefill(q, k, v, C, gs, kf, kl, og, ot, oracle.attn_scale(Dh),
                                oracle.DT_BF16 if dt is torch.bfloat16 else oracle.DT_F32)
@@ -82,6 +86,39 @@ def test_attend_prefill_bwd_vs_oracle(case, Kg):
     for a, ref, what in ((dq, rq, "dq"), (dk, rk, "dk"), (dv, rv, "dv")):
         assert a.dtype == dt and a.shape == ref.shape
         _check(a, ref, dt, what)
+
+
+@pytest.mark.parametrize("shape", [
+    dict(S=300, Dh=128, C=64, gs=16, dt=torch.bfloat16),   # 16-key-block MFMA kernel
+    dict(S=150, Dh=64, C=32, gs=8, dt=torch.bfloat16),     # LDS-tiled MFMA kernel
+    dict(S=83, Dh=16, C=8, gs=4, dt=torch.float32),        # VALU kernel
+], ids=["v2", "lds", "valu"])
+def test_forward_lse_is_logsumexp(shape):
+    """The forward's lse output = log2 of the sum over the row's visible keys of
+    2^(scale*log2(e)*q.k), float64 under the routing mask."""
+    from test_oracle_bwd import routing_mask
+    B, H, KVH, kf, kl, Kg = 1, 4, 2, 1, 1, 5
+    S, Dh, C, gs, dt = shape["S"], shape["Dh"], shape["C"], shape["gs"], shape["dt"]
+    rng = np.random.default_rng(S)
+    bf = oracle.bf16_round if dt is torch.bfloat16 else (lambda x: x)
+    q = bf(rng.standard_normal((B, H, S, Dh)).astype(np.float32))
+    k = bf(rng.standard_normal((B, KVH, S, Dh)).astype(np.float32))
+    v = bf(rng.standard_normal((B, KVH, S, Dh)).astype(np.float32))
+    og, ot = random_lists(rng, B, H, S, C, gs, kf, kl, Kg)
+    cfg = _cfg(B, H, KVH, Dh, C, gs, kf, kl, Kg, dt)
+    _, _, Kgc = ops.prefill_widths(cfg, S)
+    og, ot = og[..., :max(Kgc, 1)], ot[..., :max(Kgc, 1)]
+    T = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(DEV, dt)
+    I = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(DEV)
+    lse = torch.full((B, H, S), float("nan"), device=DEV)
+    ops.attend_prefill(cfg, T(q), T(k), T(v), I(og), I(ot), Kgc, lse=lse)
+    mask = routing_mask(B, H, S, C, gs, kf, kl, og, ot)
+    s = np.einsum("bhsd,bhtd->bhst", q.astype(np.float64),
+                  np.repeat(k, H // KVH, axis=1).astype(np.float64)) * oracle.attn_scale(Dh)
+    s = np.where(mask, s, -np.inf)
+    mx = s.max(-1, keepdims=True)
+    ref = (mx[..., 0] + np.log(np.exp(s - mx).sum(-1))) * np.log2(np.e)
+    np.testing.assert_allclose(lse.cpu().numpy(), ref, atol=1e-3, rtol=1e-5)
 
 
 def test_attend_prefill_bwd_rejects_wide_chunks():
