@@ -584,6 +584,7 @@ class ChunkRouter:
         self.cfg = cfg
         self.store = store
         self._hcfg_cache: Dict[Tuple[int, torch.dtype], object] = {}
+        self._rot_cache: Dict[object, Tuple[torch.Tensor, torch.Tensor]] = {}   # fp32 rotary rows
 
     def reset(self) -> None:
         self.store.reset()
@@ -662,6 +663,16 @@ class ChunkRouter:
             self._close_chunk(layer, n, k_rope_chunk=None)
         return routed
 
+    def _rotary_rows(self, start: int, length: int, device):
+        """Rows [start, start + length) of the fp32 rotary table, sliced from a cached table
+        (each row depends on its position only, so the values equal rotary_for_positions')."""
+        cos, sin = self._rot_cache.get(device, (None, None))
+        if cos is None or cos.shape[0] < start + length:
+            n = max(2 * (cos.shape[0] if cos is not None else 0), start + length, 4096)
+            cos, sin = rotary_for_positions(self.cfg.theta, self.cfg.head_dim, 0, n, device)
+            self._rot_cache[device] = (cos, sin)
+        return cos[start:start + length], sin[start:start + length]
+
     def _close_chunk(self, layer: int, n: int, k_rope_chunk=None) -> None:
         """Summaries of the full active chunk n with the fp32 anchor table, then hand it to the
         store (ChunkRouter._close_active_chunk, chunk_router.py:631-657)."""
@@ -674,7 +685,7 @@ class ChunkRouter:
         else:
             s = n * C
         krope = src["recent_k"][:, :, s:s + C]
-        cf, sf = rotary_for_positions(cfg.theta, D, n * C, C, st.act_kraw.device)
+        cf, sf = self._rotary_rows(n * C, C, st.act_kraw.device)
         hc = self.hcfg(st.act_kraw.shape[0], st.act_kraw.dtype)
         ops.summarize(hc, st.act_kraw, krope, cf, sf, pos0=0, chunk_k=st.chunk_k[:, :, n:],
                       group_k=st.group_k[:, :, n:])
