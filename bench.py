@@ -344,7 +344,7 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py: this build targets a single MI355X; multi-GPU runs are out of scope "
-              "(see DESIGN.md for how the path would shard)", file=sys.stderr)
+              "(one GPU's throughput is the reported value)", file=sys.stderr)
         sys.exit(2)
     if args.copy_calibration:
         copy_calibration()
