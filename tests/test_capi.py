@@ -74,3 +74,46 @@ def test_cutoff_pair_closed_forms():
     for theta, C, Dh, want in [(1e4, 64, 64, 17), (1e6, 64, 128, 23), (1e4, 8, 16, 3)]:
         assert ops.mixed_cutoff_pair(theta, C, Dh) == want
         assert oracle.cutoff_pair(theta, C, Dh) == want
+
+
+def test_workspace_queries_and_checks_without_launch():
+    """Host-side sizing of the decode router's and the backward's workspaces, and the argument
+    checks that run before any kernel (fake device pointers are never dereferenced)."""
+    import torch
+    lib = _lib.lib()
+
+    def cfg_of(B, H, KVH, Dh, C, gs, tc, tg, kf, kl, dt=torch.bfloat16):
+        return ops.make_config(batch=B, heads=H, kv_heads=KVH, head_dim=Dh, chunk_size=C,
+                               group_size=gs, topk_chunks=tc, topk_groups=tg, keep_first=kf,
+                               keep_last=kl, cutoff_pair=3, dtype=dt)
+
+    def route_ws(cfg, L, n):
+        nb = ctypes.c_int64(-1)
+        rc = lib.hga_route_decode_workspace(ctypes.byref(cfg), L, n, ctypes.byref(nb))
+        return rc, nb.value
+
+    cfg = cfg_of(1, 32, 4, 128, 64, 16, 16, 64, 2, 8)
+    assert route_ws(cfg, 1, 10) == (0, 0)                 # pool inside the windows: nothing routed
+    sizes = [route_ws(cfg, L, n)[1] for L, n in [(1, 511), (1, 2047), (64, 2047), (64, 8191)]]
+    assert all(b > 0 for b in sizes) and sizes == sorted(sizes)
+    # one-row scores of every pool chunk are part of it: at least B*H*L*pool floats
+    assert sizes[1] >= 32 * 1 * (2047 - 10) * 4 and sizes[2] >= 32 * 64 * (2047 - 10) * 4
+    assert route_ws(cfg, 65, 100)[0] == -1                 # rows outside [1, 64]
+    # too small a workspace is refused before anything is launched
+    fake = ctypes.c_void_p(1 << 20)
+    need = route_ws(cfg, 4, 700)[1]
+    rc = lib.hga_route_decode(ctypes.byref(cfg), 4, 700, fake, 0, 0, 128, fake, 0, 0, fake, 0, 0,
+                              fake, fake, fake, fake, fake, fake, fake, need - 4, None)
+    assert rc == -1 and b"workspace" in lib.hga_last_error()
+
+    # backward: fp32 dk/dv accumulators, 2*B*KVH*S*Dh floats
+    for B, KVH, S, Dh in [(1, 4, 32768, 128), (2, 1, 77, 16)]:
+        c = cfg_of(B, 4 * KVH, KVH, Dh, 64, 16, 16, 64, 2, 8)
+        nb = ctypes.c_int64()
+        assert lib.hga_attend_prefill_bwd_workspace(ctypes.byref(c), S, ctypes.byref(nb)) == 0
+        assert nb.value == 2 * B * KVH * S * Dh * 4
+    c = cfg_of(1, 2, 1, 64, 128, 16, 1, 0, 1, 1, torch.float32)
+    args = [fake, 0, 0, 64] * 5
+    rc = lib.hga_attend_prefill_bwd(ctypes.byref(c), 256, *args, None, fake, fake, 0,
+                                    *([fake, 0, 0, 64] * 3), fake, 1 << 30, None)
+    assert rc == -2 and b"chunk_size" in lib.hga_last_error()
