@@ -81,6 +81,9 @@ def prefill_widths(cfg: HgaConfig, S: int):
 
 
 ROPE_STEPS_IN_DTYPE = 1
+# Longest routing pool (chunks) of a query chunk that hga_route_prefill takes: its stage-1 rows
+# hold 8 candidates per lane of a wave in registers.
+PREFILL_MAX_POOL = 512
 
 
 def rope(cfg: HgaConfig, x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor,

@@ -70,3 +70,4 @@ def test_cpu_forward_raises():
     ids = torch.randint(0, 96, (1, 12))
     with pytest.raises(RuntimeError, match="GPU"):
         model(input_ids=ids)
+
