@@ -925,18 +925,28 @@ typedef float floatx16_t __attribute__((ext_vector_type(16)));
 constexpr int kDMT = 128;   // threads: two waves of 32 rows
 constexpr int kDMK = 32;    // keys per tile
 
+// DCA (qwen_routed_attention.py:244-283): the three fp32 query versions (intra, successive,
+// inter DCA chunk) are each split into bf16 hi + lo parts (q = hi + lo to about 16 mantissa
+// bits) staged in LDS; a key's scores from the three versions are accumulated by two MFMAs per
+// step each and the key's regime picks one (a block's rows share one DCA chunk, so the regime is
+// a property of the key).
+constexpr int kDcaQStr(int DH) { return DH + 8; }
 template <int DH>
+constexpr size_t dca_q_lds_bytes() { return 2 * 3 * 2 * 64 * (size_t)kDcaQStr(DH); }
+
+template <int DH, bool DCA>
 __global__ __launch_bounds__(kDMT) void attend_decode_mfma_kernel(DecAttnArgs A, float* part,
                                                                   int nsplit) {
     typedef uint16_t T;
     constexpr int KS = DH / 16, DB = DH / 32, CPR = DH / 8;
-    constexpr int KSTR = DH + 8, VSTR = kDMK + 4;
+    constexpr int KSTR = DH + 8, VSTR = kDMK + 4, QSTR = kDcaQStr(DH);
     __shared__ __align__(16) uint16_t sK[kDMK * KSTR];
     __shared__ __align__(16) uint16_t sVt[DH * VSTR];
-    __shared__ int sOG[256], sOT[256];
+    __shared__ int sOG[256], sOT[256], sOP[DCA ? 256 : 1];
     __shared__ unsigned long long sKP[kSplitKeys], sVP[kSplitKeys];
-    __shared__ int sKT[kSplitKeys];
+    __shared__ int sKT[kSplitKeys], sKR[DCA ? kSplitKeys : 1];
     __shared__ int sNopen;
+    extern __shared__ __align__(16) uint16_t sQd[];   // DCA: [version][hi, lo][64 rows][QSTR]
     const int split = blockIdx.x, bh = blockIdx.y, b = bh / A.H, h = bh % A.H;
     const int kvh = h / (A.H / A.KVH);
     const int w = threadIdx.x / kWave, l = lane_id(), hl = l / 32;
@@ -948,29 +958,46 @@ __global__ __launch_bounds__(kDMT) void attend_decode_mfma_kernel(DecAttnArgs A,
         const int og = A.open_grp[(int64_t)bh * Kgw + i], ot = A.open_thr[(int64_t)bh * Kgw + i];
         sOG[i] = og;
         sOT[i] = ot;
+        if constexpr (DCA) sOP[i] = A.open_pos[(int64_t)bh * Kgw + i];
         if (og >= 0 && ot >= 0) atomicMax(&sNopen, i + 1);   // length of the opened list
     }
     __syncthreads();
     DecKeys<T> keys;
     keys.init(A, b, kvh, sOG, sOT, sNopen);
+    if constexpr (DCA) keys.sOP = sOP;
     for (int t = threadIdx.x; t < kSplitKeys; t += kDMT) {
         const int k = split * kSplitKeys + t;
         const T* kp = nullptr;
         const T* vp = nullptr;
         int thr = kNoRow;
-        if (k < keys.a4) keys.locate(k, kp, vp, thr);
+        int64_t kpos = 0;
+        if (k < keys.a4) keys.locate(k, kp, vp, thr, kpos);
         sKP[t] = (unsigned long long)kp;
         sVP[t] = (unsigned long long)vp;
         sKT[t] = kp ? thr : kNoRow;
+        if constexpr (DCA) sKR[t] = dca_regime(kpos, A.start_pos, A.dca_chunk);
     }
     // this lane's query row as MFMA B operands (8 dims of each 16-dim step)
-    const T* qg = reinterpret_cast<const T*>(A.q) + b * A.q_sb + h * A.q_sh;
     bf16x8_t qb[KS];
+    if constexpr (!DCA) {
+        const T* qg = reinterpret_cast<const T*>(A.q) + b * A.q_sb + h * A.q_sh;
 #pragma unroll
-    for (int s = 0; s < KS; ++s) {
-        uint4 u = make_uint4(0u, 0u, 0u, 0u);
-        if (row < A.L) u = *reinterpret_cast<const uint4*>(qg + (int64_t)row * A.q_ss + s * 16 + 8 * hl);
-        qb[s] = __builtin_bit_cast(bf16x8_t, u);
+        for (int s = 0; s < KS; ++s) {
+            uint4 u = make_uint4(0u, 0u, 0u, 0u);
+            if (row < A.L) u = *reinterpret_cast<const uint4*>(qg + (int64_t)row * A.q_ss + s * 16 + 8 * hl);
+            qb[s] = __builtin_bit_cast(bf16x8_t, u);
+        }
+    } else {
+        // fp32 rows of the three versions -> bf16 hi + lo parts in LDS (rows past L are zero)
+        for (int idx = threadIdx.x; idx < 3 * 64 * DH; idx += kDMT) {
+            const int v = idx / (64 * DH), r = (idx / DH) % 64, d = idx % DH;
+            float x = 0.0f;
+            if (r < A.L) x = A.q_dca[v][b * A.q_sb + h * A.q_sh + (int64_t)r * A.q_ss + d];
+            const uint16_t hi = f_to_bf16(x);
+            const uint16_t lo = f_to_bf16(x - bf16_to_f(hi));
+            sQd[((v * 2 + 0) * 64 + r) * QSTR + d] = hi;
+            sQd[((v * 2 + 1) * 64 + r) * QSTR + d] = lo;
+        }
     }
     __syncthreads();
     floatx16_t acc[DB];
@@ -1006,12 +1033,36 @@ __global__ __launch_bounds__(kDMT) void attend_decode_mfma_kernel(DecAttnArgs A,
         }
         __syncthreads();
         floatx16_t sc = {};
+        if constexpr (!DCA) {
 #pragma unroll
-        for (int s = 0; s < KS; ++s)
-            sc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
-                __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const uint4*>(
-                                                 &sK[(l % 32) * KSTR + s * 16 + 8 * hl])),
-                qb[s], sc, 0, 0, 0);
+            for (int s = 0; s < KS; ++s)
+                sc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+                    __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const uint4*>(
+                                                     &sK[(l % 32) * KSTR + s * 16 + 8 * hl])),
+                    qb[s], sc, 0, 0, 0);
+        } else {
+            floatx16_t sv[3] = {floatx16_t{}, floatx16_t{}, floatx16_t{}};
+#pragma unroll
+            for (int s = 0; s < KS; ++s) {
+                const bf16x8_t ka = __builtin_bit_cast(
+                    bf16x8_t, *reinterpret_cast<const uint4*>(&sK[(l % 32) * KSTR + s * 16 + 8 * hl]));
+#pragma unroll
+                for (int v = 0; v < 3; ++v)
+#pragma unroll
+                    for (int part = 0; part < 2; ++part)
+                        sv[v] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+                            ka,
+                            __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const uint4*>(
+                                &sQd[((v * 2 + part) * 64 + w * 32 + l % 32) * QSTR + s * 16 + 8 * hl])),
+                            sv[v], 0, 0, 0);
+            }
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const int kk = 8 * (i / 4) + 4 * hl + (i % 4);
+                const int rg = t0 + kk < nk ? sKR[t0 + kk] : 0;
+                sc[i] = rg == 0 ? sv[0][i] : (rg == 1 ? sv[1][i] : sv[2][i]);
+            }
+        }
         float mx = -INFINITY;
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
@@ -1566,12 +1617,22 @@ int attend_decode_impl(const hga_config* cfg, int32_t L, int32_t n_closed, int64
         float* part = static_cast<float*>(workspace);
         const dim3 g1((unsigned)nsplit, (unsigned)(a.B * a.H)), g2((unsigned)(a.B * a.H * L));
         // blocks of 8+ rows (bf16, aligned query rows): the MFMA split kernel
-        const bool mfma = cfg->dtype == HGA_DTYPE_BF16 && !dca && L >= 8 &&
-                          (uintptr_t)q % 16 == 0 && ((q_sb | q_sh | q_ss) % 8) == 0;
+        const bool mfma = cfg->dtype == HGA_DTYPE_BF16 && L >= 8 &&
+                          (dca || ((uintptr_t)q % 16 == 0 && ((q_sb | q_sh | q_ss) % 8) == 0));
 #define HGA_DS_CASE(DTV, DHV)                                                                    \
         if (cfg->dtype == DTV && D == DHV) {                                                   \
-            if (mfma && DTV == HGA_DTYPE_BF16)                                                  \
-                attend_decode_mfma_kernel<DHV><<<g1, kDMT, 0, st>>>(a, part, nsplit);           \
+            if (mfma && DTV == HGA_DTYPE_BF16 && dca) {                                         \
+                static bool attr = false;                                                       \
+                if (!attr) {                                                                    \
+                    (void)hipFuncSetAttribute((const void*)attend_decode_mfma_kernel<DHV, true>, \
+                                              hipFuncAttributeMaxDynamicSharedMemorySize,       \
+                                              (int)dca_q_lds_bytes<DHV>());                     \
+                    attr = true;                                                                \
+                }                                                                               \
+                attend_decode_mfma_kernel<DHV, true><<<g1, kDMT, dca_q_lds_bytes<DHV>(), st>>>(  \
+                    a, part, nsplit);                                                           \
+            } else if (mfma && DTV == HGA_DTYPE_BF16)                                           \
+                attend_decode_mfma_kernel<DHV, false><<<g1, kDMT, 0, st>>>(a, part, nsplit);    \
             else if (dca) attend_decode_split_kernel<DTV, DHV, true><<<g1, kDT, 0, st>>>(a, part, nsplit); \
             else attend_decode_split_kernel<DTV, DHV, false><<<g1, kDT, 0, st>>>(a, part, nsplit); \
             rc = launch_status("hga_attend_decode (split)");                                    \
