@@ -282,20 +282,21 @@ __global__ __launch_bounds__(kDT) void route_decode_part_kernel(DecRouteArgs A) 
     windows(A.n_closed, A.kf, A.kl, &f_hi, &l_lo);
     const int nmid = l_lo > f_hi ? l_lo - f_hi : 0;
     const int s0 = sg * A.seg, sl = min(A.seg, nmid - s0);   // s0 < nmid (host grid)
-    load_q_f32<DT, DH>(A, b, h, sQ, kDT);
+    const int NT = (int)blockDim.x;                              // 64 (L <= 4) or 256 threads
+    load_q_f32<DT, DH>(A, b, h, sQ, NT);
     __syncthreads();
     const T* ckb = reinterpret_cast<const T*>(A.ck) + b * A.ck_sb + kvh * A.ck_sh +
                    (int64_t)(f_hi + s0) * DH;
     float* srow = A.ws + (int64_t)bh * L * A.SPW + s0;
     {
-        const int RG = score_row_groups(L), KP = kDT / RG, rg = threadIdx.x / KP;
+        const int RG = score_row_groups(L), KP = NT / RG, rg = threadIdx.x / KP;
         const int rpg = (L + RG - 1) / RG, r0 = min(L, rg * rpg), r1 = min(L, r0 + rpg);
         // a one-row block needs only the pooled score (its rows request the whole selection)
         for (int i = threadIdx.x % KP; i < sl; i += KP)
             sPool[rg * A.seg + i] = score_key_rows<DT, DH>(
                 sQ, r0, r1, ckb + (int64_t)i * DH, L == 1 ? sPool + i : srow + i, A.SPW, A.scale);
         __syncthreads();
-        for (int i = threadIdx.x; i < sl; i += kDT) {          // pooled over all rows (:227)
+        for (int i = threadIdx.x; i < sl; i += NT) {           // pooled over all rows (:227)
             float m = sPool[i];
             for (int g = 1; g < RG; ++g) m = fmaxf(m, sPool[g * A.seg + i]);
             sPool[i] = m;
@@ -457,8 +458,28 @@ __global__ __launch_bounds__(kDT) void route_decode_kernel(DecRouteArgs A) {
     const int nop = sScal[2];
     for (int i = threadIdx.x; i < nop; i += kDT) sFirst[i] = kNoRow;
     __syncthreads();
-    // each row requests its own top-Kgr groups (:266); first requesting row by rank
-    for (int r = w; r < L; r += kDW) {
+    // each row requests its own top-Kgr groups (:266); first requesting row by rank -- a one-row
+    // block's requests are its top-Kgr, one selection over the candidates
+    if (L == 1 && w == 0) {
+        dispatch_j<kDecJ>(T2, [&](auto jt) {
+            constexpr int J = decltype(jt)::value;
+            const uint32_t req = topk_lds<J>(sS, T2, A.Kgr);
+            // opened candidates are ascending: find each requested candidate's opened slot
+#pragma unroll
+            for (int j = 0; j < J; ++j)
+                if ((req >> j) & 1u) {
+                    const int c = l + 64 * j;
+                    int lo = 0, hi = nop;
+                    while (lo < hi) {
+                        const int mid = (lo + hi) >> 1;
+                        if (sOp[mid] < c) lo = mid + 1;
+                        else hi = mid;
+                    }
+                    if (lo < nop && sOp[lo] == c) sFirst[lo] = 0;
+                }
+        });
+    }
+    for (int r = L == 1 ? L : w; r < L; r += kDW) {
         const float* row = sS + r * SPD;
         for (int o0 = 0; o0 < nop; o0 += kWave) {
             const int o = o0 + l;
@@ -1514,8 +1535,8 @@ extern "C" int hga_route_decode(const hga_config* cfg, int32_t L, int32_t n_clos
             attr = true;                                                                        \
         }                                                                                       \
         if (a.Kc > 0) {                                                                         \
-            route_decode_part_kernel<DTV, DHV><<<dim3((unsigned)sg.nseg, grid), kDT, sg.lds,   \
-                                                 st>>>(a);                                      \
+            route_decode_part_kernel<DTV, DHV><<<dim3((unsigned)sg.nseg, grid),               \
+                                                 L <= 4 ? kWave : kDT, sg.lds, st>>>(a);        \
             rc = launch_status("hga_route_decode");                                             \
             if (rc) return rc;                                                                  \
         }                                                                                       \
