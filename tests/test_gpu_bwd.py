@@ -121,6 +121,36 @@ def test_forward_lse_is_logsumexp(shape):
     np.testing.assert_allclose(lse.cpu().numpy(), ref, atol=1e-3, rtol=1e-5)
 
 
+def test_attend_prefill_bwd_unaligned_rows_take_valu_kernel():
+    """bf16 head_dim 128 rows that are not 16-byte aligned take the VALU backward kernel; its
+    gradients match the oracle like the MFMA kernel's."""
+    B, H, KVH, S, Dh, C, gs, kf, kl, Kg, dt = 1, 4, 2, 200, 128, 64, 16, 1, 1, 6, torch.bfloat16
+    rng = np.random.default_rng(7)
+    q = oracle.bf16_round(rng.standard_normal((B, H, S, Dh)).astype(np.float32))
+    k = oracle.bf16_round(rng.standard_normal((B, KVH, S, Dh)).astype(np.float32))
+    v = oracle.bf16_round(rng.standard_normal((B, KVH, S, Dh)).astype(np.float32))
+    dout = oracle.bf16_round(rng.standard_normal((B, H, S, Dh)).astype(np.float32))
+    og, ot = random_lists(rng, B, H, S, C, gs, kf, kl, Kg)
+    cfg = _cfg(B, H, KVH, Dh, C, gs, kf, kl, Kg, dt)
+    _, _, Kgc = ops.prefill_widths(cfg, S)
+    og, ot = og[..., :max(Kgc, 1)], ot[..., :max(Kgc, 1)]
+    T = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(DEV, dt)
+    I = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(DEV)
+    qd, kd, vd = T(q), T(k), T(v)
+    out = ops.attend_prefill(cfg, qd, kd, vd, I(og), I(ot), Kgc)
+    # the same q values one element into a larger buffer: rows 2 bytes off 16-byte alignment
+    buf = torch.empty(qd.numel() + 8, dtype=dt, device=DEV)
+    qu = buf[1:1 + qd.numel()].view(B, H, S, Dh)
+    qu.copy_(qd)
+    assert qu.data_ptr() % 16 != 0
+    dq, dk, dv = ops.attend_prefill_bwd(cfg, qu, kd, vd, out, T(dout), I(og), I(ot), Kgc)
+    torch.cuda.synchronize()
+    rq, rk, rv = oracle.attend_prefill_bwd(q, k, v, dout, C, gs, kf, kl, og, ot,
+                                           oracle.attn_scale(Dh))
+    for a, ref, what in ((dq, rq, "dq"), (dk, rk, "dk"), (dv, rv, "dv")):
+        _check(a, ref, dt, what)
+
+
 def test_attend_prefill_bwd_rejects_wide_chunks():
     cfg = _cfg(1, 2, 1, 64, 128, 16, 1, 1, 0, torch.float32)
     q = torch.zeros(1, 2, 256, 64, device=DEV)
