@@ -287,7 +287,7 @@ __global__ __launch_bounds__(kDT) void route_decode_part_kernel(DecRouteArgs A) 
     __syncthreads();
     const T* ckb = reinterpret_cast<const T*>(A.ck) + b * A.ck_sb + kvh * A.ck_sh +
                    (int64_t)(f_hi + s0) * DH;
-    float* srow = A.ws + (int64_t)bh * L * A.SPW + s0;
+    float* srow = L > 1 ? A.ws + (int64_t)bh * L * A.SPW + s0 : nullptr;
     {
         const int RG = score_row_groups(L), KP = NT / RG, rg = threadIdx.x / KP;
         const int rpg = (L + RG - 1) / RG, r0 = min(L, rg * rpg), r1 = min(L, r0 + rpg);
@@ -1451,9 +1451,10 @@ extern "C" int hga_route_decode_workspace(const hga_config* cfg, int32_t L, int3
         rc = dec_segments(cfg, L, nmid, Kc, &sg);
         if (rc) return rc;
     }
-    // stage-1 scores of every row, then per (b, h, segment) Kc pooled values and chunk offsets
-    *bytes = Kc > 0 ? (int64_t)cfg->batch * cfg->heads * ((int64_t)L * nmid * 4 + sg.nseg * Kc * 8)
-                    : 0;
+    // stage-1 scores of every row (blocks of 2+ rows: their rank counts read them), then per
+    // (b, h, segment) Kc pooled values and chunk offsets
+    const int64_t score_bytes = L > 1 ? (int64_t)L * nmid * 4 : 0;
+    *bytes = Kc > 0 ? (int64_t)cfg->batch * cfg->heads * (score_bytes + sg.nseg * Kc * 8) : 0;
     return HGA_OK;
 }
 
@@ -1502,8 +1503,8 @@ extern "C" int hga_route_decode(const hga_config* cfg, int32_t L, int32_t n_clos
         a.seg = sg.seg;
         a.nseg = sg.nseg;
         a.SPW = nmid;
-        a.ws = (float*)workspace;
-        a.wv = a.ws + (int64_t)a.B * a.H * L * nmid;
+        a.ws = L > 1 ? (float*)workspace : nullptr;
+        a.wv = (float*)workspace + (L > 1 ? (int64_t)a.B * a.H * L * nmid : 0);
         a.wi = (int32_t*)(a.wv + (int64_t)a.B * a.H * sg.nseg * a.Kc);
     }
     // merge kernel LDS: sQ [L][D] | sS [L][SPD] | sPool, sFirst [SPD] | sSel, sThr [64] |

@@ -96,8 +96,8 @@ def test_workspace_queries_and_checks_without_launch():
     assert route_ws(cfg, 1, 10) == (0, 0)                 # pool inside the windows: nothing routed
     sizes = [route_ws(cfg, L, n)[1] for L, n in [(1, 511), (1, 2047), (64, 2047), (64, 8191)]]
     assert all(b > 0 for b in sizes) and sizes == sorted(sizes)
-    # one-row scores of every pool chunk are part of it: at least B*H*L*pool floats
-    assert sizes[1] >= 32 * 1 * (2047 - 10) * 4 and sizes[2] >= 32 * 64 * (2047 - 10) * 4
+    # a multi-row block's scores of every pool chunk are part of it: at least B*H*L*pool floats
+    assert sizes[2] >= 32 * 64 * (2047 - 10) * 4 > 2 * sizes[1]
     assert route_ws(cfg, 65, 100)[0] == -1                 # rows outside [1, 64]
     # too small a workspace is refused before anything is launched
     fake = ctypes.c_void_p(1 << 20)
