@@ -5,8 +5,10 @@ this package.  The product path (``hierarchicalglobalattention_amd``) never does
 
 ``hga_oracle.c`` is a single-threaded C restatement of the reference's prefill path
 (``ExistingModelFineTuning/KvRouter/vectorized.py:189-492`` + ``chunk_router.py:139-162``) and
-decode path (``chunk_router.py:187-407``), with the canonical score/tie rules documented at the
-top of that file.  This module wraps it for numpy float32 arrays (bf16 tensors are passed as
+decode path (``chunk_router.py:187-407``), the Dual Chunk Attention decode
+(``qwen_routed_attention.py:244-283``) and the gradient of the prefill attention (what autograd
+computes through ``HierarchicalGlobalAttentionRouted.py:137-177``), with the canonical score/tie
+rules documented at the top of that file.  This module wraps it for numpy float32 arrays (bf16 tensors are passed as
 float32 arrays holding bf16-representable values) and restates the small host-side formulas
 (cutoff pair, window ranges) independently of the product package.
 

@@ -20,9 +20,11 @@
  *   Masked candidates (fill -1e4 in the reference) never outrank a real score; this assumes
  *   |score| < 1e4, which holds for any normalised activations.
  *
- * Parity pins: tests/test_oracle_golden.py compares every function here against fixtures
- * written by the reference itself (tests/golden/make_golden.py), and tests/test_oracle_props.py
- * against closed forms and invariants.
+ * Parity pins: tests/test_oracle_golden.py compares the routing, summary and attention
+ * functions here against fixtures written by the reference itself (tests/golden/make_golden.py),
+ * tests/test_oracle_props.py against closed forms and invariants, tests/test_oracle_dca.py the
+ * Dual Chunk Attention decode against dense DCA, and tests/test_oracle_bwd.py the attention
+ * gradient against float64 autograd of the masked dense attention.
  */
 #include <math.h>
 #include <stdint.h>
