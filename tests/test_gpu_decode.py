@@ -176,6 +176,9 @@ ROUTE_CASES = [
     (1, 4, 2, 128, 64, 16, 16, 64, 2, 8, 2047, 64, torch.bfloat16),   # 128K context, 64-row block
     (1, 4, 2, 128, 64, 16, 64, 256, 2, 8, 1200, 64, torch.float32),   # Kc 64, fp32: short segments
     (1, 4, 2, 64, 64, 16, 4, 64, 0, 0, 1300, 2, torch.float32),       # forced previous, long pool
+    (1, 2, 1, 128, 64, 16, 16, 64, 2, 8, 8191, 64, torch.bfloat16),   # 64 rows, 512K: merge of 2048
+    (1, 4, 2, 64, 64, 16, 16, 64, 2, 8, 650, 16, torch.bfloat16),     # pool = 10 whole 64-segments
+    (1, 4, 2, 64, 64, 16, 40, 160, 0, 3, 300, 5, torch.float32),      # 5 rows, Kc 40, one segment
 ]
 
 
