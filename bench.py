@@ -184,6 +184,50 @@ def run_gpu(args):
                 route_bytes=route_bytes, score_flops=score_flops, backward=bwd)
 
 
+def run_c2(reps: int = 5, warmup: int = 2):
+    """the 40M-class stack, 8 HGA attention layers (d_model 512, 8 query
+    heads, 2 KV heads, head_dim 64, chunk 64, group 16, keep_first 2, keep_last 8, topk_chunks 16,
+    topk_groups 64, bf16, projections ~ N(0, 0.02)), prefill of 8192 tokens with inputs ~ N(0,1),
+    each layer's output feeding the next.  Times the layers' forward (projections, RoPE, router,
+    attention, o_proj); the model's MLPs, norms and embeddings are not part of the path."""
+    import hierarchicalglobalattention_amd as hga
+    dev = torch.device("cuda:0")
+    torch.manual_seed(0)
+    layers = []
+    for i in range(8):
+        m = hga.HierarchicalGlobalAttentionRouted(d_model=512, nhead=8, kv_heads=2, chunk_size=64,
+                                                  group_size=16, topk_chunks=16, topk_groups=64,
+                                                  keep_first=2, keep_last=8, theta=1e4,
+                                                  layer_idx=i)
+        for prm in m.parameters():
+            torch.nn.init.normal_(prm, std=0.02)
+        layers.append(m.to(dev, torch.bfloat16).eval())
+    x0 = torch.randn(1, 8192, 512, device=dev, dtype=torch.bfloat16)
+
+    def stack():
+        x = x0
+        for m in layers:
+            x, _ = m(hidden_states=x)
+        return x
+
+    with torch.no_grad():
+        for _ in range(warmup):
+            stack()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            out = stack()
+        e1.record()
+        torch.cuda.synchronize()
+    assert torch.isfinite(out.float()).all()
+    ms = e0.elapsed_time(e1) / reps
+    return dict(layers=8, seq_len=8192, ms_per_stack=ms, ms_per_layer=ms / 8,
+                tokens_per_s=8192 / (ms * 1e-3),
+                note="8 attention layers (projections + routed attention); the reference's "
+                     "published 40M figure times the whole model on other hardware")
+
+
 def copy_calibration(nbytes: int = 1 << 30, reps: int = 3):
     """A plain device copy of known size, for scaling the FETCH_SIZE / WRITE_SIZE counters."""
     dev = torch.device("cuda:0")
@@ -338,6 +382,7 @@ def main():
     ap.add_argument("--cpu-budget", type=float, default=15.0)
     ap.add_argument("--no-decode", action="store_true", help="skip the decode legs (c4, c5)")
     ap.add_argument("--no-backward", action="store_true", help="skip the attention backward leg")
+    ap.add_argument("--no-c2", action="store_true", help="skip the 40M 8-layer prefill leg")
     ap.add_argument("--decode-steps", type=int, default=256)
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run only a 1 GiB device copy (scales the HBM byte counters)")
@@ -381,6 +426,7 @@ def main():
                                                     steps=max(ds // 8, 4), warmup=4, block=64),
         }
         torch.cuda.empty_cache()
+    c2 = None if args.no_c2 else run_c2()
     cpu = None
     if not args.no_cpu:
         cpu = cpu_baseline(args.cpu_budget)
@@ -412,6 +458,7 @@ def main():
                                "algorithmic_flops": g["flops"], "visible_qk_pairs": g["pairs"]},
         "decode": dec,
         "backward": g["backward"],
+        "c2_40m_8layer_prefill_8k": c2,
         "cpu_baseline": cpu,
         "host": {"cpu": platform.processor() or platform.machine(), "torch": torch.__version__},
     }
