@@ -68,6 +68,7 @@ SIGNATURES = {
                                  ctypes.POINTER(ctypes.c_int64)], _i32),
     "hga_gather_decode": ([_CFG, _i32, _vp, _vp, _i32, _vp, _vp, _i64, _i64, _i64, _i32, _vp,
                            _vp, _i32, _vp, _vp, _i64, _vp], ctypes.c_int),
+    "hga_write_tokens": ([_CFG, _i32] + [_vp, _i64, _i64, _i64] * 6 + [_vp], ctypes.c_int),
 }
 
 _lib = None

@@ -363,6 +363,34 @@ def gather_decode(cfg: HgaConfig, n_closed: int, open_grp: torch.Tensor, open_th
     return sk, sv, sg
 
 
+def write_tokens(cfg: HgaConfig, L: int, pairs) -> None:
+    """One launch copying up to three (src, dst) row sets, each a [B, KVH, L, Dh] view of
+    cfg's dtype with a contiguous last dim: a decode block's RoPE'd keys, values and raw keys
+    into the token record or ring and the active-chunk buffer.  A pair may be None."""
+    pairs = list(pairs)
+    if len(pairs) > 3:
+        raise ValueError("write_tokens takes at most three row sets")
+    want = (cfg.batch, cfg.kv_heads, L, cfg.head_dim)
+    src_args, dst_args = [], []
+    for pr in pairs + [None] * (3 - len(pairs)):
+        if pr is None:
+            src_args += [ctypes.c_void_p(0), 0, 0, 0]
+            dst_args += [ctypes.c_void_p(0), 0, 0, 0]
+            continue
+        src, dst = pr
+        _dev(src, dst)
+        if tuple(src.shape) != want or tuple(dst.shape) != want:
+            raise ValueError(f"write_tokens: rows {tuple(src.shape)} -> {tuple(dst.shape)}, "
+                             f"expected {want}")
+        if src.dtype != dst.dtype or _DT.get(src.dtype) != cfg.dtype:
+            raise TypeError(f"write_tokens: {src.dtype} -> {dst.dtype} under a config of "
+                            f"another dtype")
+        src_args += [_p(src), *_s4(src)]
+        dst_args += [_p(dst), *_s4(dst)]
+    check(lib().hga_write_tokens(ctypes.byref(cfg), L, *src_args, *dst_args, _stream()),
+          "hga_write_tokens")
+
+
 def attend_decode(cfg: HgaConfig, q: torch.Tensor, n_closed: int, start_pos: int,
                   recent_k: torch.Tensor, recent_v: torch.Tensor, ring_chunks: int,
                   first_k, first_v, record_k, record_v, record_on_host: bool,

@@ -182,11 +182,15 @@ class VramKVCacheStore(_StoreBase):
     def _record_len(self, st):
         return st.cap * self.C
 
-    def write_tokens(self, layer: int, pos: int, k_rope, v) -> None:
+    def token_rows(self, layer: int, pos: int, L: int):
+        """Device views [B, KVH, L, Dh] that tokens pos..pos+L-1 (one active chunk) go to."""
         st = self.layer(layer)
-        L = k_rope.shape[2]
-        st.tok_k[:, :, pos:pos + L] = k_rope
-        st.tok_v[:, :, pos:pos + L] = v
+        return st.tok_k[:, :, pos:pos + L], st.tok_v[:, :, pos:pos + L]
+
+    def write_tokens(self, layer: int, pos: int, k_rope, v) -> None:
+        kd, vd = self.token_rows(layer, pos, k_rope.shape[2])
+        kd.copy_(k_rope)
+        vd.copy_(v)
 
     def close_chunk(self, layer: int, n: int) -> None:
         pass
@@ -259,14 +263,18 @@ class RamKVCacheStore(_StoreBase):
         super().prepare_block(layer, first_chunk, last_chunk)
         self._ensure_hot(self.layer(layer), last_chunk - first_chunk + 1)
 
-    def write_tokens(self, layer: int, pos: int, k_rope, v) -> None:
+    def token_rows(self, layer: int, pos: int, L: int):
+        """Ring views [B, KVH, L, Dh] that tokens pos..pos+L-1 (one active chunk) go to."""
         st = self.layer(layer)
         self._ensure_hot(st)
         C = self.C
         s = self._ring_slot(st, pos // C) * C + pos % C
-        L = k_rope.shape[2]
-        st.ring_k[:, :, s:s + L] = k_rope
-        st.ring_v[:, :, s:s + L] = v
+        return st.ring_k[:, :, s:s + L], st.ring_v[:, :, s:s + L]
+
+    def write_tokens(self, layer: int, pos: int, k_rope, v) -> None:
+        kd, vd = self.token_rows(layer, pos, k_rope.shape[2])
+        kd.copy_(k_rope)
+        vd.copy_(v)
 
     def close_chunk(self, layer: int, n: int) -> None:
         """Chunk n left the active slot: copy it to the host record (async D2H into pinned
@@ -648,9 +656,9 @@ class ChunkRouter:
         n_closed = st.n_closed
         assert n_closed == n, f"active chunk {n} != closed {n_closed}; out-of-order block"
         st = self.store.ensure_capacity(layer, n_closed + 1)
-        self.store.write_tokens(layer, start_pos, k_rope, v)
-        st.act_kraw[:, :, c0:c0 + L] = k_raw
         hc = self.hcfg(B, q.dtype)
+        kd, vd = self.store.token_rows(layer, start_pos, L)
+        ops.write_tokens(hc, L, [(k_rope, kd), (v, vd), (k_raw, st.act_kraw[:, :, c0:c0 + L])])
         if n_closed > 0:
             routing = ops.route_decode(hc, q, st.chunk_k, st.group_k, n_closed)
         else:

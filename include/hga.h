@@ -268,6 +268,22 @@ int hga_attend_decode_dca(const hga_config* cfg, int32_t L, int32_t n_closed,
 int32_t hga_attend_decode_workspace(const hga_config* cfg, int32_t L, int32_t n_closed,
                                     int64_t start_pos, int32_t Kg, int64_t* bytes);
 
+/*
+ * Decode token ingest (chunk_router.py:317 decode_block -> _append_active, :603-614, together
+ * with the store's token write): up to three row sets of [B, KVH, L, head_dim] rows of cfg's
+ * dtype, each copied from src to dst in one launch: the block's RoPE'd keys and its values into
+ * the token record or ring, its raw keys into the active-chunk buffer.  Each set gives element
+ * strides (batch, KV head, row) with a contiguous head dim, rows 16-byte aligned; a set with both
+ * pointers NULL is skipped.  Offsets are 64-bit, so the rows may lie anywhere in a record of any
+ * size.
+ */
+int hga_write_tokens(const hga_config* cfg, int32_t L, const void* k, int64_t k_sb, int64_t k_sh,
+                     int64_t k_ss, const void* v, int64_t v_sb, int64_t v_sh, int64_t v_ss,
+                     const void* k_raw, int64_t r_sb, int64_t r_sh, int64_t r_ss, void* dst_k,
+                     int64_t dk_sb, int64_t dk_sh, int64_t dk_ss, void* dst_v, int64_t dv_sb,
+                     int64_t dv_sh, int64_t dv_ss, void* dst_raw, int64_t dr_sb, int64_t dr_sh,
+                     int64_t dr_ss, void* stream);
+
 /* Sizes for hga_gather_decode: staging capacity per (batch, KV head) in groups (rep * Kg, the
  * most distinct groups the rep query heads can open), bytes of each of the K and V staging
  * buffers ([B, KVH, stage_groups, group_size, head_dim]) and bytes of the int32 scratch. */

@@ -117,3 +117,30 @@ def test_workspace_queries_and_checks_without_launch():
     rc = lib.hga_attend_prefill_bwd(ctypes.byref(c), 256, *args, None, fake, fake, 0,
                                     *([fake, 0, 0, 64] * 3), fake, 1 << 30, None)
     assert rc == -2 and b"chunk_size" in lib.hga_last_error()
+
+
+def test_write_tokens_checks_without_launch():
+    """hga_write_tokens refuses a half-given row set, unaligned rows and negative counts before
+    launching; an empty block or no row set at all is a no-op."""
+    import torch
+    lib = _lib.lib()
+    cfg = ops.make_config(batch=1, heads=8, kv_heads=2, head_dim=64, chunk_size=64,
+                          group_size=16, topk_chunks=4, topk_groups=8, keep_first=1,
+                          keep_last=2, cutoff_pair=3, dtype=torch.bfloat16)
+    fake, odd, z = ctypes.c_void_p(1 << 20), ctypes.c_void_p((1 << 20) + 8), ctypes.c_void_p(0)
+    good = [fake, 128 * 64, 64 * 64, 64]
+
+    def call(L, sets):
+        args = [a for s in sets for a in s[0]] + [a for s in sets for a in s[1]]
+        return lib.hga_write_tokens(ctypes.byref(cfg), L, *args, None)
+
+    none = [z, 0, 0, 0]
+    assert call(4, [(none, none)] * 3) == 0                       # nothing to copy
+    assert call(0, [(good, good)] * 3) == 0                        # empty block
+    assert call(-1, [(good, good)] * 3) == -1
+    rc = call(4, [(good, none), (none, none), (none, none)])
+    assert rc == -1 and b"half given" in lib.hga_last_error()
+    rc = call(4, [(good, good), (good, [odd, 128 * 64, 64 * 64, 64]), (none, none)])
+    assert rc == -1 and b"aligned" in lib.hga_last_error()
+    rc = call(4, [(good, [fake, 128 * 64, 64 * 64, 68]), (none, none), (none, none)])
+    assert rc == -1 and b"aligned" in lib.hga_last_error()

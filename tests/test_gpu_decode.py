@@ -385,3 +385,72 @@ def test_attend_decode_rejects_bad_blocks():
         ops.attend_decode(cfg, q, 1, 64 + 63, kv, kv, 0, kv, kv, kv, kv, False, e, e, 0)
     with pytest.raises(hga.HgaError, match="ring"):
         ops.attend_decode(cfg, q, 3, 3 * 64, kv, kv, 1, kv, kv, kv, kv, False, e, e, 0)
+
+
+# ----------------------------------------------------------------------------------------------
+# token ingest: hga_write_tokens against torch's copies
+# ----------------------------------------------------------------------------------------------
+def _wcfg(B, KVH, Dh, dt):
+    return ops.make_config(batch=B, heads=2 * KVH, kv_heads=KVH, head_dim=Dh, chunk_size=64,
+                           group_size=16, topk_chunks=4, topk_groups=8, keep_first=1, keep_last=2,
+                           cutoff_pair=3, dtype=dt)
+
+
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("L", [1, 7, 64])
+def test_write_tokens_matches_copies(dt, L):
+    """Strided sources (a [B, L, KVH, Dh] tensor seen as [B, KVH, L, Dh]) land bit-exactly in a
+    record slice, a ring slice and an active-chunk slice; every other element stays as it was."""
+    B, KVH, Dh = 2, 3, 64
+    g = torch.Generator(device=DEV).manual_seed(11 + L)
+    srcs = [torch.randn(B, L, KVH, Dh, generator=g, device=DEV).to(dt).transpose(1, 2)
+            for _ in range(3)]
+    rec = torch.randn(B, KVH, 300, Dh, generator=g, device=DEV).to(dt)
+    ring = torch.randn(B, KVH, 192, Dh, generator=g, device=DEV).to(dt)
+    act = torch.randn(B, KVH, 64, Dh, generator=g, device=DEV).to(dt)
+    want = [t.clone() for t in (rec, ring, act)]
+    p, s, c0 = 130, 64, 64 - L
+    for w, src, a in zip(want, srcs, (p, s, c0)):
+        w[:, :, a:a + L] = src
+    ops.write_tokens(_wcfg(B, KVH, Dh, dt), L, [(srcs[0], rec[:, :, p:p + L]),
+                                                (srcs[1], ring[:, :, s:s + L]),
+                                                (srcs[2], act[:, :, c0:c0 + L])])
+    torch.cuda.synchronize()
+    for got, w in zip((rec, ring, act), want):
+        assert torch.equal(got, w)
+
+
+def test_write_tokens_past_2g_elements_and_skipped_sets():
+    """Rows beyond element 2^31 of a record are addressed exactly (64-bit offsets), and a row set
+    given as None is left out."""
+    Dh, L = 64, 5
+    rows = (1 << 31) // Dh + 96
+    rec = torch.empty(1, 1, rows, Dh, dtype=torch.bfloat16, device=DEV)
+    try:
+        g = torch.Generator(device=DEV).manual_seed(3)
+        k = torch.randn(1, 1, L, Dh, generator=g, device=DEV).to(torch.bfloat16)
+        raw = torch.randn(1, 1, L, Dh, generator=g, device=DEV).to(torch.bfloat16)
+        act = torch.zeros(1, 1, 64, Dh, dtype=torch.bfloat16, device=DEV)
+        pos = rows - 40
+        before = rec[:, :, pos - 8:pos].clone()
+        ops.write_tokens(_wcfg(1, 1, Dh, torch.bfloat16), L,
+                         [(k, rec[:, :, pos:pos + L]), None, (raw, act[:, :, 3:3 + L])])
+        torch.cuda.synchronize()
+        assert torch.equal(rec[:, :, pos:pos + L], k)
+        assert torch.equal(rec[:, :, pos - 8:pos], before)
+        assert torch.equal(act[:, :, 3:3 + L], raw)
+        assert not act[:, :, :3].any() and not act[:, :, 3 + L:].any()
+    finally:
+        del rec
+        torch.cuda.empty_cache()
+
+
+def test_write_tokens_rejects_mismatches():
+    cfg = _wcfg(1, 2, 64, torch.bfloat16)
+    a = torch.zeros(1, 2, 4, 64, dtype=torch.bfloat16, device=DEV)
+    with pytest.raises(TypeError):
+        ops.write_tokens(cfg, 4, [(a.float(), a.float())])
+    with pytest.raises(ValueError):
+        ops.write_tokens(cfg, 3, [(a, a)])
+    with pytest.raises(RuntimeError):
+        ops.write_tokens(cfg, 4, [(a.cpu(), a)])
