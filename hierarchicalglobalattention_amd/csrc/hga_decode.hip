@@ -30,6 +30,21 @@ constexpr int kMaxL = 64;
 constexpr int kDecJ = 32;            // wave selections over <= 2048 candidates
 constexpr int kDecSegJ = 32;         // stage-1 segment: <= 64 * kDecSegJ chunks
 
+// Work item (inner, outer) of the calling workgroup in a grid (inner, outer) whose outer index
+// runs over (batch, query head).  Workgroups go to the 8 XCDs round-robin by linear id and each
+// XCD has its own L2; when the inner count is not a multiple of 8, adjacent heads (those sharing
+// a KV head, which read the same summaries and window keys) would land on different XCDs, so the
+// linear id is permuted to give XCD k the contiguous item range [k n/8, (k+1) n/8).  Otherwise
+// (inner count a multiple of 8: each inner index of every head already stays on one XCD, or
+// n not a multiple of 8) the identity is kept.  A bijection on [0, n) either way.
+__device__ __forceinline__ void xcd_item(int& inner, int& outer) {
+    const int64_t ni = gridDim.x, n = ni * gridDim.y;
+    int64_t x = blockIdx.x + ni * blockIdx.y;
+    if ((ni & 7) != 0 && (n & 7) == 0) x = (x & 7) * (n >> 3) + (x >> 3);
+    inner = (int)(x % ni);
+    outer = (int)(x / ni);
+}
+
 struct DecRouteArgs {
     const void* q;
     int64_t q_sb, q_sh, q_ss;
@@ -276,7 +291,9 @@ __global__ __launch_bounds__(kDT) void route_decode_part_kernel(DecRouteArgs A) 
     const int L = A.L, K = A.Kc;
     float* sQ = reinterpret_cast<float*>(smem_raw);             // [L][DH] fp32
     float* sPool = sQ + L * DH;                                 // [RG][seg] partial maxima
-    const int sg = blockIdx.x, bh = blockIdx.y, b = bh / A.H, h = bh % A.H;
+    int sg, bh;
+    xcd_item(sg, bh);
+    const int b = bh / A.H, h = bh % A.H;
     const int kvh = h / (A.H / A.KVH);
     int f_hi, l_lo;
     windows(A.n_closed, A.kf, A.kl, &f_hi, &l_lo);
@@ -327,7 +344,9 @@ __global__ __launch_bounds__(kDT) void route_decode_kernel(DecRouteArgs A) {
     int* sOp = sScal + 8;                                       // [256] opened candidates
     int* sPI = sOp + 256;                                       // [Kc] pooled selection ids
 
-    const int bh = blockIdx.x, b = bh / A.H, h = bh % A.H, kvh = h / (A.H / A.KVH);
+    int one, bh;
+    xcd_item(one, bh);   // grid (1, B*H)
+    const int b = bh / A.H, h = bh % A.H, kvh = h / (A.H / A.KVH);
     const int w = threadIdx.x / kWave, l = lane_id();
     int f_hi, l_lo;
     windows(A.n_closed, A.kf, A.kl, &f_hi, &l_lo);
@@ -808,7 +827,9 @@ __global__ __launch_bounds__(kDT) void attend_decode_split_kernel(DecAttnArgs A,
     __shared__ unsigned long long sKP[kSplitKeys], sVP[kSplitKeys];
     __shared__ int sKT[kSplitKeys], sKX[DCA ? kSplitKeys : 1];
     __shared__ int sNopen;
-    const int split = blockIdx.x, bh = blockIdx.y, b = bh / A.H, h = bh % A.H;
+    int split, bh;
+    xcd_item(split, bh);
+    const int b = bh / A.H, h = bh % A.H;
     const int kvh = h / (A.H / A.KVH);
     const int l = lane_id(), j = l & 15, G = (int)(threadIdx.x >> 4);
     const int Kgw = A.Kg > 0 ? A.Kg : 1;
@@ -968,7 +989,9 @@ __global__ __launch_bounds__(kDMT) void attend_decode_mfma_kernel(DecAttnArgs A,
     __shared__ int sKT[kSplitKeys], sKR[DCA ? kSplitKeys : 1];
     __shared__ int sNopen;
     extern __shared__ __align__(16) uint16_t sQd[];   // DCA: [version][hi, lo][64 rows][QSTR]
-    const int split = blockIdx.x, bh = blockIdx.y, b = bh / A.H, h = bh % A.H;
+    int split, bh;
+    xcd_item(split, bh);
+    const int b = bh / A.H, h = bh % A.H;
     const int kvh = h / (A.H / A.KVH);
     const int w = threadIdx.x / kWave, l = lane_id(), hl = l / 32;
     const int row = w * 32 + (l % 32);
@@ -1541,7 +1564,7 @@ extern "C" int hga_route_decode(const hga_config* cfg, int32_t L, int32_t n_clos
             rc = launch_status("hga_route_decode");                                             \
             if (rc) return rc;                                                                  \
         }                                                                                       \
-        route_decode_kernel<DTV, DHV><<<grid, kDT, lds, st>>>(a);                               \
+        route_decode_kernel<DTV, DHV><<<dim3(1u, grid), kDT, lds, st>>>(a);                     \
         return launch_status("hga_route_decode");                                               \
     }
     HGA_DEC_CASE(HGA_DTYPE_BF16, 128)
