@@ -56,7 +56,9 @@ __device__ __forceinline__ void ld_tab(const float* p, float* v) {
     }
 }
 
-template <int DT, bool STEPS>
+// HPT rows per thread: consecutive heads of one (position, batch), so the position's cos/sin
+// slices are loaded once for all of them (HPT divides the head count).
+template <int DT, bool STEPS, int HPT>
 __global__ __launch_bounds__(256) void rope_kernel(const char* x, int64_t x_sb, int64_t x_sh,
                                                    int64_t x_ss, char* out, int64_t o_sb,
                                                    int64_t o_sh, int64_t o_ss, const float* cos,
@@ -64,45 +66,52 @@ __global__ __launch_bounds__(256) void rope_kernel(const char* x, int64_t x_sb, 
                                                    int S, int Dh, int64_t nrows) {
     constexpr int N = Vec<DT>::N, E = Vec<DT>::kBytes;
     const int half = Dh / 2, tpr = half / N, rpb = 256 / tpr;
-    const int64_t row = (int64_t)blockIdx.x * rpb + threadIdx.x / tpr;
-    if (row >= nrows) return;
+    const int64_t row0 = ((int64_t)blockIdx.x * rpb + threadIdx.x / tpr) * HPT;
+    if (row0 >= nrows) return;
     const int d0 = (threadIdx.x % tpr) * N;
     // rows in (position, batch, head) order, heads fastest: the heads of one position share
     // its cos/sin row while it is in cache (head-major order would stream the whole table
     // once per head)
     const int64_t BX = nrows / S;
-    const int s = (int)(row / BX);
-    const int64_t bx = row % BX;
-    const int h = (int)(bx % X);
+    const int s = (int)(row0 / BX);
+    const int64_t bx = row0 % BX;
+    const int h0 = (int)(bx % X);
     const int64_t b = bx / X;
-    const char* xr = x + (b * x_sb + h * x_sh + s * x_ss) * E;
-    char* orow = out + (b * o_sb + h * o_sh + s * o_ss) * E;
     const float* cr = cos + b * cos_bstride + (int64_t)s * Dh;
     const float* sr = sin + b * cos_bstride + (int64_t)s * Dh;
-    float x1[N], x2[N], o1[N], o2[N], c1[N], c2[N], s1[N], s2[N];
-    Vec<DT>::ld(xr + d0 * E, x1);
-    Vec<DT>::ld(xr + (d0 + half) * E, x2);
+    float x1[HPT][N], x2[HPT][N], c1[N], c2[N], s1[N], s2[N];
+#pragma unroll
+    for (int k = 0; k < HPT; ++k) {
+        const char* xr = x + (b * x_sb + (h0 + k) * x_sh + s * x_ss) * E;
+        Vec<DT>::ld(xr + d0 * E, x1[k]);
+        Vec<DT>::ld(xr + (d0 + half) * E, x2[k]);
+    }
     ld_tab<N>(cr + d0, c1);
     ld_tab<N>(cr + d0 + half, c2);
     ld_tab<N>(sr + d0, s1);
     ld_tab<N>(sr + d0 + half, s2);
 #pragma unroll
-    for (int e = 0; e < N; ++e) {
-        float a = x1[e] * c1[e];
-        float r1 = -x2[e] * s1[e];
-        float c = x2[e] * c2[e];
-        float r2 = x1[e] * s2[e];
-        if constexpr (STEPS) {
-            a = round_dt(a, DT);
-            r1 = round_dt(r1, DT);
-            c = round_dt(c, DT);
-            r2 = round_dt(r2, DT);
+    for (int k = 0; k < HPT; ++k) {
+        float o1[N], o2[N];
+#pragma unroll
+        for (int e = 0; e < N; ++e) {
+            float a = x1[k][e] * c1[e];
+            float r1 = -x2[k][e] * s1[e];
+            float c = x2[k][e] * c2[e];
+            float r2 = x1[k][e] * s2[e];
+            if constexpr (STEPS) {
+                a = round_dt(a, DT);
+                r1 = round_dt(r1, DT);
+                c = round_dt(c, DT);
+                r2 = round_dt(r2, DT);
+            }
+            o1[e] = a + r1;
+            o2[e] = c + r2;
         }
-        o1[e] = a + r1;
-        o2[e] = c + r2;
+        char* orow = out + (b * o_sb + (h0 + k) * o_sh + s * o_ss) * E;
+        Vec<DT>::st(orow + d0 * E, o1);
+        Vec<DT>::st(orow + (d0 + half) * E, o2);
     }
-    Vec<DT>::st(orow + d0 * E, o1);
-    Vec<DT>::st(orow + (d0 + half) * E, o2);
 }
 
 }  // namespace
@@ -132,7 +141,8 @@ extern "C" int hga_rope(const hga_config* cfg, int32_t nheads, int32_t S, const 
     (void)E;
     const int tpr = Dh / 2 / N, rpb = 256 / tpr;
     const int64_t nrows = (int64_t)cfg->batch * nheads * S;
-    const int64_t grid = (nrows + rpb - 1) / rpb;
+    const int hpt = nheads % 4 == 0 ? 4 : 1;   // heads per thread (rows stay within a position)
+    const int64_t grid = (nrows / hpt + rpb - 1) / rpb;
     hipStream_t st = (hipStream_t)stream;
     const bool steps = (flags & HGA_ROPE_STEPS_IN_DTYPE) != 0;
     auto launch = [&](auto kern) {
@@ -141,10 +151,13 @@ extern "C" int hga_rope(const hga_config* cfg, int32_t nheads, int32_t S, const 
                                                          cos_bstride, nheads, S, Dh, nrows);
     };
     if (cfg->dtype == HGA_DTYPE_BF16) {
-        if (steps) launch(rope_kernel<HGA_DTYPE_BF16, true>);
-        else launch(rope_kernel<HGA_DTYPE_BF16, false>);
-    } else {
-        launch(rope_kernel<HGA_DTYPE_F32, false>);   // fp32: every step is already fp32
+        if (steps) hpt == 4 ? launch(rope_kernel<HGA_DTYPE_BF16, true, 4>)
+                            : launch(rope_kernel<HGA_DTYPE_BF16, true, 1>);
+        else hpt == 4 ? launch(rope_kernel<HGA_DTYPE_BF16, false, 4>)
+                      : launch(rope_kernel<HGA_DTYPE_BF16, false, 1>);
+    } else {   // fp32: every step is already fp32
+        hpt == 4 ? launch(rope_kernel<HGA_DTYPE_F32, false, 4>)
+                 : launch(rope_kernel<HGA_DTYPE_F32, false, 1>);
     }
     return launch_status("hga_rope");
 }
