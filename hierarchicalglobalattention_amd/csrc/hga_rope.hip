@@ -141,7 +141,9 @@ extern "C" int hga_rope(const hga_config* cfg, int32_t nheads, int32_t S, const 
     (void)E;
     const int tpr = Dh / 2 / N, rpb = 256 / tpr;
     const int64_t nrows = (int64_t)cfg->batch * nheads * S;
-    const int hpt = nheads % 4 == 0 ? 4 : 1;   // heads per thread (rows stay within a position)
+    // heads per thread (rows stay within a position); four only while the grid keeps at least
+    // 2048 workgroups (8 per CU)
+    const int hpt = nheads % 4 == 0 && nrows / 4 >= (int64_t)2048 * rpb ? 4 : 1;
     const int64_t grid = (nrows / hpt + rpb - 1) / rpb;
     hipStream_t st = (hipStream_t)stream;
     const bool steps = (flags & HGA_ROPE_STEPS_IN_DTYPE) != 0;

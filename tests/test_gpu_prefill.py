@@ -38,11 +38,11 @@ def _cmp_sets(r, ref_id, ref_thr, key_id, key_thr):
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
-@pytest.mark.parametrize("X,Dh", [(3, 64), (8, 128)])     # one head per thread / four
-def test_rope_bit_exact(hga, dtype, X, Dh):
+# one head per thread; four heads per thread (taken once the grid has >= 2048 workgroups)
+@pytest.mark.parametrize("B,X,S,Dh", [(2, 3, 77, 64), (1, 8, 32768, 128)])
+def test_rope_bit_exact(hga, dtype, B, X, S, Dh):
     from hierarchicalglobalattention_amd import ops
     g = torch.Generator().manual_seed(0)
-    B, S = 2, 77
     x = torch.randn(B, S, X, Dh, generator=g).to(dtype).transpose(1, 2)   # strided view
     cos, sin = rotary_table(S, Dh, 1e4)
     ref = rope_torch(x.float(), cos, sin).to(dtype)

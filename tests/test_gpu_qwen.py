@@ -40,12 +40,13 @@ def _rot_table(theta, S, Dh, dtype, pos0=0, B=1):
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
-def test_rope_steps_match_hf(hga, dtype):
+@pytest.mark.parametrize("S", [77, 32768])   # 32768: q takes four heads per thread
+def test_rope_steps_match_hf(hga, dtype, S):
     from transformers.models.qwen3_moe.modeling_qwen3_moe import apply_rotary_pos_emb
     from hierarchicalglobalattention_amd import ops
-    print(f"[qwen] rope steps {dtype}", flush=True)
+    print(f"[qwen] rope steps {dtype} S={S}", flush=True)
     g = torch.Generator().manual_seed(3)
-    B, H, KVH, S, Dh = 2, 4, 2, 77, 128
+    B, H, KVH, Dh = 2, 4, 2, 128
     q = torch.randn(B, S, H, Dh, generator=g).to(dtype).transpose(1, 2)     # strided view
     k = torch.randn(B, KVH, S, Dh, generator=g).to(dtype)
     c1, s1 = _rot_table(1e6, S, Dh, dtype, pos0=5)
