@@ -87,8 +87,7 @@ def run_gpu(args):
     state = {}
 
     def step():
-        q = ops.rope(hc, q_raw, cos, sin)
-        k_rope = ops.rope(hc, k_raw, cos, sin)
+        q, k_rope = ops.rope_qk(hc, q_raw, k_raw, cos, sin)
         (routed, lo, hi), = router.route_query_block(0, q, k_rope, k_raw, v, 0, cos=cos_r,
                                                      sin=sin_r)
         out = routed.attend(q)
@@ -107,8 +106,7 @@ def run_gpu(args):
         st = store.layer(0)
         store.ensure_capacity(0, N)
         ev[0].record()
-        q = ops.rope(hc, q_raw, cos, sin)
-        k_rope = ops.rope(hc, k_raw, cos, sin)
+        q, k_rope = ops.rope_qk(hc, q_raw, k_raw, cos, sin)
         ev[1].record()
         ck, gk, _, _ = ops.summarize(hc, k_raw, k_rope, cos_rf, sin_rf, cos_b=cos, sin_b=sin,
                                      chunk_k_b=st.chunk_k[:, :, :N], group_k_b=st.group_k[:, :, :N])
@@ -157,8 +155,7 @@ def run_gpu(args):
     if not args.no_backward:
         # training leg: gradient of the routed attention (hga_attend_prefill_bwd) for an upstream
         # gradient, same block and routing; 5 products per visible (query, key) pair
-        q = ops.rope(hc, q_raw, cos, sin)
-        k_rope = ops.rope(hc, k_raw, cos, sin)
+        q, k_rope = ops.rope_qk(hc, q_raw, k_raw, cos, sin)
         # as in training: the forward keeps each row's log-sum-exp for the backward
         lse = torch.empty(B, c["H"], S, dtype=torch.float32, device=dev)
         out = ops.attend_prefill(hc, q, k_rope, v, r_t["open_grp"], r_t["open_thr"], r_t["Kg"],

@@ -38,6 +38,8 @@ SIGNATURES = {
     "hga_prefill_widths": ([_CFG, _i32, _I32P, _I32P, _I32P], _i32),
     "hga_rope": ([_CFG, _i32, _i32, _vp, _i64, _i64, _i64, _vp, _i64, _i64, _i64, _vp, _vp,
                   _i64, _i32, _vp], ctypes.c_int),
+    "hga_rope_qk": ([_CFG, _i32] + [_vp, _i64, _i64, _i64] * 4 + [_vp, _vp, _i64, _i32, _vp],
+                    ctypes.c_int),
     "hga_summarize": ([_CFG, _i32, _i64, _vp, _i64, _i64, _i64, _vp, _i64, _i64, _i64, _vp,
                        _vp, _vp, _i64, _i64, _vp, _i64, _i64, _vp, _vp, _vp, _vp, _vp],
                       ctypes.c_int),

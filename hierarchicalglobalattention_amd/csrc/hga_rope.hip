@@ -56,33 +56,39 @@ __device__ __forceinline__ void ld_tab(const float* p, float* v) {
     }
 }
 
+// One tensor's rows: [B, X, S, Dh] input and output views (element strides b, head, position).
+struct RopeSet {
+    const char* x;
+    char* out;
+    int64_t x_sb, x_sh, x_ss, o_sb, o_sh, o_ss, nrows;
+    int X;
+};
+
 // HPT rows per thread: consecutive heads of one (position, batch), so the position's cos/sin
-// slices are loaded once for all of them (HPT divides the head count).
+// slices are loaded once for all of them (HPT divides the head count).  blk: the workgroup's
+// index within this tensor's part of the grid.
 template <int DT, bool STEPS, int HPT>
-__global__ __launch_bounds__(256) void rope_kernel(const char* x, int64_t x_sb, int64_t x_sh,
-                                                   int64_t x_ss, char* out, int64_t o_sb,
-                                                   int64_t o_sh, int64_t o_ss, const float* cos,
-                                                   const float* sin, int64_t cos_bstride, int X,
-                                                   int S, int Dh, int64_t nrows) {
+__device__ __forceinline__ void rope_rows(const RopeSet& R, int64_t blk, const float* cos,
+                                          const float* sin, int64_t cos_bstride, int S, int Dh) {
     constexpr int N = Vec<DT>::N, E = Vec<DT>::kBytes;
     const int half = Dh / 2, tpr = half / N, rpb = 256 / tpr;
-    const int64_t row0 = ((int64_t)blockIdx.x * rpb + threadIdx.x / tpr) * HPT;
-    if (row0 >= nrows) return;
+    const int64_t row0 = (blk * rpb + threadIdx.x / tpr) * HPT;
+    if (row0 >= R.nrows) return;
     const int d0 = (threadIdx.x % tpr) * N;
     // rows in (position, batch, head) order, heads fastest: the heads of one position share
     // its cos/sin row while it is in cache (head-major order would stream the whole table
     // once per head)
-    const int64_t BX = nrows / S;
+    const int64_t BX = R.nrows / S;
     const int s = (int)(row0 / BX);
     const int64_t bx = row0 % BX;
-    const int h0 = (int)(bx % X);
-    const int64_t b = bx / X;
+    const int h0 = (int)(bx % R.X);
+    const int64_t b = bx / R.X;
     const float* cr = cos + b * cos_bstride + (int64_t)s * Dh;
     const float* sr = sin + b * cos_bstride + (int64_t)s * Dh;
     float x1[HPT][N], x2[HPT][N], c1[N], c2[N], s1[N], s2[N];
 #pragma unroll
     for (int k = 0; k < HPT; ++k) {
-        const char* xr = x + (b * x_sb + (h0 + k) * x_sh + s * x_ss) * E;
+        const char* xr = R.x + (b * R.x_sb + (h0 + k) * R.x_sh + s * R.x_ss) * E;
         Vec<DT>::ld(xr + d0 * E, x1[k]);
         Vec<DT>::ld(xr + (d0 + half) * E, x2[k]);
     }
@@ -108,10 +114,86 @@ __global__ __launch_bounds__(256) void rope_kernel(const char* x, int64_t x_sb, 
             o1[e] = a + r1;
             o2[e] = c + r2;
         }
-        char* orow = out + (b * o_sb + (h0 + k) * o_sh + s * o_ss) * E;
+        char* orow = R.out + (b * R.o_sb + (h0 + k) * R.o_sh + s * R.o_ss) * E;
         Vec<DT>::st(orow + d0 * E, o1);
         Vec<DT>::st(orow + (d0 + half) * E, o2);
     }
+}
+
+// Workgroups [0, g0) rotate set 0 (H0 heads per thread), the rest set 1 (H1): q and k of a
+// block in one launch, so k's small grid fills q's tail instead of running after it.
+template <int DT, bool STEPS, int H0, int H1>
+__global__ __launch_bounds__(256) void rope_kernel(RopeSet r0, RopeSet r1, int64_t g0,
+                                                   const float* cos, const float* sin,
+                                                   int64_t cos_bstride, int S, int Dh) {
+    const int64_t blk = blockIdx.x;
+    if (blk < g0) rope_rows<DT, STEPS, H0>(r0, blk, cos, sin, cos_bstride, S, Dh);
+    else rope_rows<DT, STEPS, H1>(r1, blk - g0, cos, sin, cos_bstride, S, Dh);
+}
+
+}  // namespace
+}  // namespace hga
+
+namespace hga {
+namespace {
+
+int rope_launch(const hga_config* cfg, int S, RopeSet* sets, int nsets, const float* cos,
+                const float* sin, int64_t cos_bstride, int32_t flags, void* stream,
+                const char* what) {
+    int rc = check_config(cfg);
+    if (rc) return rc;
+    HGA_REQUIRE(cos && sin, HGA_ERR_ARG, "%s: NULL pointer", what);
+    HGA_REQUIRE(S >= 0, HGA_ERR_ARG, "%s: bad S", what);
+    HGA_REQUIRE((flags & ~HGA_ROPE_STEPS_IN_DTYPE) == 0, HGA_ERR_ARG, "%s: unknown flags", what);
+    const int Dh = cfg->head_dim;
+    const bool bf = cfg->dtype == HGA_DTYPE_BF16;
+    const int N = bf ? 8 : 4;   // elements per 16-byte access
+    HGA_REQUIRE((Dh / 2) % N == 0, HGA_ERR_UNSUPPORTED, "%s: head_dim %d not a multiple of %d",
+                what, Dh, 2 * N);
+    HGA_REQUIRE(((uintptr_t)cos % 16) == 0 && ((uintptr_t)sin % 16) == 0 && (cos_bstride % 4) == 0,
+                HGA_ERR_ARG, "%s: rotary tables must allow 16-byte vector access", what);
+    const int tpr = Dh / 2 / N, rpb = 256 / tpr;
+    int hpt[2] = {1, 1};
+    int64_t g[2] = {0, 0};
+    for (int i = 0; i < nsets; ++i) {
+        RopeSet& R = sets[i];
+        HGA_REQUIRE(R.x && R.out, HGA_ERR_ARG, "%s: NULL pointer", what);
+        HGA_REQUIRE(R.X > 0, HGA_ERR_ARG, "%s: bad head count", what);
+        const uintptr_t al = (uintptr_t)R.x | (uintptr_t)R.out;
+        HGA_REQUIRE((al % 16) == 0 &&
+                        ((R.x_sb | R.x_sh | R.x_ss | R.o_sb | R.o_sh | R.o_ss) % N) == 0,
+                    HGA_ERR_ARG, "%s: pointers/strides must allow 16-byte vector access", what);
+        R.nrows = (int64_t)cfg->batch * R.X * S;
+        // heads per thread (rows stay within a position); four only while the tensor's grid
+        // keeps at least 2048 workgroups (8 per CU)
+        hpt[i] = R.X % 4 == 0 && R.nrows / 4 >= (int64_t)2048 * rpb ? 4 : 1;
+        g[i] = (R.nrows / hpt[i] + rpb - 1) / rpb;
+    }
+    if (S == 0) return HGA_OK;
+    RopeSet none{};
+    const RopeSet& r1 = nsets > 1 ? sets[1] : none;
+    const int64_t grid = g[0] + g[1];
+    hipStream_t st = (hipStream_t)stream;
+    const bool steps = (flags & HGA_ROPE_STEPS_IN_DTYPE) != 0;
+    auto launch = [&](auto kern) {
+        kern<<<dim3((unsigned)grid), dim3(256), 0, st>>>(sets[0], r1, g[0], cos, sin, cos_bstride,
+                                                         S, Dh);
+    };
+    auto by_heads = [&](auto k11, auto k14, auto k41, auto k44) {
+        if (hpt[0] == 4) hpt[1] == 4 ? launch(k44) : launch(k41);
+        else hpt[1] == 4 ? launch(k14) : launch(k11);
+    };
+    constexpr int B16 = HGA_DTYPE_BF16, F32 = HGA_DTYPE_F32;
+    if (bf && steps)
+        by_heads(rope_kernel<B16, true, 1, 1>, rope_kernel<B16, true, 1, 4>,
+                 rope_kernel<B16, true, 4, 1>, rope_kernel<B16, true, 4, 4>);
+    else if (bf)
+        by_heads(rope_kernel<B16, false, 1, 1>, rope_kernel<B16, false, 1, 4>,
+                 rope_kernel<B16, false, 4, 1>, rope_kernel<B16, false, 4, 4>);
+    else   // fp32: every step is already fp32
+        by_heads(rope_kernel<F32, false, 1, 1>, rope_kernel<F32, false, 1, 4>,
+                 rope_kernel<F32, false, 4, 1>, rope_kernel<F32, false, 4, 4>);
+    return launch_status(what);
 }
 
 }  // namespace
@@ -122,44 +204,22 @@ extern "C" int hga_rope(const hga_config* cfg, int32_t nheads, int32_t S, const 
                         int64_t o_sh, int64_t o_ss, const float* cos, const float* sin,
                         int64_t cos_bstride, int32_t flags, void* stream) {
     using namespace hga;
-    int rc = check_config(cfg);
-    if (rc) return rc;
-    HGA_REQUIRE(x && out && cos && sin, HGA_ERR_ARG, "hga_rope: NULL pointer");
-    HGA_REQUIRE(nheads > 0 && S >= 0, HGA_ERR_ARG, "hga_rope: bad nheads/S");
-    HGA_REQUIRE((flags & ~HGA_ROPE_STEPS_IN_DTYPE) == 0, HGA_ERR_ARG, "hga_rope: unknown flags");
-    if (S == 0) return HGA_OK;
-    const int Dh = cfg->head_dim;
-    const bool bf = cfg->dtype == HGA_DTYPE_BF16;
-    const int E = bf ? 2 : 4, N = bf ? 8 : 4;   // elements per 16-byte access
-    HGA_REQUIRE((Dh / 2) % N == 0, HGA_ERR_UNSUPPORTED, "hga_rope: head_dim %d not a multiple of %d",
-                Dh, 2 * N);
-    const uintptr_t al = (uintptr_t)x | (uintptr_t)out;
-    HGA_REQUIRE((al % 16) == 0 && ((x_sb | x_sh | x_ss | o_sb | o_sh | o_ss) % N) == 0 &&
-                    ((uintptr_t)cos % 16) == 0 && ((uintptr_t)sin % 16) == 0 &&
-                    (cos_bstride % 4) == 0,
-                HGA_ERR_ARG, "hga_rope: pointers/strides must allow 16-byte vector access");
-    (void)E;
-    const int tpr = Dh / 2 / N, rpb = 256 / tpr;
-    const int64_t nrows = (int64_t)cfg->batch * nheads * S;
-    // heads per thread (rows stay within a position); four only while the grid keeps at least
-    // 2048 workgroups (8 per CU)
-    const int hpt = nheads % 4 == 0 && nrows / 4 >= (int64_t)2048 * rpb ? 4 : 1;
-    const int64_t grid = (nrows / hpt + rpb - 1) / rpb;
-    hipStream_t st = (hipStream_t)stream;
-    const bool steps = (flags & HGA_ROPE_STEPS_IN_DTYPE) != 0;
-    auto launch = [&](auto kern) {
-        kern<<<dim3((unsigned)grid), dim3(256), 0, st>>>((const char*)x, x_sb, x_sh, x_ss,
-                                                         (char*)out, o_sb, o_sh, o_ss, cos, sin,
-                                                         cos_bstride, nheads, S, Dh, nrows);
-    };
-    if (cfg->dtype == HGA_DTYPE_BF16) {
-        if (steps) hpt == 4 ? launch(rope_kernel<HGA_DTYPE_BF16, true, 4>)
-                            : launch(rope_kernel<HGA_DTYPE_BF16, true, 1>);
-        else hpt == 4 ? launch(rope_kernel<HGA_DTYPE_BF16, false, 4>)
-                      : launch(rope_kernel<HGA_DTYPE_BF16, false, 1>);
-    } else {   // fp32: every step is already fp32
-        hpt == 4 ? launch(rope_kernel<HGA_DTYPE_F32, false, 4>)
-                 : launch(rope_kernel<HGA_DTYPE_F32, false, 1>);
-    }
-    return launch_status("hga_rope");
+    HGA_REQUIRE(x && out, HGA_ERR_ARG, "hga_rope: NULL pointer");
+    RopeSet r{(const char*)x, (char*)out, x_sb, x_sh, x_ss, o_sb, o_sh, o_ss, 0, nheads};
+    return rope_launch(cfg, S, &r, 1, cos, sin, cos_bstride, flags, stream, "hga_rope");
+}
+
+extern "C" int hga_rope_qk(const hga_config* cfg, int32_t S, const void* q, int64_t q_sb,
+                           int64_t q_sh, int64_t q_ss, void* q_out, int64_t qo_sb, int64_t qo_sh,
+                           int64_t qo_ss, const void* k, int64_t k_sb, int64_t k_sh, int64_t k_ss,
+                           void* k_out, int64_t ko_sb, int64_t ko_sh, int64_t ko_ss,
+                           const float* cos, const float* sin, int64_t cos_bstride,
+                           int32_t flags, void* stream) {
+    using namespace hga;
+    HGA_REQUIRE(q && q_out && k && k_out, HGA_ERR_ARG, "hga_rope_qk: NULL pointer");
+    RopeSet r[2] = {
+        {(const char*)q, (char*)q_out, q_sb, q_sh, q_ss, qo_sb, qo_sh, qo_ss, 0, cfg ? cfg->heads : 0},
+        {(const char*)k, (char*)k_out, k_sb, k_sh, k_ss, ko_sb, ko_sh, ko_ss, 0,
+         cfg ? cfg->kv_heads : 0}};
+    return rope_launch(cfg, S, r, 2, cos, sin, cos_bstride, flags, stream, "hga_rope_qk");
 }

@@ -107,6 +107,29 @@ def rope(cfg: HgaConfig, x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor,
     return out
 
 
+def rope_qk(cfg: HgaConfig, q: torch.Tensor, k: torch.Tensor, cos: torch.Tensor,
+            sin: torch.Tensor, steps_in_dtype: bool = False):
+    """rope of q [B, heads, S, Dh] and k [B, kv_heads, S, Dh] with the same tables in one
+    launch; returns (q_rope, k_rope), equal to two rope calls."""
+    _dev(q, k, cos, sin)
+    B, H, S, D = q.shape
+    if tuple(k.shape) != (B, cfg.kv_heads, S, D) or H != cfg.heads or k.dtype != q.dtype:
+        raise ValueError(f"rope_qk: q {tuple(q.shape)} / k {tuple(k.shape)} {k.dtype} do not "
+                         f"match the config")
+    qo = torch.empty((B, H, S, D), dtype=q.dtype, device=q.device)
+    ko = torch.empty(tuple(k.shape), dtype=k.dtype, device=k.device)
+    cos = cos.contiguous().float()
+    sin = sin.contiguous().float()
+    if cos.shape[-2:] != (S, D):
+        raise ValueError(f"rotary table {tuple(cos.shape)} does not cover [{S}, {D}]")
+    cb = 0 if cos.dim() == 2 or cos.shape[0] == 1 else S * D
+    check(lib().hga_rope_qk(ctypes.byref(cfg), S, _p(q), *_s4(q), _p(qo), *_s4(qo), _p(k),
+                            *_s4(k), _p(ko), *_s4(ko), _p(cos), _p(sin), cb,
+                            ROPE_STEPS_IN_DTYPE if steps_in_dtype else 0, _stream()),
+          "hga_rope_qk")
+    return qo, ko
+
+
 def summarize(cfg: HgaConfig, k_raw: torch.Tensor, k_rope: torch.Tensor, cos_tab: torch.Tensor,
               sin_tab: torch.Tensor, pos0: int = 0, chunk_k=None, group_k=None, cos_b=None,
               sin_b=None, chunk_k_b=None, group_k_b=None):

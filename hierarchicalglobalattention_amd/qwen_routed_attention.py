@@ -128,8 +128,7 @@ class QwenRoutedAttention(nn.Module):
         cos = cos.reshape(-1, S, Dh)
         sin = sin.reshape(-1, S, Dh)
         hc = router.hcfg(B, x.dtype)
-        q_rope = ops.rope(hc, q, cos, sin, steps_in_dtype=True)
-        k_rope = ops.rope(hc, k_raw, cos, sin, steps_in_dtype=True)
+        q_rope, k_rope = ops.rope_qk(hc, q, k_raw, cos, sin, steps_in_dtype=True)
         # summaries anchor with the model's table in the activation dtype (:192-193)
         cos_r, sin_r = cos[:1].to(x.dtype), sin[:1].to(x.dtype)
         segments = router.route_query_block(self.layer_idx, q_rope, k_rope, k_raw, v, start_pos,
@@ -152,8 +151,7 @@ class QwenRoutedAttention(nn.Module):
         hc = router.hcfg(B, dt)
         pos = torch.arange(start_pos, start_pos + S, device=dev)
         kcos, ksin = _dca_rope(pos % L_c, Dh, theta, dev, dt)
-        k_dca = ops.rope(hc, k_raw, kcos, ksin, steps_in_dtype=True)
-        q_sel = ops.rope(hc, q, kcos, ksin, steps_in_dtype=True)
+        q_sel, k_dca = ops.rope_qk(hc, q, k_raw, kcos, ksin, steps_in_dtype=True)
         segments = router.route_query_block(self.layer_idx, q_sel, k_dca, k_raw, v, start_pos,
                                             return_positions=True)
         # attention queries in fp32 (:259-266)

@@ -99,8 +99,7 @@ class HierarchicalGlobalAttentionRouted(nn.Module):
             q_rope = ops.RopeFunction.apply(hc, q_raw, cos[:, 0], sin[:, 0])
             k_rope = ops.RopeFunction.apply(hc, k_raw, cos[:, 0], sin[:, 0])
         else:
-            q_rope = ops.rope(hc, q_raw, cos[:, 0], sin[:, 0])
-            k_rope = ops.rope(hc, k_raw, cos[:, 0], sin[:, 0])
+            q_rope, k_rope = ops.rope_qk(hc, q_raw, k_raw, cos[:, 0], sin[:, 0])
         cos_r, sin_r = cos[:1].to(x.dtype), sin[:1].to(x.dtype)
         with torch.no_grad():
             segments = router.route_query_block(self.layer_idx, q_rope.detach(), k_rope.detach(),

@@ -83,6 +83,15 @@ int hga_rope(const hga_config* cfg, int32_t nheads, int32_t S, const void* x, in
              const float* cos, const float* sin, int64_t cos_bstride, int32_t flags,
              void* stream);
 
+/* q and k of one block in a single launch (the two rotations of
+ * HierarchicalGlobalAttentionRouted.py:156-157 / qwen_routed_attention.py:176): q [B, heads, S,
+ * Dh] and k [B, kv_heads, S, Dh] views, same tables, flags and results as two hga_rope calls. */
+int hga_rope_qk(const hga_config* cfg, int32_t S, const void* q, int64_t q_sb, int64_t q_sh,
+                int64_t q_ss, void* q_out, int64_t qo_sb, int64_t qo_sh, int64_t qo_ss,
+                const void* k, int64_t k_sb, int64_t k_sh, int64_t k_ss, void* k_out,
+                int64_t ko_sb, int64_t ko_sh, int64_t ko_ss, const float* cos, const float* sin,
+                int64_t cos_bstride, int32_t flags, void* stream);
+
 /*
  * Mixed-RoPE chunk and group key summaries at KV-head granularity
  * (vectorized._rope_summary, vectorized.py:146-183, as applied at :265-287; the store twin

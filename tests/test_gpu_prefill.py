@@ -53,6 +53,29 @@ def test_rope_bit_exact(hga, dtype, B, X, S, Dh):
     assert torch.equal(out.cpu(), ref)
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("B,H,KVH,S,Dh", [(2, 6, 3, 77, 64), (1, 32, 4, 32768, 128)])
+@pytest.mark.parametrize("steps", [False, True])
+def test_rope_qk_matches_two_ropes(hga, dtype, B, H, KVH, S, Dh, steps):
+    """q and k in one launch (q's grid first, k's after) equal two separate rope calls bit for
+    bit, and the fp32-rotation variant equals torch's."""
+    from hierarchicalglobalattention_amd import ops
+    g = torch.Generator().manual_seed(1)
+    q = torch.randn(B, S, H, Dh, generator=g).to(dtype).transpose(1, 2).cuda()   # strided
+    k = torch.randn(B, KVH, S, Dh, generator=g).to(dtype).cuda()
+    cos, sin = rotary_table(S, Dh, 1e6)
+    cfg = _cfg(ops, B=B, H=H, KVH=KVH, Dh=Dh, C=8, gs=4, kf=0, kl=0, tc=0, tg=0, theta=1e6,
+               dtype=dtype)
+    cos, sin = cos.cuda(), sin.cuda()
+    qo, ko = ops.rope_qk(cfg, q, k, cos, sin, steps_in_dtype=steps)
+    q1 = ops.rope(cfg, q, cos, sin, steps_in_dtype=steps)
+    k1 = ops.rope(cfg, k, cos, sin, steps_in_dtype=steps)
+    torch.cuda.synchronize()
+    assert torch.equal(qo, q1) and torch.equal(ko, k1)
+    if not steps:
+        assert torch.equal(ko.cpu(), rope_torch(k.cpu().float(), cos.cpu(), sin.cpu()).to(dtype))
+
+
 @pytest.mark.parametrize("name", ["c1_full", "c1_ragged", "forced_prev", "ref_shape", "wide_topk"])
 def test_prefill_fp32_vs_reference(hga, name):
     from hierarchicalglobalattention_amd import ops
