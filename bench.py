@@ -185,7 +185,7 @@ def run_c2(reps: int = 5, warmup: int = 2):
     """the 40M-class stack, 8 HGA attention layers (d_model 512, 8 query
     heads, 2 KV heads, head_dim 64, chunk 64, group 16, keep_first 2, keep_last 8, topk_chunks 16,
     topk_groups 64, bf16, projections ~ N(0, 0.02)), prefill of 8192 tokens with inputs ~ N(0,1),
-    each layer's output feeding the next.  Times the layers' forward (projections, RoPE, router,
+    each layer adding its output to the residual stream that feeds the next (h <- h + attn(h)).  Times the layers' forward (projections, RoPE, router,
     attention, o_proj); the model's MLPs, norms and embeddings are not part of the path."""
     import hierarchicalglobalattention_amd as hga
     dev = torch.device("cuda:0")
@@ -204,7 +204,8 @@ def run_c2(reps: int = 5, warmup: int = 2):
     def stack():
         x = x0
         for m in layers:
-            x, _ = m(hidden_states=x)
+            a, _ = m(hidden_states=x)
+            x = x + a
         return x
 
     with torch.no_grad():

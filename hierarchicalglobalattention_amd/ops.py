@@ -305,6 +305,14 @@ def decode_widths(cfg: HgaConfig, n_closed: int):
     return kc.value, kg.value
 
 
+def route_decode_workspace(cfg: HgaConfig, L: int, n_closed: int) -> int:
+    """Workspace bytes hga_route_decode needs for an L-row block over n_closed chunks."""
+    nb = ctypes.c_int64()
+    check(lib().hga_route_decode_workspace(ctypes.byref(cfg), L, n_closed, ctypes.byref(nb)),
+          "hga_route_decode_workspace")
+    return nb.value
+
+
 def route_decode(cfg: HgaConfig, q: torch.Tensor, chunk_k: torch.Tensor, group_k: torch.Tensor,
                  n_closed: int) -> dict:
     """Decode routing of q [B,H,L,Dh] against the store tables chunk_k [B,KVH,cap,Dh] and
@@ -323,15 +331,13 @@ def route_decode(cfg: HgaConfig, q: torch.Tensor, chunk_k: torch.Tensor, group_k
     if chunk_k.stride(-1) != 1 or chunk_k.stride(2) != D or group_k.stride(3) != D or \
             group_k.stride(2) != group_k.shape[3] * D:
         raise ValueError("store tables must be chunk-contiguous with a contiguous head dim")
-    nb = ctypes.c_int64()
-    check(lib().hga_route_decode_workspace(ctypes.byref(cfg), L, n_closed, ctypes.byref(nb)),
-          "hga_route_decode_workspace")
-    ws = torch.empty(max(nb.value, 16), dtype=torch.uint8, device=dev)
+    nb = route_decode_workspace(cfg, L, n_closed)
+    ws = torch.empty(max(nb, 16), dtype=torch.uint8, device=dev)
     check(lib().hga_route_decode(
         ctypes.byref(cfg), L, n_closed, _p(q), *_s4(q), _p(chunk_k), chunk_k.stride(0),
         chunk_k.stride(1), _p(group_k), group_k.stride(0), group_k.stride(1), _p(r["mid"]),
         _p(r["mid_thr"]), _p(r["n_mid"]), _p(r["open_grp"]), _p(r["open_thr"]), _p(r["n_open"]),
-        _p(ws), nb.value, _stream()), "hga_route_decode")
+        _p(ws), nb, _stream()), "hga_route_decode")
     r["Kc"], r["Kg"] = Kc, Kg
     return r
 

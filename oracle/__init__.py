@@ -155,7 +155,10 @@ def route_prefill(q, chunk_k, group_k, S, C, gs, keep_first, keep_last, topk_chu
     return r
 
 
-def attend_prefill(q, k, v, C, gs, keep_first, keep_last, open_grp, open_thr, scale, dt):
+def attend_prefill(q, k, v, C, gs, keep_first, keep_last, open_grp, open_thr, scale, dt,
+                   chunks=None):
+    """Routed prefill attention; with ``chunks`` (query chunk ids) only those chunks' rows are
+    computed and the other rows of the result are NaN."""
     q, pq = _f(q)
     k, pk = _f(k)
     v, pv = _f(v)
@@ -163,11 +166,38 @@ def attend_prefill(q, k, v, C, gs, keep_first, keep_last, open_grp, open_thr, sc
     KVH = k.shape[1]
     og = np.ascontiguousarray(open_grp, np.int32)
     ot = np.ascontiguousarray(open_thr, np.int32)
-    out = np.empty_like(q)
-    lib().orc_attend_prefill(pq, pk, pv, B, H, KVH, S, Dh, C, gs, keep_first, keep_last,
-                             _i(og), _i(ot), og.shape[-1], ctypes.c_float(scale), dt,
-                             _f(out)[1])
+    out = np.full_like(q, np.nan)
+    if chunks is None:
+        lib().orc_attend_prefill(pq, pk, pv, B, H, KVH, S, Dh, C, gs, keep_first, keep_last,
+                                 _i(og), _i(ot), og.shape[-1], ctypes.c_float(scale), dt,
+                                 _f(out)[1])
+    else:
+        ch = np.ascontiguousarray(chunks, np.int32)
+        lib().orc_attend_prefill_chunks(pq, pk, pv, B, H, KVH, S, Dh, C, gs, keep_first,
+                                        keep_last, _i(og), _i(ot), og.shape[-1],
+                                        ctypes.c_float(scale), dt, _i(ch), len(ch), _f(out)[1])
     return out
+
+
+def route_prefill_heads(q, chunk_k, group_k, S, C, gs, keep_first, keep_last, topk_chunks,
+                        topk_groups, scale, threads=None):
+    """route_prefill with one oracle call per query head on a thread pool (the C oracle releases
+    the GIL); results are identical to one call over all heads."""
+    from concurrent.futures import ThreadPoolExecutor
+    q = np.ascontiguousarray(q, np.float32)
+    B, H = q.shape[:2]
+    KVH = chunk_k.shape[1]
+    rep = H // KVH
+    n = threads or min(H, len(os.sched_getaffinity(0)))
+
+    def one(h):
+        kv = h // rep
+        return route_prefill(q[:, h:h + 1], chunk_k[:, kv:kv + 1], group_k[:, kv:kv + 1], S, C,
+                             gs, keep_first, keep_last, topk_chunks, topk_groups, scale)
+
+    with ThreadPoolExecutor(n) as ex:
+        parts = list(ex.map(one, range(H)))
+    return {key: np.concatenate([p[key] for p in parts], axis=1) for key in parts[0]}
 
 
 def attend_prefill_bwd(q, k, v, dout, C, gs, keep_first, keep_last, open_grp, open_thr, scale):

@@ -414,18 +414,25 @@ static void attend_row(const float* qr, const float* kb, const float* vb, const 
     attend_row_sel(qsel, NULL, kb, vb, keys, nk, Dh, scale, dt, orow, p);
 }
 
-void orc_attend_prefill(const float* q, const float* k, const float* v, int B, int H, int KVH,
-                        int S, int Dh, int C, int gs, int kf, int kl, const int* open_grp,
-                        const int* open_thr, int Kgw, float scale, int dt, float* out) {
+/* Rows of the query chunks listed in chunks[0..nchunks) only (chunks == NULL: every chunk); the
+ * other rows of out are left as they are.  Lets a test check a few query chunks of a long
+ * sequence in seconds. */
+void orc_attend_prefill_chunks(const float* q, const float* k, const float* v, int B, int H,
+                               int KVH, int S, int Dh, int C, int gs, int kf, int kl,
+                               const int* open_grp, const int* open_thr, int Kgw, float scale,
+                               int dt, const int* chunks, int nchunks, float* out) {
     const int N = (S + C - 1) / C, M = C / gs, rep = H / KVH;
     long* keys = (long*)malloc(sizeof(long) * ((long)S + 16));
     double* p = (double*)malloc(sizeof(double) * ((long)S + 16));
+    const int nlist = chunks ? nchunks : N;
     for (int b = 0; b < B; ++b)
         for (int h = 0; h < H; ++h) {
             const int kvh = h / rep;
             const float* kb = k + ((long)b * KVH + kvh) * S * Dh;
             const float* vb = v + ((long)b * KVH + kvh) * S * Dh;
-            for (int n = 0; n < N; ++n) {
+            for (int ci = 0; ci < nlist; ++ci) {
+                const int n = chunks ? chunks[ci] : ci;
+                if (n < 0 || n >= N) continue;
                 int f_hi = kf > 0 ? (n < kf ? n : kf) : 0;
                 int l_lo = n;
                 if (kl > 0) {
@@ -453,6 +460,13 @@ void orc_attend_prefill(const float* q, const float* k, const float* v, int B, i
         }
     free(keys);
     free(p);
+}
+
+void orc_attend_prefill(const float* q, const float* k, const float* v, int B, int H, int KVH,
+                        int S, int Dh, int C, int gs, int kf, int kl, const int* open_grp,
+                        const int* open_thr, int Kgw, float scale, int dt, float* out) {
+    orc_attend_prefill_chunks(q, k, v, B, H, KVH, S, Dh, C, gs, kf, kl, open_grp, open_thr, Kgw,
+                              scale, dt, NULL, 0, out);
 }
 
 /* ------------------------------------------------------------------------------------------

@@ -100,3 +100,26 @@ def test_canonical_score_is_the_fma_chain():
     got = lib.orc_score(fp(q), fp(k), 64, ctypes.c_float(0.125))
     exact = float(np.dot(q.astype(np.float64), k.astype(np.float64))) * 0.125
     assert abs(got - exact) <= 64 * 2 ** -24 * float(np.abs(q * k).sum())
+
+
+def test_per_head_routing_and_chunk_subset_attention_agree():
+    """The test helpers that make the 32K cases fit in seconds: routing one query head per
+    thread equals one call over all heads, and attention of a query-chunk subset equals those
+    rows of the full attention (NaN elsewhere)."""
+    B, H, KVH, S, Dh, C, gs = 2, 4, 2, 700, 32, 32, 8
+    q, k, k_raw, v, cos, sin = _inputs(7, B, H, KVH, S, Dh, 1e4)
+    out, r, ck, gk = oracle.prefill(q.numpy(), k.numpy(), k_raw.numpy(), v.numpy(), cos.numpy(),
+                                    sin.numpy(), C=C, gs=gs, keep_first=1, keep_last=2,
+                                    topk_chunks=3, topk_groups=5, theta=1e4, dt=oracle.DT_F32)
+    rh = oracle.route_prefill_heads(q.numpy(), ck, gk, S, C, gs, 1, 2, 3, 5,
+                                    oracle.attn_scale(Dh), threads=3)
+    for key in r:
+        np.testing.assert_array_equal(rh[key], r[key])
+    chunks = [0, 5, 21]
+    sub = oracle.attend_prefill(q.numpy(), k.numpy(), v.numpy(), C, gs, 1, 2, r["open_grp"],
+                                r["open_thr"], oracle.attn_scale(Dh), oracle.DT_F32,
+                                chunks=chunks)
+    rows = np.concatenate([np.arange(n * C, min(S, (n + 1) * C)) for n in chunks])
+    np.testing.assert_array_equal(sub[:, :, rows], out[:, :, rows])
+    other = np.setdiff1d(np.arange(S), rows)
+    assert np.isnan(sub[:, :, other]).all()
