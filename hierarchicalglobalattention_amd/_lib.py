@@ -15,6 +15,7 @@ CSRC = os.path.join(_HERE, "csrc")
 
 HGA_DTYPE_F32, HGA_DTYPE_BF16 = 0, 1
 HGA_ROUTE_CANONICAL = 1
+HGA_ROUTE_SPLIT = 2
 
 # every exported entry point and its argument types (include/hga.h)
 _i32, _i64, _f32, _vp = ctypes.c_int32, ctypes.c_int64, ctypes.c_float, ctypes.c_void_p

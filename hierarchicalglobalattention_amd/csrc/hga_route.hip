@@ -251,7 +251,7 @@ __device__ float pooled_exact(int i, int rows, const uint32_t* sBits, int BW, Ca
 // candidate `ip` (evicting the last-ranked one when full), written ascending to sSel/sThr with
 // ids base_id + i; returns the count (wave-uniform).
 template <int J, class Canon>
-__device__ int pooled_select(int ncand, int k, int rows, const uint32_t* sBits, int BW,
+__device__ __forceinline__ int pooled_select(int ncand, int k, int rows, const uint32_t* sBits, int BW,
                              const uint32_t* sPk, const int* sFirst, float dpool,
                              Canon canon_row, int ip, int base_id, int* sSel, int* sThr,
                              int* amb) {
@@ -1126,6 +1126,768 @@ void route_stage2_kernel(RouteArgs A) {
     }
 }
 
+// ==========================================================================================
+// Fused router (bf16 MFMA path): stage 1 and stage 2 of one (b, h, query chunk) in one
+// workgroup of four waves.  Wave w owns query rows 16w..16w+15 in both stages; its rows' scores
+// never leave registers: S^T = K * Q^T by v_mfma_f32_16x16x32_bf16 puts query row l % 16 in lane
+// l, with candidates 16*tau + 4*(l/16) + i (i < 4) of candidate tile tau, so the four lanes
+// l % 16 + 16*qd of a row hold a quarter of its scores each.  The query rows stay in registers
+// as the B operand for both stages (q is read once).
+//
+// Stage 1, per segment of up to 256 pool candidates: counting probes (a Gaussian quantile of a
+// sample of the row, then regula falsi / Newton steps; counts summed over the row's four lanes)
+// find a key threshold T with k < count(key >= T) <= 32; those keys and their candidate ids are
+// appended to the row's LDS survivor list.  The survivors hold the row's top-(k+1) (each
+// segment's top-(k+1) survives), so sorting them (32-key or 64-key bitonic network over the 16
+// lanes of a DPP row) gives the exact k-th and (k+1)-th MFMA keys; certification and the
+// canonical re-rank of uncertain rows are as in the split kernels, except that an uncertain row
+// is rescored canonically in full.  Pooling, the pooled selection and stage 2 follow the split
+// kernels' rules.
+// ==========================================================================================
+constexpr int kFThreads = 256;
+constexpr int kFWaves = kFThreads / kWave;
+constexpr int kSegTiles = 16;             // 16-candidate tiles per stage-1 segment
+constexpr int kSegCand = 16 * kSegTiles;  // 256
+constexpr int kSurv = 32;                 // survivors per row and segment
+constexpr int kSvStride = 66;             // survivor list slots per row: 2 x 32, padded (bank spread)
+constexpr int kFusedMaxPool = 2 * kSegCand;
+constexpr int kFusedMaxT2 = 64;
+
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+
+// sums / maxima over the four lanes of a row (l % 16 + 16 * qd); butterflies, so all four
+// lanes end bit-identical
+__device__ __forceinline__ int q4_sum(int x) {
+    x += __shfl_xor(x, 16, kWave);
+    return x + __shfl_xor(x, 32, kWave);
+}
+__device__ __forceinline__ float q4_fsum(float x) {
+    x += __shfl_xor(x, 16, kWave);
+    return x + __shfl_xor(x, 32, kWave);
+}
+
+// One candidate tile: lane l loads candidate row (l % 16) of the tile, dims 32 ks + 8 (l / 16)
+// (zeros past ncand); returns the sum of squares of its part for the norm bound.
+template <int DH, class RowPtr>
+__device__ __forceinline__ void load_tile(RowPtr rowptr, int c, bool cv, uint4 (&a)[DH / 32]) {
+    const uint16_t* kp = rowptr(cv ? c : 0);
+    const int qd = lane_id() / 16;
+#pragma unroll
+    for (int ks = 0; ks < DH / 32; ++ks) {
+        a[ks] = make_uint4(0u, 0u, 0u, 0u);
+        if (cv) a[ks] = *reinterpret_cast<const uint4*>(kp + 32 * ks + 8 * qd);
+    }
+}
+template <int DH>
+__device__ __forceinline__ floatx4 tile_mfma(const uint4 (&a)[DH / 32], const bf16x8 (&qb)[DH / 32]) {
+    floatx4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int ks = 0; ks < DH / 32; ++ks)
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(a[ks]), qb[ks], acc, 0, 0, 0);
+    return acc;
+}
+template <int DH>
+__device__ __forceinline__ float tile_knorm(const uint4 (&a)[DH / 32]) {
+    float x = 0.0f;
+#pragma unroll
+    for (int ks = 0; ks < DH / 32; ++ks) x += sumsq_bf16x8(a[ks]);
+    return __builtin_sqrtf(q4_fsum(x));
+}
+
+// Scores of the wave's rows against candidates [c0, c0 + 16 * nt) (nt <= NT tiles, wave-uniform)
+// as order-preserving keys kv[4 tau + i] (0: candidate >= ncand).
+// Updates knmax with the norms of the candidates of the tiles tau with tau % nw == w (the nw
+// active waves of a workgroup see the same candidates: their maximum covers all of them) and
+// the sample statistics (s1, s2, ns) of the first four tiles.  Tiles are loaded four at a time.
+template <int DH, int NT, class RowPtr>
+__device__ __forceinline__ void fused_scores(RowPtr rowptr, int c0, int nt, int ncand, int w, int nw,
+                                             const bf16x8 (&qb)[DH / 32], float scale,
+                                             uint32_t (&kv)[4 * NT], float& knmax, float& s1,
+                                             float& s2, int& ns) {
+    constexpr int G = 4;
+    const int l = lane_id(), r16 = l % 16, qd = l / 16;
+#pragma unroll
+    for (int g0 = 0; g0 < NT; g0 += G) {
+        if (g0 < nt) {                                    // wave-uniform
+            uint4 a[G][DH / 32];
+#pragma unroll
+            for (int u = 0; u < G; ++u) {
+                const int c = c0 + 16 * (g0 + u) + r16;
+                load_tile<DH>(rowptr, c, g0 + u < nt && c < ncand, a[u]);
+            }
+#pragma unroll
+            for (int u = 0; u < G; ++u) {
+                const int tau = g0 + u;
+                const floatx4 acc = tile_mfma<DH>(a[u], qb);
+                if (tau % nw == w) {                      // wave-uniform
+                    const float kn = tile_knorm<DH>(a[u]);
+                    if (tau < nt && c0 + 16 * tau + r16 < ncand) knmax = fmaxf(knmax, kn);
+                }
+                const int cb = c0 + 16 * tau + 4 * qd;
+                const bool full = c0 + 16 * (tau + 1) <= ncand;   // wave-uniform
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const float sc = fmaf(acc[i], scale, 0.0f);
+                    const bool valid = tau < nt && (full || cb + i < ncand);
+                    kv[4 * tau + i] = valid ? okey_fast(sc) : 0u;
+                    if (tau < 4 && valid) {
+                        s1 += sc;
+                        s2 = fmaf(sc, sc, s2);
+                        ns += 1;
+                    }
+                }
+            }
+        } else {
+#pragma unroll
+            for (int i = 4 * g0; i < 4 * (g0 + G); ++i) kv[i] = 0u;
+        }
+    }
+}
+
+// Threshold probes for the rows of a wave (four lanes per row): on success T leaves
+// k < count(key >= T) <= kSurv keys in the row (rows with at most kSurv valid keys take T = 1:
+// all of them).  Returns false for rows (open ones only) where no threshold was found.
+template <int NK>
+__device__ __forceinline__ bool fused_probe(const uint32_t (&kv)[NK], int nk, bool open, int nv,
+                                            int k, float s1, float s2, int ns, uint32_t& T) {
+    bool ok = !open || nv <= kSurv;
+    T = 1u;
+    const float rn = __builtin_amdgcn_rcpf((float)(ns > 0 ? ns : 1));
+    const float mu = s1 * rn;
+    const float sd = __builtin_amdgcn_sqrtf(fmaxf(s2 * rn - mu * mu, 0.0f));
+    const float rv = __builtin_amdgcn_rcpf((float)(nv > 0 ? nv : 1));
+    const float target = 0.5f * (float)(k + 1 + kSurv);
+    float x = mu + z_upper_fast((target + 0.5f) * rv) * sd;
+    float lf = 0.0f, hf = 0.0f;
+    int clo = -1, chi = -1;
+    for (int it = 0; it < 6 && __ballot(!ok) != 0; ++it) {
+        const uint32_t tx = min(max(okey_fast(x), 1u), 0xfffffffeu);
+        int cl = 0;
+#pragma unroll
+        for (int g = 0; g < NK / 16; ++g)
+            if (16 * g < nk) {                             // wave-uniform
+#pragma unroll
+                for (int i = 16 * g; i < 16 * g + 16; ++i) cl += kv[i] >= tx ? 1 : 0;
+            }
+        const int c = q4_sum(cl);
+        if (!ok) {
+            if (c > k && c <= kSurv) {
+                ok = true;
+                T = tx;
+            } else {
+                if (c > kSurv) {
+                    lf = x;
+                    clo = c;
+                } else {
+                    hf = x;
+                    chi = c;
+                }
+                if (clo >= 0 && chi >= 0) {
+                    x = lf + (hf - lf) * ((float)clo - target) * __builtin_amdgcn_rcpf((float)(clo - chi));
+                } else {
+                    const float z = (x - mu) * __builtin_amdgcn_rcpf(sd > 0.0f ? sd : 1.0f);
+                    const float dens = (float)nv * 0.39894228f * __expf(-0.5f * z * z) *
+                                       __builtin_amdgcn_rcpf(sd > 0.0f ? sd : 1.0f);
+                    const float step = ((float)c - target) * __builtin_amdgcn_rcpf(fmaxf(dens, 1e-30f));
+                    x += fminf(fmaxf(step, -2.0f * sd), 2.0f * sd);
+                }
+            }
+        }
+    }
+    return ok;
+}
+
+// Appends this lane's keys >= T (and their candidate ids id0 + 16 * (i / 4) + 4 * qd + i % 4) to
+// the row's survivor list at base; returns the row's new survivor count (all four lanes).
+template <int NK>
+__device__ __forceinline__ int fused_compact(const uint32_t (&kv)[NK], int nk, uint32_t T, int id0,
+                                             uint2* rowbuf, int base, bool on) {
+    const int qd = lane_id() / 16;
+    int cl = 0;
+#pragma unroll
+    for (int g = 0; g < NK / 16; ++g)
+        if (16 * g < nk) {
+#pragma unroll
+            for (int i = 16 * g; i < 16 * g + 16; ++i) cl += (on && kv[i] >= T) ? 1 : 0;
+        }
+    // exclusive prefix over the row's lanes qd = 0..3
+    const int x16 = __shfl_xor(cl, 16, kWave);
+    const int pair = cl + x16;
+    const int x32 = __shfl_xor(pair, 32, kWave);
+    int pos = base + ((qd & 1) ? x16 : 0) + ((qd & 2) ? x32 : 0);
+    // the counts above must not keep 64 compare results alive: recompute them below
+    asm volatile("" : "+v"(T));
+#pragma unroll
+    for (int g = 0; g < NK / 16; ++g)
+        if (16 * g < nk) {
+#pragma unroll
+            for (int i = 16 * g; i < 16 * g + 16; ++i) {
+                const bool in = on && kv[i] >= T;
+                if (in) rowbuf[pos] = make_uint2(kv[i], (uint32_t)(id0 + 16 * (i / 4) + 4 * qd + (i % 4)));
+                pos += in ? 1 : 0;
+            }
+        }
+    return base + pair + x32;
+}
+
+__device__ __forceinline__ void fused_request(int t, int id, uint32_t key, uint32_t* sPk,
+                                              int* sFirst, uint32_t* sBits, int BW) {
+    atomicMax(&sPk[id], key);
+    atomicMin(&sFirst[id], t);
+    atomicOr(&sBits[t * BW + id / 32], 1u << (id % 32));
+}
+
+// Exact k-th and (k+1)-th largest keys of a row list (ns <= 16 * SW entries at rowbuf): DPP row
+// d (lanes 16d..16d+15) sorts one row with a 32-key (SW = 2) or 64-key (SW = 4) bitonic network.
+// Returns the lane's SW entries (zero keys past ns).
+template <int SW>
+__device__ __forceinline__ void list_kth(const uint2* rowbuf, int ns, int k, uint32_t& kth,
+                                         uint32_t& k1th, uint2 (&e)[SW]) {
+    const int seg = lane_id() & 15;
+#pragma unroll
+    for (int r = 0; r < SW; ++r) {
+        const int x = SW * seg + r;
+        e[r] = x < ns ? rowbuf[x] : make_uint2(0u, 0u);
+    }
+    if constexpr (SW == 2) {
+        uint32_t a = e[0].x, b = e[1].x;
+        sort32_row(a, b, seg);
+        const int ek = 32 - k, ek1 = ek - 1;
+        kth = r16_umax(seg == (ek >> 1) ? ((ek & 1) ? b : a) : 0u);
+        k1th = r16_umax(seg == (ek1 >> 1) ? ((ek1 & 1) ? b : a) : 0u);
+    } else {
+        uint32_t R[4] = {e[0].x, e[1].x, e[2].x, e[3].x};
+        sort64_row(R, seg);
+        const int ek = 64 - k, ek1 = ek - 1;
+        const uint32_t vk = (ek & 3) == 0 ? R[0] : (ek & 3) == 1 ? R[1] : (ek & 3) == 2 ? R[2] : R[3];
+        const uint32_t vk1 = (ek1 & 3) == 0 ? R[0] : (ek1 & 3) == 1 ? R[1] : (ek1 & 3) == 2 ? R[2] : R[3];
+        kth = r16_umax(seg == (ek >> 2) ? vk : 0u);
+        k1th = r16_umax(seg == (ek1 >> 2) ? vk1 : 0u);
+    }
+}
+
+// Selections of the wave's 16 rows from their lists (stage 1: survivor lists; stage 2: the full
+// candidate lists), four rows per pass: certified rows request their members; uncertain rows are
+// queued in sAmb with their re-rank band key in sBand (0: rescore every candidate).
+// sRowN[t]: list length, -1 no selection work (inactive, or everything valid was requested
+// already), -2 probes failed (uncertain, full rescoring).  sRowT[t] (stage 1, else nullptr): the
+// largest compaction threshold of the row's segments.
+template <int SW>
+__device__ __forceinline__ void list_rows(int w, int k, float dsc, const float* sQn, const uint2* sSv,
+                                          const int* sRowN, const uint32_t* sRowT, uint32_t* sPk,
+                                          int* sFirst, uint32_t* sBits, int BW, int* sAmb,
+                                          int* sAmbN, uint32_t* sBand) {
+    const int l = lane_id(), seg = l & 15;
+    for (int p = 0; p < 4; ++p) {
+        const int t = 16 * w + 4 * p + l / 16;
+        const int ns = sRowN[t];
+        uint32_t kth = 0u, k1th = 0u;
+        uint2 e[SW];
+        list_kth<SW>(sSv + t * kSvStride, ns < 0 ? 0 : ns, k, kth, k1th, e);
+        if (ns == -1) continue;
+        const float delta = dsc * sQn[t];
+        const bool amb = ns == -2 || kth == k1th || !(okey_inv(kth) - 2.0f * delta > okey_inv(k1th));
+        if (amb) {
+            if (seg == 0) {
+                const uint32_t band = okey_fast(okey_inv(kth) - 2.0f * delta);
+                sBand[t] = (ns == -2 || !sRowT || band < sRowT[t]) ? 0u : (band > 1u ? band : 1u);
+                sAmb[atomicAdd(sAmbN, 1)] = t;
+            }
+            continue;
+        }
+#pragma unroll
+        for (int r = 0; r < SW; ++r)
+            if (e[r].x >= kth && e[r].x != 0u) fused_request(t, (int)e[r].y, e[r].x, sPk, sFirst, sBits, BW);
+    }
+}
+
+// Canonical re-rank of an uncertain stage-1 row t from its survivor list (one wave): every
+// survivor whose MFMA key is >= band (which holds every candidate that can be among the row's
+// canonical top k: those have MFMA scores >= kth - 2 delta) is rescored with the canonical chain;
+// the k best by (canonical score, lower id) are requested.
+template <int DH>
+__device__ __noinline__ void fused_canon_band(int t, int k, uint32_t band, const uint2* rowbuf,
+                                              int ns, const uint16_t* qr, const uint16_t* kb,
+                                              float scale, uint32_t* sPk, int* sFirst,
+                                              uint32_t* sBits, int BW) {
+    const int l = lane_id();
+    const uint2 e = l < ns ? rowbuf[l] : make_uint2(0u, 0u);
+    const bool in = l < ns && e.x >= band;
+    const float E = in ? canon_dot<HGA_DTYPE_BF16, DH>(qr, kb + (int64_t)e.y * DH, scale) : -INFINITY;
+    int rank = 0;
+    for (uint64_t m = __ballot(in); m != 0ull; m &= m - 1ull) {
+        const int j = __builtin_ctzll(m);
+        const float Ej = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(E), j));
+        const int idj = __builtin_amdgcn_readlane((int)e.y, j);
+        rank += (Ej > E || (Ej == E && idj < (int)e.y)) ? 1 : 0;
+    }
+    if (in && rank < k) fused_request(t, (int)e.y, okey(E), sPk, sFirst, sBits, BW);
+}
+
+// Rows whose selection the MFMA scores could not certify (queued in sAmb): every candidate
+// rescored with the canonical chain, one dot product at a time, and the exact top-k requested.
+// Candidate i is row kb + i*DH (stage 1, sel == nullptr) or group sel[i/M]*M + i%M of kb
+// (stage 2, visible to row t iff thr[i/M] <= t).  Returns the number of rows this wave took.
+template <int DH>
+__device__ __noinline__ int fused_canon_rows(int w, int namb, const int* sAmb, int ncand, int k,
+                                             const uint16_t* qg, int64_t q_ss, const uint16_t* kb,
+                                             const int* sel, int M, const int* thr, float scale,
+                                             uint32_t* sPk, int* sFirst, uint32_t* sBits, int BW) {
+    const int l = lane_id();
+    int taken = 0;
+    auto row_of = [&](int i) -> const uint16_t* {
+        return sel ? kb + ((int64_t)sel[i / M] * M + (i % M)) * DH : kb + (int64_t)i * DH;
+    };
+    dispatch_j(ncand, [&](auto jt) {
+        constexpr int J = decltype(jt)::value;
+        for (int a = w; a < namb; a += kFWaves) {
+            const int ta = sAmb[a];
+            const uint16_t* qr = qg + ta * q_ss;
+            float v[J];
+#pragma unroll
+            for (int j = 0; j < J; ++j) {
+                const int i = l + 64 * j;
+                const bool vis = i < ncand && (!thr || thr[i / M] <= ta);
+                v[j] = vis ? canon_dot<HGA_DTYPE_BF16, DH>(qr, row_of(vis ? i : 0), scale) : -INFINITY;
+                asm volatile("" ::: "memory");    // one dot product in flight at a time
+            }
+            int unused = 0;
+            row_request<J>(ta, v, k, 0.0f, [](int) { return 0.0f; }, sPk, sFirst, sBits, BW, &unused);
+            ++taken;
+        }
+    });
+    return taken;
+}
+
+// Pooled selection of the fused kernel (wave 0): the certified top-k of the requested
+// candidates (sFirst < kNoRow) by pooled key, the forced candidate ip, written ascending to
+// sSel/sThr with ids base_id + i.  Probes (Gaussian quantile, then secant / Newton steps) find a
+// threshold leaving k < count <= 32 keys; those are compacted into buf (32 slots) and sorted by
+// lanes 0..15, which gives the exact k-th and (k+1)-th pooled keys.  Returns the count, or -1
+// when no threshold was found, the pooled scores could not be certified or the forced
+// candidate must evict a selected one (the caller then runs the general selection).
+__device__ __forceinline__ int fused_pool_fast(int P, int k, const uint32_t* sPk, const int* sFirst,
+                                               float dpool, int ip, int base_id, int* sSel,
+                                               int* sThr, uint2* buf) {
+    constexpr int J = kFusedMaxPool / kWave;
+    const int l = lane_id();
+    uint32_t kv[J];
+    int nreq = 0;
+    float s1 = 0.0f, s2 = 0.0f;
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+        const int i = l + 64 * j;
+        kv[j] = 0u;
+        if (64 * j < P) {                                 // wave-uniform
+            if (i < P && sFirst[i] < kNoRow) kv[j] = sPk[i];
+            nreq += __popcll(__ballot(kv[j] != 0u));
+            const float v = kv[j] != 0u ? okey_inv(kv[j]) : 0.0f;
+            s1 += v;
+            s2 = fmaf(v, v, s2);
+        }
+    }
+    uint32_t x = 1u;                                      // members: keys >= x
+    if (nreq > k) {
+        // a threshold T leaving k < count(key >= T) <= 32 requested candidates
+        s1 = wsum(s1);
+        s2 = wsum(s2);
+        const float mu = s1 / (float)nreq;
+        const float sd = sqrtf(fmaxf(s2 / (float)nreq - mu * mu, 0.0f));
+        const float target = 0.5f * (float)(k + 1 + 32);
+        uint32_t T = 1u;
+        bool ok = nreq <= 32;
+        float xf = mu + z_upper((target + 0.5f) / (float)nreq) * sd, lf = 0.0f, hf = 0.0f;
+        int clo = -1, chi = -1;
+        for (int it = 0; it < 8 && !ok; ++it) {
+            const uint32_t tx = min(max(okey(xf), 1u), 0xfffffffeu);
+            int c = 0;
+#pragma unroll
+            for (int j = 0; j < J; ++j)
+                if (64 * j < P) c += __popcll(__ballot(kv[j] >= tx));
+            if (c > k && c <= 32) {
+                ok = true;
+                T = tx;
+            } else {
+                if (c > 32) {
+                    lf = xf;
+                    clo = c;
+                } else {
+                    hf = xf;
+                    chi = c;
+                }
+                if (clo >= 0 && chi >= 0) {
+                    xf = lf + (hf - lf) * ((float)clo - target) / (float)(clo - chi);
+                } else {
+                    const float z = (xf - mu) / (sd > 0.0f ? sd : 1.0f);
+                    const float dens = (float)nreq * 0.39894228f * expf(-0.5f * z * z) /
+                                       (sd > 0.0f ? sd : 1.0f);
+                    const float step = ((float)c - target) / fmaxf(dens, 1e-30f);
+                    xf += fminf(fmaxf(step, -2.0f * sd), 2.0f * sd);
+                }
+            }
+        }
+        if (!ok) return -1;
+        // compact the keys >= T (with their candidate index) and sort them on lanes 0..15
+        int base = 0;
+#pragma unroll
+        for (int j = 0; j < J; ++j) {
+            if (64 * j < P) {
+                const bool in = kv[j] >= T && kv[j] != 0u;
+                const uint64_t bal = __ballot(in);
+                if (in) buf[base + lanes_below(bal)] = make_uint2(kv[j], (uint32_t)(l + 64 * j));
+                base += __popcll(bal);
+            }
+        }
+        __builtin_amdgcn_wave_barrier();
+        const int seg = l & 15;
+        uint32_t a = l < 16 && 2 * seg < base ? buf[2 * seg].x : 0u;
+        uint32_t bb = l < 16 && 2 * seg + 1 < base ? buf[2 * seg + 1].x : 0u;
+        sort32_row(a, bb, seg);
+        const int ek = 32 - k, ek1 = ek - 1;
+        const uint32_t kth = (uint32_t)__builtin_amdgcn_readfirstlane(
+            (int)r16_umax(seg == (ek >> 1) ? ((ek & 1) ? bb : a) : 0u));
+        const uint32_t k1th = (uint32_t)__builtin_amdgcn_readfirstlane(
+            (int)r16_umax(seg == (ek1 >> 1) ? ((ek1 & 1) ? bb : a) : 0u));
+        if (kth == k1th || !(okey_inv(kth) - 2.0f * dpool > okey_inv(k1th))) return -1;
+        x = kth;
+    }
+    int nsel = nreq < k ? nreq : k;
+    if (ip >= 0) {
+        bool have = false;
+#pragma unroll
+        for (int j = 0; j < J; ++j)
+            if (j == ip / 64) have = kv[j] >= x && kv[j] != 0u;   // meaningful in lane ip % 64
+        const bool have_w = __ballot(l == ip % 64 && have) != 0ull;
+        if (!have_w) {
+            if (nsel >= k) return -1;                     // eviction: general path
+#pragma unroll
+            for (int j = 0; j < J; ++j)
+                if (j == ip / 64 && l == ip % 64) kv[j] = 0xffffffffu;   // forced in (key >= x)
+            ++nsel;
+        }
+    }
+    int base = 0;
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+        const bool m = kv[j] >= x && kv[j] != 0u;
+        const uint64_t bal = __ballot(m);
+        if (m) {
+            const int i = l + 64 * j;
+            const int pos = base + lanes_below(bal);
+            sSel[pos] = base_id + i;
+            sThr[pos] = i == ip ? 0 : sFirst[i];
+        }
+        base += __popcll(bal);
+    }
+    return base;
+}
+
+// General pooled selection (certified with canonical pooled values, forced-candidate
+// eviction): the split kernels' routine, out of line.
+template <int DH>
+__device__ __noinline__ int fused_pool_general(int P, int k, int rows, const uint32_t* sBits, int BW,
+                                               const uint32_t* sPk, const int* sFirst, float dpool,
+                                               const uint16_t* qg, int64_t q_ss, const uint16_t* kb,
+                                               float scale, int ip, int base_id, int* sSel,
+                                               int* sThr, int* amb) {
+    auto canon = [&](int t, int i) {
+        return canon_dot<HGA_DTYPE_BF16, DH>(qg + t * q_ss, kb + (int64_t)i * DH, scale);
+    };
+    return pooled_select<kFusedMaxPool / kWave>(P, k, rows, sBits, BW, sPk, sFirst, dpool, canon,
+                                                 ip, base_id, sSel, sThr, amb);
+}
+
+template <int DH>
+__global__ __launch_bounds__(kFThreads) __attribute__((amdgpu_waves_per_eu(2)))
+void route_fused_kernel(RouteArgs A) {
+    constexpr int KS = DH / 32;
+    extern __shared__ __align__(16) unsigned char smem_raw[];
+    uint2* sSv = reinterpret_cast<uint2*>(smem_raw);                   // [64][kSvStride] survivors
+    float* sQn = reinterpret_cast<float*>(sSv + kRows * kSvStride);    // [64] row norms
+    int* sRowN = reinterpret_cast<int*>(sQn + kRows);                  // [64] survivors of a row
+    uint32_t* sBand = reinterpret_cast<uint32_t*>(sRowN + kRows);      // [64] re-rank band key
+    uint32_t* sRowT = sBand + kRows;                                   // [64] compaction threshold
+    int* sSel = reinterpret_cast<int*>(sRowT + kRows);                 // [kMaxSel]
+    int* sThr = sSel + kMaxSel;                                        // [kMaxSel]
+    int* sScal = sThr + kMaxSel;                                       // [8]
+    int* sAmb = sScal + 8;                                             // [64]
+    float* sKn = reinterpret_cast<float*>(sAmb + kRows);               // [4] per-wave norm maxima
+    uint32_t* sPk = reinterpret_cast<uint32_t*>(sKn + 4);              // [SPP] pooled key
+    int* sFirst = reinterpret_cast<int*>(sPk + A.SPP);                 // [SPP]
+    uint32_t* sBits = reinterpret_cast<uint32_t*>(sFirst + A.SPP);     // [64][BW]
+
+    const int N = A.N, C = A.C, M = A.M, BW = A.BW;
+    const int n = N - 1 - (int)(blockIdx.x / (A.B * A.H));            // heavy chunks first
+    const int bh = blockIdx.x % (A.B * A.H);
+    const int b = bh / A.H, h = bh % A.H, kvh = h / (A.H / A.KVH);
+    const int w = threadIdx.x / kWave, l = lane_id(), r16 = l % 16, qd = l / 16;
+    int rows = A.S - n * C;
+    if (rows > C) rows = C;
+    int f_hi, l_lo;
+    windows(n, A.kf, A.kl, &f_hi, &l_lo);
+    const int P = l_lo > f_hi ? l_lo - f_hi : 0;
+    const int64_t o = ((int64_t)b * A.H + h) * N + n;
+    const int Kcw = A.Kc > 0 ? A.Kc : 1, Kgw = A.Kg > 0 ? A.Kg : 1;
+    int32_t* out_sc = A.sel_chunk + o * Kcw;
+    int32_t* out_st = A.sel_thr + o * Kcw;
+    int32_t* out_og = A.open_grp + o * Kgw;
+    int32_t* out_ot = A.open_thr + o * Kgw;
+    if (A.Kc == 0 || P == 0) {
+        for (int i = threadIdx.x; i < Kcw; i += kFThreads) out_sc[i] = out_st[i] = -1;
+        for (int i = threadIdx.x; i < Kgw; i += kFThreads) out_og[i] = out_ot[i] = -1;
+        if (threadIdx.x == 0) A.n_sel[o] = A.n_open[o] = 0;
+        return;
+    }
+    const float scale = A.scale;
+    const uint16_t* qg = reinterpret_cast<const uint16_t*>(A.q) + b * A.q_sb + h * A.q_sh +
+                         (int64_t)n * C * A.q_ss;
+    const uint16_t* ckb = reinterpret_cast<const uint16_t*>(A.ck) + b * A.ck_sb + kvh * A.ck_sh;
+    const uint16_t* gkb = reinterpret_cast<const uint16_t*>(A.gk) + b * A.gk_sb + kvh * A.gk_sh;
+    const uint16_t* pool = ckb + (int64_t)f_hi * DH;             // candidate i = chunk f_hi + i
+    const int t = 16 * w + r16;                 // this lane's row (MFMA layout)
+    const bool act = t < rows;
+    const bool wave_act = 16 * w < rows;        // wave-uniform
+    const int nwact = (rows + 15) / 16;         // active waves (they split the norm bound)
+
+    // query rows: B operand (row l % 16, dims 32 ks + 8 qd) and norms
+    bf16x8 qb[KS];
+    {
+        float x = 0.0f;
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) {
+            uint4 u = make_uint4(0u, 0u, 0u, 0u);
+            // q is streamed once (256 MiB at 32K): non-temporal, so the summaries stay in L2
+            if (act) {
+                typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+                const u32x4 r = __builtin_nontemporal_load(
+                    reinterpret_cast<const u32x4*>(qg + (int64_t)t * A.q_ss + 32 * ks + 8 * qd));
+                u = make_uint4(r.x, r.y, r.z, r.w);
+            }
+            x += sumsq_bf16x8(u);
+            qb[ks] = as_bf16x8(u);
+        }
+        x = q4_fsum(x);
+        if (qd == 0) sQn[t] = __builtin_sqrtf(x);
+    }
+    for (int i = threadIdx.x; i < A.SPP; i += kFThreads) {
+        sPk[i] = 0u;
+        sFirst[i] = kNoRow;
+    }
+    for (int i = threadIdx.x; i < kRows * BW; i += kFThreads) sBits[i] = 0u;
+    if (threadIdx.x < 8) sScal[threadIdx.x] = 0;
+    __syncthreads();
+
+    // ---- stage 1: segments of up to 256 pool candidates ------------------------------------
+    const int kreq = A.Kc < P ? A.Kc : P;
+    const bool open = act && P > kreq;
+    float knmax = 0.0f;
+    int nsurv = 0;
+    bool hard = false;
+    uint32_t tmax = 1u;                         // largest compaction threshold of the segments
+    const int nseg = (P + kSegCand - 1) / kSegCand;
+    if (wave_act) {
+        for (int sg = 0; sg < nseg; ++sg) {
+            const int c0 = sg * kSegCand;
+            const int ncs = P - c0 < kSegCand ? P - c0 : kSegCand;
+            const int nt = (ncs + 15) / 16;
+            uint32_t kv[4 * kSegTiles];
+            float s1 = 0.0f, s2 = 0.0f;
+            int ns = 0;
+            fused_scores<DH, kSegTiles>([&](int i) { return pool + (int64_t)i * DH; }, c0, nt, P, w,
+                                        nwact, qb, scale, kv, knmax, s1, s2, ns);
+            if (!open) {
+                // every valid candidate requested (P <= Kc: one tile)
+                if (act) {
+#pragma unroll
+                    for (int i = 0; i < 4; ++i)
+                        if (kv[i] != 0u) fused_request(t, 4 * qd + i, kv[i], sPk, sFirst, sBits, BW);
+                }
+                continue;
+            }
+            s1 = q4_fsum(s1);
+            s2 = q4_fsum(s2);
+            ns = q4_sum(ns);
+            uint32_t T;
+            const bool ok = fused_probe<4 * kSegTiles>(kv, 4 * nt, !hard, ncs, kreq, s1, s2, ns, T);
+            hard = hard || !ok;
+            tmax = max(tmax, T);
+            nsurv = fused_compact<4 * kSegTiles>(kv, 4 * nt, T, c0, sSv + t * kSvStride, nsurv,
+                                                 !hard);
+        }
+        if (qd == 0) {
+            sRowN[t] = !open ? -1 : (hard ? -2 : nsurv);
+            sRowT[t] = tmax;
+        }
+        knmax = wmax(knmax);
+    }
+    if (l == 0) sKn[w] = knmax;
+    __syncthreads();
+    knmax = fmaxf(fmaxf(sKn[0], sKn[1]), fmaxf(sKn[2], sKn[3]));
+    const float ds1 = kDeltaRel * knmax * scale * 1.01f;
+    if (wave_act) {
+        if (nseg > 1)
+            list_rows<4>(w, kreq, ds1, sQn, sSv, sRowN, sRowT, sPk, sFirst, sBits, BW, sAmb, &sScal[4], sBand);
+        else
+            list_rows<2>(w, kreq, ds1, sQn, sSv, sRowN, sRowT, sPk, sFirst, sBits, BW, sAmb, &sScal[4], sBand);
+    }
+    __syncthreads();
+    int amb1 = 0, amb1p = 0;
+    {
+        const int namb = sScal[4];
+        for (int a = w; a < namb; a += kFWaves) {
+            const int ta = sAmb[a];
+            if (sBand[ta] != 0u)
+                fused_canon_band<DH>(ta, kreq, sBand[ta], sSv + ta * kSvStride, sRowN[ta],
+                                     qg + ta * A.q_ss, pool, scale, sPk, sFirst, sBits, BW);
+            else
+                fused_canon_rows<DH>(0, 1, sAmb + a, P, kreq, qg, A.q_ss, pool, nullptr, 0, nullptr,
+                                     scale, sPk, sFirst, sBits, BW);
+            ++amb1;
+        }
+    }
+    __syncthreads();
+    float qnmax = 0.0f;
+    {
+        float x = 0.0f;
+        if (l < rows) x = sQn[l];
+        qnmax = wmax(x);
+    }
+    if (w == 0) {
+        const float dpool = kDeltaRel * knmax * qnmax * scale * 1.01f;
+        const int prev = n - 1;
+        const int ip = (n > 0 && prev >= f_hi && prev < l_lo) ? prev - f_hi : -1;
+        int cnt = fused_pool_fast(P, A.Kc, sPk, sFirst, dpool, ip, f_hi, sSel, sThr, sSv);
+        if (cnt < 0)
+            cnt = fused_pool_general<DH>(P, A.Kc, rows, sBits, BW, sPk, sFirst, dpool, qg, A.q_ss,
+                                         pool, scale, ip, f_hi, sSel, sThr, &amb1p);
+        if (l == 0) sScal[0] = cnt;
+    }
+    __syncthreads();
+    const int nsel = sScal[0];
+    for (int i = threadIdx.x; i < Kcw; i += kFThreads) {
+        out_sc[i] = i < nsel ? sSel[i] : -1;
+        out_st[i] = i < nsel ? sThr[i] : -1;
+    }
+    if (threadIdx.x == 0) A.n_sel[o] = nsel;
+    if (A.stats && threadIdx.x == 0 && amb1p) atomicAdd(&A.stats[1], amb1p);
+    if (A.stats && l == 0 && amb1) atomicAdd(&A.stats[0], amb1);
+
+    // ---- stage 2: the M groups of each selected chunk --------------------------------------
+    if (A.Kg == 0 || A.Kgr == 0 || nsel == 0) {
+        for (int i = threadIdx.x; i < Kgw; i += kFThreads) out_og[i] = out_ot[i] = -1;
+        if (threadIdx.x == 0) A.n_open[o] = 0;
+        return;
+    }
+    const int T2 = nsel * M;
+    const int BW2 = A.BW2;
+    for (int i = threadIdx.x; i < T2 + 1; i += kFThreads) {
+        sPk[i] = 0u;
+        sFirst[i] = kNoRow;
+    }
+    for (int i = threadIdx.x; i < kRows * BW2; i += kFThreads) sBits[i] = 0u;
+    if (threadIdx.x < 8) sScal[threadIdx.x] = 0;
+    __syncthreads();
+    auto grow = [&](int i) -> const uint16_t* {
+        return gkb + ((int64_t)sSel[i / M] * M + (i % M)) * DH;
+    };
+    float knmax2 = 0.0f;
+    if (wave_act) {
+        uint32_t kv2[16];
+        bool open2 = false;
+        int nv2 = 0;
+        float s1 = 0.0f, s2 = 0.0f;
+        int ns = 0;
+        fused_scores<DH, 4>(grow, 0, (T2 + 15) / 16, T2, w, nwact, qb, scale, kv2, knmax2, s1, s2, ns);
+        // candidate c is visible to row t from its parent's first row on
+        ns = 0;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const int c = 16 * (i / 4) + 4 * qd + (i % 4);
+            const int pt = c < T2 ? sThr[c / M] : kNoRow;
+            kv2[i] = pt <= t ? kv2[i] : 0u;
+            ns += kv2[i] != 0u ? 1 : 0;
+        }
+        nv2 = q4_sum(ns);
+        open2 = act && nv2 > A.Kgr;
+        if (act && !open2) {
+            // every visible group requested
+#pragma unroll
+            for (int i = 0; i < 16; ++i)
+                if (kv2[i] != 0u)
+                    fused_request(t, 16 * (i / 4) + 4 * qd + (i % 4), kv2[i], sPk, sFirst, sBits, BW2);
+        }
+        if (open2) {
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const int id = 16 * (i / 4) + 4 * qd + (i % 4);
+                sSv[t * kSvStride + id] = make_uint2(kv2[i], (uint32_t)id);
+            }
+        }
+        if (qd == 0) sRowN[t] = open2 ? kFusedMaxT2 : -1;
+        knmax2 = wmax(knmax2);
+    }
+    if (l == 0) sKn[w] = knmax2;
+    __syncthreads();
+    knmax2 = fmaxf(fmaxf(sKn[0], sKn[1]), fmaxf(sKn[2], sKn[3]));
+    const float ds2 = kDeltaRel * knmax2 * scale * 1.01f;
+    if (wave_act)
+        list_rows<4>(w, A.Kgr, ds2, sQn, sSv, sRowN, nullptr, sPk, sFirst, sBits, BW2, sAmb, &sScal[4], sBand);
+    __syncthreads();
+    int amb2 = 0, amb2p = 0;
+    const int namb2 = sScal[4];
+    if (namb2 > 0)
+        amb2 = fused_canon_rows<DH>(w, namb2, sAmb, T2, A.Kgr, qg, A.q_ss, gkb, sSel, M, sThr,
+                                    scale, sPk, sFirst, sBits, BW2);
+    __syncthreads();
+    if (w == 0) {
+        const float dpool2 = ds2 * qnmax;
+        auto canonG2 = [&](int tt, int i) {
+            return canon_dot<HGA_DTYPE_BF16, DH>(qg + tt * A.q_ss, grow(i), scale);
+        };
+        float v[1];
+        v[0] = (l < T2 && sFirst[l] < kNoRow) ? okey_inv(sPk[l]) : -INFINITY;
+        auto canon_pool2 = [&](int i) { return pooled_exact(i, rows, sBits, BW2, canonG2); };
+        const uint32_t op = select_certified<1>(v, A.Kg, dpool2, canon_pool2, &amb2p);
+        const bool m = op & 1u;
+        const uint64_t bal = __ballot(m);
+        if (m) {
+            const int pos = lanes_below(bal);
+            if (pos < Kgw) {
+                out_og[pos] = sSel[l / M] * M + (l % M);
+                out_ot[pos] = sFirst[l];
+            }
+        }
+        const int cnt = __popcll(bal);
+        for (int i = cnt + l; i < Kgw; i += kWave) out_og[i] = out_ot[i] = -1;
+        if (l == 0) A.n_open[o] = cnt;
+        if (A.stats && l == 0 && amb2p) atomicAdd(&A.stats[3], amb2p);
+    }
+    if (A.stats && l == 0 && amb2) atomicAdd(&A.stats[2], amb2);
+}
+
+size_t fused_lds(const RouteArgs& a) {
+    return sizeof(uint2) * kRows * kSvStride + sizeof(float) * kRows + 3 * sizeof(int) * kRows +
+           sizeof(int) * (2 * kMaxSel + 8 + kRows) + sizeof(float) * 4 +
+           2 * sizeof(int) * (size_t)a.SPP + sizeof(uint32_t) * kRows * (size_t)a.BW;
+}
+
+template <int DH>
+int launch_route_fused(const RouteArgs& a, size_t lds, hipStream_t st) {
+    auto k = route_fused_kernel<DH>;
+    static bool attr_done = false;
+    if (!attr_done) {
+        if (hipFuncSetAttribute((const void*)k, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                163840) != hipSuccess) {
+            set_error("hga_route_prefill: cannot raise the LDS limit");
+            return HGA_ERR_LAUNCH;
+        }
+        attr_done = true;
+    }
+    const unsigned grid = (unsigned)(a.B * a.H * a.N);
+    k<<<dim3(grid), dim3(kFThreads), lds, st>>>(a);
+    return launch_status("hga_route_prefill (fused)");
+}
+
 template <int DT, int DH>
 int launch_route(const RouteArgs& a, size_t lds1, size_t lds2, hipStream_t st) {
     auto k1 = route_stage1_kernel<DT, DH>;
@@ -1222,6 +1984,20 @@ extern "C" int hga_route_prefill(const hga_config* cfg, int32_t S, const void* q
                     HGA_ERR_ARG, "hga_route_prefill: q and summaries need 16-byte aligned rows");
     }
     hipStream_t st = (hipStream_t)stream;
+    // bf16 MFMA scoring with a chunk of at most 64 rows, top-k chunks <= 16, pools of at most
+    // 512 chunks and at most 64 group candidates: the fused kernel (one launch, q read once)
+    const bool fused = cfg->dtype == HGA_DTYPE_BF16 && !a.canonical && !(flags & HGA_ROUTE_SPLIT) &&
+                       (D == 64 || D == 128) && a.Kc <= kCompactK && Pmax <= kFusedMaxPool &&
+                       T2max <= kFusedMaxT2;
+    if (fused) {
+        RouteArgs f = a;
+        f.SPP = (Pmax > T2max ? Pmax : T2max) + 1;
+        f.BW = (f.SPP + 31) / 32;
+        f.BW2 = (T2max + 1 + 31) / 32;
+        const size_t lds = fused_lds(f);
+        HGA_REQUIRE(lds <= 163840, HGA_ERR_UNSUPPORTED, "hga_route_prefill: %zu bytes of LDS", lds);
+        return D == 128 ? launch_route_fused<128>(f, lds, st) : launch_route_fused<64>(f, lds, st);
+    }
 #define HGA_ROUTE_CASE(DTV, DHV) \
     if (cfg->dtype == DTV && D == DHV) return launch_route<DTV, DHV>(a, lds1, lds2, st);
     HGA_ROUTE_CASE(HGA_DTYPE_BF16, 128)

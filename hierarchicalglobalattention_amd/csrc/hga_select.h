@@ -72,7 +72,7 @@ __device__ __forceinline__ float z_upper(float p) {
 // Members of the top-k (largest keys; equal keys -> lower candidate index lane + 64*j).
 // v holds the float values of the keys (only used to steer the search).
 template <int J>
-__device__ uint32_t exact_topk(const uint32_t (&kv)[J], const float (&v)[J], int k) {
+__device__ __forceinline__ uint32_t exact_topk(const uint32_t (&kv)[J], const float (&v)[J], int k) {
     const int nvalid = count_ge<J>(kv, 1u);
     uint32_t bits = 0;
     if (nvalid <= k) {
@@ -153,7 +153,7 @@ __device__ uint32_t exact_topk(const uint32_t (&kv)[J], const float (&v)[J], int
 // +-delta.  Ambiguous boundaries are resolved with canon(candidate) (exact).  Returns member
 // bits; *amb is incremented (wave-uniformly) when the canonical re-rank ran.
 template <int J, class Canon>
-__device__ uint32_t select_certified(const float (&v)[J], int k, float delta, Canon canon,
+__device__ __forceinline__ uint32_t select_certified(const float (&v)[J], int k, float delta, Canon canon,
                                      int* amb) {
     uint32_t kv[J];
 #pragma unroll

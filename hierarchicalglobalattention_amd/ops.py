@@ -177,10 +177,11 @@ def summarize(cfg: HgaConfig, k_raw: torch.Tensor, k_rope: torch.Tensor, cos_tab
 
 def route_prefill(cfg: HgaConfig, q: torch.Tensor, chunk_k: torch.Tensor,
                   group_k: torch.Tensor, S: int | None = None, canonical: bool = False,
-                  stats: torch.Tensor | None = None) -> dict:
+                  stats: torch.Tensor | None = None, split: bool = False) -> dict:
     """Two-level routing of a fresh prefill block.  Returns int32 tensors
     sel_chunk/sel_thr [B,H,N,Kc], n_sel [B,H,N], open_grp/open_thr [B,H,N,Kg], n_open [B,H,N]
-    (widths at least 1)."""
+    (widths at least 1).  ``canonical`` scores every candidate with the fp32 FMA chain;
+    ``split`` runs bf16 routing as two kernels instead of the fused one (same lists)."""
     _dev(q, chunk_k, group_k)
     B, H, Sq, D = q.shape
     S = Sq if S is None else S
@@ -195,7 +196,7 @@ def route_prefill(cfg: HgaConfig, q: torch.Tensor, chunk_k: torch.Tensor,
     if chunk_k.stride(-1) != 1 or chunk_k.stride(2) != D or group_k.stride(3) != D or \
             group_k.stride(2) != group_k.shape[3] * D:
         raise ValueError("summaries must be chunk-contiguous with a contiguous head dim")
-    flags = _lib.HGA_ROUTE_CANONICAL if canonical else 0
+    flags = (_lib.HGA_ROUTE_CANONICAL if canonical else 0) | (_lib.HGA_ROUTE_SPLIT if split else 0)
     check(lib().hga_route_prefill(
         ctypes.byref(cfg), S, _p(q), *_s4(q), _p(chunk_k), chunk_k.stride(0), chunk_k.stride(1),
         _p(group_k), group_k.stride(0), group_k.stride(1), _p(r["sel_chunk"]), _p(r["sel_thr"]),

@@ -32,6 +32,8 @@ enum {
 enum {
     HGA_ROUTE_CANONICAL = 1, /* score every candidate with the canonical fp32 FMA chain
                                 (no MFMA pre-pass); slower, same result */
+    HGA_ROUTE_SPLIT = 2,     /* bf16: separate stage-1 and stage-2 kernels instead of the fused
+                                one; same result */
 };
 
 /* Layer configuration; mirrors RouterConfig + ChunkPlacementPolicy
