@@ -1166,18 +1166,43 @@ __device__ __forceinline__ float q4_fsum(float x) {
     return x + __shfl_xor(x, 32, kWave);
 }
 
-// One candidate tile: lane l loads candidate row (l % 16) of the tile, dims 32 ks + 8 (l / 16)
-// (zeros past ncand); returns the sum of squares of its part for the norm bound.
-template <int DH, class RowPtr>
-__device__ __forceinline__ void load_tile(RowPtr rowptr, int c, bool cv, uint4 (&a)[DH / 32]) {
-    const uint16_t* kp = rowptr(cv ? c : 0);
-    const int qd = lane_id() / 16;
+// Direct global->LDS copy of 16 bytes per lane: lane i's bytes at sbase + voff land at LDS byte
+// address lds_addr + 16 i (lds_addr wave-uniform).  Inline assembly, so the compiler inserts no
+// waits for it; the kernel waits (s_waitcnt 0) before the barrier that publishes a stage.  M0
+// holds the LDS address; nothing else in this kernel uses M0.
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ __forceinline__ void route_lds_copy16(const void* sbase, uint32_t voff, uint32_t lds_addr) {
+    // base and LDS address are wave-uniform: make them scalar operands
+    const uint64_t b64 = (uint64_t)(uintptr_t)sbase;
+    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)b64);
+    const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(b64 >> 32));
+    const void* sb = (const void*)(uintptr_t)(((uint64_t)hi << 32) | lo);
+    const uint32_t la = __builtin_amdgcn_readfirstlane(lds_addr);
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2"
+                 :: "s"(la), "v"(voff), "s"(sb) : "memory", "m0");
+}
+#pragma clang diagnostic pop
+
+// A stage holds 64 candidate rows (DH bf16 each, row-major) with the 16-byte pieces of row r
+// XOR-swizzled: piece j at slot j ^ (r % PPR), so the 16 rows of a tile read the same piece from
+// different banks.  Wave w copies rows 16w..16w+15: row r (< nrows) from sbase + off(r) bytes.
+template <int DH, class Off>
+__device__ __forceinline__ void stage_rows(const void* sbase, Off off, int nrows, uint32_t stage,
+                                           int w) {
+    constexpr int PPR = DH / 8;          // 16-byte pieces per row
+    constexpr int RPI = 64 / PPR;        // rows per wave instruction
+    const int l = lane_id();
 #pragma unroll
-    for (int ks = 0; ks < DH / 32; ++ks) {
-        a[ks] = make_uint4(0u, 0u, 0u, 0u);
-        if (cv) a[ks] = *reinterpret_cast<const uint4*>(kp + 32 * ks + 8 * qd);
+    for (int r = 0; r < 16 / RPI; ++r) {
+        const int row = 16 * w + RPI * r + l / PPR;
+        const int j = (l % PPR) ^ (row % PPR);
+        if (row < nrows)
+            route_lds_copy16(sbase, off(row) + 16u * (uint32_t)j,
+                             stage + (uint32_t)((16 * w + RPI * r) * DH * 2));
     }
 }
+
 template <int DH>
 __device__ __forceinline__ floatx4 tile_mfma(const uint4 (&a)[DH / 32], const bf16x8 (&qb)[DH / 32]) {
     floatx4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
@@ -1194,52 +1219,47 @@ __device__ __forceinline__ float tile_knorm(const uint4 (&a)[DH / 32]) {
     return __builtin_sqrtf(q4_fsum(x));
 }
 
-// Scores of the wave's rows against candidates [c0, c0 + 16 * nt) (nt <= NT tiles, wave-uniform)
-// as order-preserving keys kv[4 tau + i] (0: candidate >= ncand).
-// Updates knmax with the norms of the candidates of the tiles tau with tau % nw == w (the nw
-// active waves of a workgroup see the same candidates: their maximum covers all of them) and
-// the sample statistics (s1, s2, ns) of the first four tiles.  Tiles are loaded four at a time.
-template <int DH, int NT, class RowPtr>
-__device__ __forceinline__ void fused_scores(RowPtr rowptr, int c0, int nt, int ncand, int w, int nw,
-                                             const bf16x8 (&qb)[DH / 32], float scale,
-                                             uint32_t (&kv)[4 * NT], float& knmax, float& s1,
-                                             float& s2, int& ns) {
-    constexpr int G = 4;
+// Scores of the wave's rows against the 4 tiles (64 candidates c0 + 16 u + ..) of a stage as
+// order-preserving keys kv[4 tau + i], tau = tau0 + u (0: candidate >= ncand).  A operands from
+// the stage: lane l reads candidate row 16 u + l % 16, dims 32 ks + 8 (l / 16).  Updates knmax
+// with the norms of the tiles with tau % nw == w (the nw active waves see the same candidates:
+// their maximum covers all) and the sample statistics (s1, s2, ns) of tiles 0..3.
+template <int DH, int NK>
+__device__ __forceinline__ void stage_scores(const unsigned char* stage, int tau0, int c0, int ncand,
+                                             int w, int nw, const bf16x8 (&qb)[DH / 32], float scale,
+                                             uint32_t (&kv)[NK], float& knmax, float& s1, float& s2,
+                                             int& ns) {
+    constexpr int PPR = DH / 8;
     const int l = lane_id(), r16 = l % 16, qd = l / 16;
 #pragma unroll
-    for (int g0 = 0; g0 < NT; g0 += G) {
-        if (g0 < nt) {                                    // wave-uniform
-            uint4 a[G][DH / 32];
+    for (int u = 0; u < 4; ++u) {
+        const int tau = tau0 + u;
+        if (tau >= NK / 4) break;
+        const int row = 16 * u + r16;
+        uint4 a[DH / 32];
 #pragma unroll
-            for (int u = 0; u < G; ++u) {
-                const int c = c0 + 16 * (g0 + u) + r16;
-                load_tile<DH>(rowptr, c, g0 + u < nt && c < ncand, a[u]);
+        for (int ks = 0; ks < DH / 32; ++ks) {
+            const int j = (4 * ks + qd) ^ (row % PPR);
+            a[ks] = *reinterpret_cast<const uint4*>(stage + row * (DH * 2) + 16 * j);
+        }
+        const floatx4 acc = tile_mfma<DH>(a, qb);
+        const int cbase = c0 + 16 * u;
+        if (tau % nw == w) {                      // wave-uniform
+            const float kn = tile_knorm<DH>(a);
+            if (cbase + r16 < ncand) knmax = fmaxf(knmax, kn);
+        }
+        const int cb = cbase + 4 * qd;
+        const bool full = cbase + 16 <= ncand;    // wave-uniform
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const float sc = fmaf(acc[i], scale, 0.0f);
+            const bool valid = full || cb + i < ncand;
+            kv[4 * tau + i] = valid ? okey_fast(sc) : 0u;
+            if (tau < 4 && valid) {
+                s1 += sc;
+                s2 = fmaf(sc, sc, s2);
+                ns += 1;
             }
-#pragma unroll
-            for (int u = 0; u < G; ++u) {
-                const int tau = g0 + u;
-                const floatx4 acc = tile_mfma<DH>(a[u], qb);
-                if (tau % nw == w) {                      // wave-uniform
-                    const float kn = tile_knorm<DH>(a[u]);
-                    if (tau < nt && c0 + 16 * tau + r16 < ncand) knmax = fmaxf(knmax, kn);
-                }
-                const int cb = c0 + 16 * tau + 4 * qd;
-                const bool full = c0 + 16 * (tau + 1) <= ncand;   // wave-uniform
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const float sc = fmaf(acc[i], scale, 0.0f);
-                    const bool valid = tau < nt && (full || cb + i < ncand);
-                    kv[4 * tau + i] = valid ? okey_fast(sc) : 0u;
-                    if (tau < 4 && valid) {
-                        s1 += sc;
-                        s2 = fmaf(sc, sc, s2);
-                        ns += 1;
-                    }
-                }
-            }
-        } else {
-#pragma unroll
-            for (int i = 4 * g0; i < 4 * (g0 + G); ++i) kv[i] = 0u;
         }
     }
 }
@@ -1601,8 +1621,10 @@ template <int DH>
 __global__ __launch_bounds__(kFThreads) __attribute__((amdgpu_waves_per_eu(2)))
 void route_fused_kernel(RouteArgs A) {
     constexpr int KS = DH / 32;
+    constexpr int kStageBytes = 64 * DH * 2;                           // 64 candidate rows
     extern __shared__ __align__(16) unsigned char smem_raw[];
-    uint2* sSv = reinterpret_cast<uint2*>(smem_raw);                   // [64][kSvStride] survivors
+    unsigned char* sStage = smem_raw;                                  // [2][64][DH] candidate rows
+    uint2* sSv = reinterpret_cast<uint2*>(sStage + 2 * kStageBytes);   // [64][kSvStride] survivors
     float* sQn = reinterpret_cast<float*>(sSv + kRows * kSvStride);    // [64] row norms
     int* sRowN = reinterpret_cast<int*>(sQn + kRows);                  // [64] survivors of a row
     uint32_t* sBand = reinterpret_cast<uint32_t*>(sRowN + kRows);      // [64] re-rank band key
@@ -1648,6 +1670,8 @@ void route_fused_kernel(RouteArgs A) {
     const bool act = t < rows;
     const bool wave_act = 16 * w < rows;        // wave-uniform
     const int nwact = (rows + 15) / 16;         // active waves (they split the norm bound)
+    const uint32_t stage_lds =
+        (uint32_t)(uintptr_t)(__attribute__((address_space(3))) unsigned char*)sStage;
 
     // query rows: B operand (row l % 16, dims 32 ks + 8 qd) and norms
     bf16x8 qb[KS];
@@ -1685,35 +1709,54 @@ void route_fused_kernel(RouteArgs A) {
     bool hard = false;
     uint32_t tmax = 1u;                         // largest compaction threshold of the segments
     const int nseg = (P + kSegCand - 1) / kSegCand;
-    if (wave_act) {
-        for (int sg = 0; sg < nseg; ++sg) {
-            const int c0 = sg * kSegCand;
-            const int ncs = P - c0 < kSegCand ? P - c0 : kSegCand;
-            const int nt = (ncs + 15) / 16;
-            uint32_t kv[4 * kSegTiles];
-            float s1 = 0.0f, s2 = 0.0f;
-            int ns = 0;
-            fused_scores<DH, kSegTiles>([&](int i) { return pool + (int64_t)i * DH; }, c0, nt, P, w,
-                                        nwact, qb, scale, kv, knmax, s1, s2, ns);
-            if (!open) {
-                // every valid candidate requested (P <= Kc: one tile)
-                if (act) {
+    for (int sg = 0; sg < nseg; ++sg) {
+        // every wave copies a quarter of each 64-candidate group into an LDS stage (double
+        // buffered, one group ahead); the waves with query rows score the stage
+        const int c0 = sg * kSegCand;
+        const int ncs = P - c0 < kSegCand ? P - c0 : kSegCand;
+        const int nt = (ncs + 15) / 16;
+        const int ngr = (nt + 3) / 4;
+        uint32_t kv[4 * kSegTiles];
+        float s1 = 0.0f, s2 = 0.0f;
+        int ns = 0;
+        if (sg > 0) __syncthreads();              // the previous segment's stages are read
+        stage_rows<DH>(pool, [&](int r) { return (uint32_t)((c0 + r) * DH * 2); }, ncs, stage_lds, w);
 #pragma unroll
-                    for (int i = 0; i < 4; ++i)
-                        if (kv[i] != 0u) fused_request(t, 4 * qd + i, kv[i], sPk, sFirst, sBits, BW);
-                }
-                continue;
+        for (int g = 0; g < kSegTiles / 4; ++g) {
+            if (g < ngr) {                                            // workgroup-uniform
+                __builtin_amdgcn_s_waitcnt(0);
+                __syncthreads();          // stage g % 2 complete, stage (g + 1) % 2 no longer read
+                if (g + 1 < ngr)
+                    stage_rows<DH>(pool, [&](int r) { return (uint32_t)((c0 + 64 * (g + 1) + r) * DH * 2); },
+                                   ncs - 64 * (g + 1), stage_lds + (uint32_t)(((g + 1) & 1) * kStageBytes), w);
+                if (wave_act)
+                    stage_scores<DH, 4 * kSegTiles>(sStage + (g & 1) * kStageBytes, 4 * g, c0 + 64 * g, P,
+                                                    w, nwact, qb, scale, kv, knmax, s1, s2, ns);
+            } else {
+#pragma unroll
+                for (int i = 16 * g; i < 16 * g + 16; ++i) kv[i] = 0u;
             }
-            s1 = q4_fsum(s1);
-            s2 = q4_fsum(s2);
-            ns = q4_sum(ns);
-            uint32_t T;
-            const bool ok = fused_probe<4 * kSegTiles>(kv, 4 * nt, !hard, ncs, kreq, s1, s2, ns, T);
-            hard = hard || !ok;
-            tmax = max(tmax, T);
-            nsurv = fused_compact<4 * kSegTiles>(kv, 4 * nt, T, c0, sSv + t * kSvStride, nsurv,
-                                                 !hard);
         }
+        if (!wave_act) continue;
+        if (!open) {
+            // every valid candidate requested (P <= Kc: one tile)
+            if (act) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    if (kv[i] != 0u) fused_request(t, 4 * qd + i, kv[i], sPk, sFirst, sBits, BW);
+            }
+            continue;
+        }
+        s1 = q4_fsum(s1);
+        s2 = q4_fsum(s2);
+        ns = q4_sum(ns);
+        uint32_t T;
+        const bool ok = fused_probe<4 * kSegTiles>(kv, 4 * nt, !hard, ncs, kreq, s1, s2, ns, T);
+        hard = hard || !ok;
+        tmax = max(tmax, T);
+        nsurv = fused_compact<4 * kSegTiles>(kv, 4 * nt, T, c0, sSv + t * kSvStride, nsurv, !hard);
+    }
+    if (wave_act) {
         if (qd == 0) {
             sRowN[t] = !open ? -1 : (hard ? -2 : nsurv);
             sRowT[t] = tmax;
@@ -1780,12 +1823,16 @@ void route_fused_kernel(RouteArgs A) {
     }
     const int T2 = nsel * M;
     const int BW2 = A.BW2;
+    __syncthreads();                              // the stage-1 stages are read
+    stage_rows<DH>(gkb, [&](int r) { return (uint32_t)(((int64_t)sSel[r / M] * M + (r % M)) * DH * 2); },
+                   T2, stage_lds, w);
     for (int i = threadIdx.x; i < T2 + 1; i += kFThreads) {
         sPk[i] = 0u;
         sFirst[i] = kNoRow;
     }
     for (int i = threadIdx.x; i < kRows * BW2; i += kFThreads) sBits[i] = 0u;
     if (threadIdx.x < 8) sScal[threadIdx.x] = 0;
+    __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
     auto grow = [&](int i) -> const uint16_t* {
         return gkb + ((int64_t)sSel[i / M] * M + (i % M)) * DH;
@@ -1797,7 +1844,7 @@ void route_fused_kernel(RouteArgs A) {
         int nv2 = 0;
         float s1 = 0.0f, s2 = 0.0f;
         int ns = 0;
-        fused_scores<DH, 4>(grow, 0, (T2 + 15) / 16, T2, w, nwact, qb, scale, kv2, knmax2, s1, s2, ns);
+        stage_scores<DH, 16>(sStage, 0, 0, T2, w, nwact, qb, scale, kv2, knmax2, s1, s2, ns);
         // candidate c is visible to row t from its parent's first row on
         ns = 0;
 #pragma unroll
@@ -1865,8 +1912,8 @@ void route_fused_kernel(RouteArgs A) {
     if (A.stats && l == 0 && amb2) atomicAdd(&A.stats[2], amb2);
 }
 
-size_t fused_lds(const RouteArgs& a) {
-    return sizeof(uint2) * kRows * kSvStride + sizeof(float) * kRows + 3 * sizeof(int) * kRows +
+size_t fused_lds(const RouteArgs& a, int D) {
+    return 2 * 64 * (size_t)D * 2 + sizeof(uint2) * kRows * kSvStride + sizeof(float) * kRows + 3 * sizeof(int) * kRows +
            sizeof(int) * (2 * kMaxSel + 8 + kRows) + sizeof(float) * 4 +
            2 * sizeof(int) * (size_t)a.SPP + sizeof(uint32_t) * kRows * (size_t)a.BW;
 }
@@ -1994,7 +2041,7 @@ extern "C" int hga_route_prefill(const hga_config* cfg, int32_t S, const void* q
         f.SPP = (Pmax > T2max ? Pmax : T2max) + 1;
         f.BW = (f.SPP + 31) / 32;
         f.BW2 = (T2max + 1 + 31) / 32;
-        const size_t lds = fused_lds(f);
+        const size_t lds = fused_lds(f, D);
         HGA_REQUIRE(lds <= 163840, HGA_ERR_UNSUPPORTED, "hga_route_prefill: %zu bytes of LDS", lds);
         return D == 128 ? launch_route_fused<128>(f, lds, st) : launch_route_fused<64>(f, lds, st);
     }

@@ -3,7 +3,8 @@
 * c3 (Qwen3-30B-A3B layer, 32K prefill): every query chunk's routing pool from 0 to 502 chunks,
   so every stage-1 selection width of the prefill router runs (rows of 1..32 candidates per lane
   of a 16-lane row group); query heads reduced to 4 (one KV head) so the C oracle finishes in
-  seconds.  Lists compared bit for bit in the MFMA-certified and the canonical scoring mode,
+  seconds.  Lists compared bit for bit in the fused and split MFMA-certified kernels and the
+  canonical scoring mode,
   with and without exact ties at the wide pools; attention within the bf16 bar on a few query
   chunks.
 * c5 (batched decode, B64 x 64K, topk 32/128, needle chunks): one decode step for all 64
@@ -85,11 +86,12 @@ def _route_c3(d, ck, gk, o_ck, o_gk):
     stats = torch.zeros(4, dtype=torch.int32, device=DEV)
     r = ops.route_prefill(d["cfg"], q, ck, gk, stats=stats)
     rc = ops.route_prefill(d["cfg"], q, ck, gk, canonical=True)
+    rs = ops.route_prefill(d["cfg"], q, ck, gk, split=True)
     torch.cuda.synchronize()
     o_r = oracle.route_prefill_heads(d["q"].float().numpy(), o_ck, o_gk, c["S"], c["C"], c["gs"],
                                      c["kf"], c["kl"], c["tc"], c["tg"],
                                      oracle.attn_scale(c["Dh"]))
-    for rr in (r, rc):
+    for rr in (r, rc, rs):      # fused, canonical, split
         _same(rr["sel_chunk"].cpu().numpy(), o_r["sel_chunk"])
         _same(rr["sel_thr"].cpu().numpy(), o_r["sel_thr"])
         _same(rr["open_grp"].cpu().numpy(), o_r["open_grp"])

@@ -138,10 +138,11 @@ def test_prefill_bf16_vs_oracle(hga, shape):
     stats = torch.zeros(4, dtype=torch.int32, device=dev)
     r = ops.route_prefill(cfg, q.to(dev), ck, gk, stats=stats)
     rc = ops.route_prefill(cfg, q.to(dev), ck, gk, canonical=True)
+    rs = ops.route_prefill(cfg, q.to(dev), ck, gk, split=True)
     o_r = oracle.route_prefill(f(q), o_ck, o_gk, shape["S"], shape["C"], shape["gs"],
                                shape["kf"], shape["kl"], shape["tc"], shape["tg"],
                                oracle.attn_scale(shape["Dh"]))
-    for rr in (r, rc):
+    for rr in (r, rc, rs):      # fused (where eligible), canonical, split MFMA kernels
         _cmp_sets(rr, o_r["sel_chunk"], o_r["sel_thr"], "sel_chunk", "sel_thr")
         _cmp_sets(rr, o_r["open_grp"], o_r["open_thr"], "open_grp", "open_thr")
     print("ambiguous rows/pools:", stats.cpu().tolist())
@@ -193,9 +194,10 @@ def test_route_exact_ties(hga):
     r = ops.route_prefill(cfg, q.to(dev), ck, gk, stats=stats)
     stats_c = torch.zeros(4, dtype=torch.int32, device=dev)
     rc = ops.route_prefill(cfg, q.to(dev), ck, gk, canonical=True, stats=stats_c)
+    rs = ops.route_prefill(cfg, q.to(dev), ck, gk, split=True)
     f = lambda t: t.float().cpu().numpy()
     o_r = oracle.route_prefill(f(q), f(ck), f(gk), S, C, gs, 1, 1, 4, 8, oracle.attn_scale(Dh))
-    for rr in (r, rc):                   # MFMA-certified and canonical scoring
+    for rr in (r, rc, rs):               # fused MFMA-certified, canonical, split kernels
         _cmp_sets(rr, o_r["sel_chunk"], o_r["sel_thr"], "sel_chunk", "sel_thr")
         _cmp_sets(rr, o_r["open_grp"], o_r["open_thr"], "open_grp", "open_thr")
     print("ambiguous rows/pools:", stats.cpu().tolist(), "canonical:", stats_c.cpu().tolist())
@@ -223,9 +225,10 @@ def test_route_many_ties_full_search(hga):
     stats = torch.zeros(4, dtype=torch.int32, device=dev)
     r = ops.route_prefill(cfg, q.to(dev), ck, gk, stats=stats)
     rc = ops.route_prefill(cfg, q.to(dev), ck, gk, canonical=True)
+    rs = ops.route_prefill(cfg, q.to(dev), ck, gk, split=True)
     f = lambda t: t.float().cpu().numpy()
     o_r = oracle.route_prefill(f(q), f(ck), f(gk), S, C, gs, 1, 1, 16, 64, oracle.attn_scale(Dh))
-    for rr in (r, rc):
+    for rr in (r, rc, rs):
         _cmp_sets(rr, o_r["sel_chunk"], o_r["sel_thr"], "sel_chunk", "sel_thr")
         _cmp_sets(rr, o_r["open_grp"], o_r["open_thr"], "open_grp", "open_thr")
     print("ambiguous rows/pools:", stats.cpu().tolist())
