@@ -560,6 +560,9 @@ struct DecAttnArgs {
     const float* q_dca[3];
     const int32_t* open_pos;
     int dca_chunk;
+    // split kernels: partial slots [0, n1) hold the windows and the active chunk, [n1, n1 + n2)
+    // the opened groups; phase 0 launches all of them, phase 1 the first range, phase 2 the second
+    int phase, n1;
 };
 
 // The key sequence of a decode block for (b, query head): [first window | last window | opened
@@ -571,9 +574,11 @@ struct DecKeys {
     int64_t r_ss, f_ss, d_ss, c0;
     const int *sOG, *sOT, *sOP;
     int a1, a2, a3, a4, C, gs, M, n_closed, l_lo, ring;
+    int n, skip;   // keys of the phase's sequence; phase 1 skips the opened groups, 2 the rest
 
+    // ph: 0 the whole sequence, 1 [first | last | active], 2 [opened]
     __device__ void init(const DecAttnArgs& A, int b, int kvh, const int* og, const int* ot,
-                         int nopen) {
+                         int nopen, int ph = 0) {
         int f_hi;
         windows(A.n_closed, A.kf, A.kl, &f_hi, &l_lo);
         C = A.C; gs = A.gs; M = A.M; n_closed = A.n_closed; ring = A.ring;
@@ -583,6 +588,8 @@ struct DecKeys {
         a2 = a1 + (A.n_closed - l_lo) * C;
         a3 = a2 + nopen * gs;
         a4 = a3 + (int)c0 + A.L;
+        n = ph == 1 ? a4 - (a3 - a2) : (ph == 2 ? a3 - a2 : a4);
+        skip = ph;
         kr = reinterpret_cast<const T*>(A.kr) + b * A.r_sb + kvh * A.r_sh;
         vr = reinterpret_cast<const T*>(A.vr) + b * A.r_sb + kvh * A.r_sh;
         kf = reinterpret_cast<const T*>(A.kfst) + b * A.f_sb + kvh * A.f_sh;
@@ -591,8 +598,11 @@ struct DecKeys {
         vd = reinterpret_cast<const T*>(A.vd) + b * A.d_sb + kvh * A.d_sh;
         r_ss = A.r_ss; f_ss = A.f_ss; d_ss = A.d_ss;
     }
-    // kpos: the key's absolute position (opened groups: from sOP, the groups' own ids)
+    // kpos: the key's absolute position (opened groups: from sOP, the groups' own ids); k is an
+    // index into the phase's sequence (phase 1: [first | last | active], phase 2: [opened])
     __device__ void locate(int k, const T*& kp, const T*& vp, int& thr, int64_t& kpos) const {
+        if (skip == 1 && k >= a2) k += a3 - a2;
+        else if (skip == 2) k += a2;
         if (k < a1) {
             kp = kf + (int64_t)k * f_ss;
             vp = vf + (int64_t)k * f_ss;
@@ -829,6 +839,9 @@ __global__ __launch_bounds__(kDT) void attend_decode_split_kernel(DecAttnArgs A,
     __shared__ int sNopen;
     int split, bh;
     xcd_item(split, bh);
+    const int gsplit = A.phase == 2 ? A.n1 + split : split;           // partial slot
+    const int ph = gsplit < A.n1 ? 1 : 2;
+    split = ph == 1 ? gsplit : gsplit - A.n1;                          // split of the phase
     const int b = bh / A.H, h = bh % A.H;
     const int kvh = h / (A.H / A.KVH);
     const int l = lane_id(), j = l & 15, G = (int)(threadIdx.x >> 4);
@@ -844,7 +857,7 @@ __global__ __launch_bounds__(kDT) void attend_decode_split_kernel(DecAttnArgs A,
     }
     __syncthreads();
     DecKeys<T> keys;
-    keys.init(A, b, kvh, sOG, sOT, sNopen);
+    keys.init(A, b, kvh, sOG, sOT, sNopen, ph);
     if constexpr (DCA) keys.sOP = sOP;
     {
         const int k = split * kSplitKeys + (int)threadIdx.x;
@@ -852,10 +865,10 @@ __global__ __launch_bounds__(kDT) void attend_decode_split_kernel(DecAttnArgs A,
         const T* vp = nullptr;
         int thr = kNoRow;
         int64_t kpos = 0;
-        if (k < keys.a4) keys.locate(k, kp, vp, thr, kpos);
+        if (k < keys.n) keys.locate(k, kp, vp, thr, kpos);
         sKP[threadIdx.x] = (unsigned long long)kp;
         sVP[threadIdx.x] = (unsigned long long)vp;
-        sKT[threadIdx.x] = k < keys.a4 ? thr : kNoRow;
+        sKT[threadIdx.x] = k < keys.n ? thr : kNoRow;
         if constexpr (DCA) sKX[threadIdx.x] = (int)kpos;
     }
     __syncthreads();
@@ -888,7 +901,7 @@ __global__ __launch_bounds__(kDT) void attend_decode_split_kernel(DecAttnArgs A,
                 int64_t kpos = 0;
                 if constexpr (DCA) kpos = sKX[kl];
                 float d = 0.0f;
-                const bool vis = k < keys.a4 && row >= thr;
+                const bool vis = k < keys.n && row >= thr;
                 if (vis) {
                     float kx[DPL];
                     load_slice<DT, DPL>(kp + j * DPL, kx);
@@ -937,7 +950,7 @@ __global__ __launch_bounds__(kDT) void attend_decode_split_kernel(DecAttnArgs A,
         for (int e = 0; e < DPL; ++e) sAcc[G][j * DPL + e] = acc[e];
         __syncthreads();
         // merge the 16 groups: partial of this split for this row
-        float* pp = part + (((int64_t)bh * A.L + row) * nsplit + split) * (DH + 2);
+        float* pp = part + (((int64_t)bh * A.L + row) * nsplit + gsplit) * (DH + 2);
         float mt = -INFINITY;
         for (int g = 0; g < NG; ++g) mt = fmaxf(mt, sM[g]);
         const float mu = mt == -INFINITY ? 0.0f : mt;
@@ -991,6 +1004,9 @@ __global__ __launch_bounds__(kDMT) void attend_decode_mfma_kernel(DecAttnArgs A,
     extern __shared__ __align__(16) uint16_t sQd[];   // DCA: [version][hi, lo][64 rows][QSTR]
     int split, bh;
     xcd_item(split, bh);
+    const int gsplit = A.phase == 2 ? A.n1 + split : split;           // partial slot
+    const int ph = gsplit < A.n1 ? 1 : 2;
+    split = ph == 1 ? gsplit : gsplit - A.n1;                          // split of the phase
     const int b = bh / A.H, h = bh % A.H;
     const int kvh = h / (A.H / A.KVH);
     const int w = threadIdx.x / kWave, l = lane_id(), hl = l / 32;
@@ -1007,7 +1023,7 @@ __global__ __launch_bounds__(kDMT) void attend_decode_mfma_kernel(DecAttnArgs A,
     }
     __syncthreads();
     DecKeys<T> keys;
-    keys.init(A, b, kvh, sOG, sOT, sNopen);
+    keys.init(A, b, kvh, sOG, sOT, sNopen, ph);
     if constexpr (DCA) keys.sOP = sOP;
     for (int t = threadIdx.x; t < kSplitKeys; t += kDMT) {
         const int k = split * kSplitKeys + t;
@@ -1015,7 +1031,7 @@ __global__ __launch_bounds__(kDMT) void attend_decode_mfma_kernel(DecAttnArgs A,
         const T* vp = nullptr;
         int thr = kNoRow;
         int64_t kpos = 0;
-        if (k < keys.a4) keys.locate(k, kp, vp, thr, kpos);
+        if (k < keys.n) keys.locate(k, kp, vp, thr, kpos);
         sKP[t] = (unsigned long long)kp;
         sVP[t] = (unsigned long long)vp;
         sKT[t] = kp ? thr : kNoRow;
@@ -1049,7 +1065,7 @@ __global__ __launch_bounds__(kDMT) void attend_decode_mfma_kernel(DecAttnArgs A,
     for (int d = 0; d < DB; ++d) acc[d] = floatx16_t{};
     float m_run = -INFINITY, l_run = 0.0f;
     const float c2 = A.scale * 1.4426950408889634f;
-    const int nk = min(kSplitKeys, keys.a4 - split * kSplitKeys);
+    const int nk = min(kSplitKeys, keys.n - split * kSplitKeys);
     for (int t0 = 0; t0 < nk; t0 += kDMK) {
         const uint4 z = make_uint4(0u, 0u, 0u, 0u);
         for (int c = threadIdx.x; c < kDMK * CPR; c += kDMT) {
@@ -1153,7 +1169,7 @@ __global__ __launch_bounds__(kDMT) void attend_decode_mfma_kernel(DecAttnArgs A,
         __syncthreads();
     }
     if (row < A.L) {
-        float* pp = part + (((int64_t)bh * A.L + row) * nsplit + split) * (DH + 2);
+        float* pp = part + (((int64_t)bh * A.L + row) * nsplit + gsplit) * (DH + 2);
         if (hl == 0) {
             pp[0] = m_run == -INFINITY ? -INFINITY : m_run * 0.6931471805599453f;
             pp[1] = l_run;
@@ -1273,21 +1289,49 @@ __global__ __launch_bounds__(kGT) void gather_plan_kernel(GatherArgs A) {
 
 // One workgroup per (staging slot, kv head, b): copies the group's gs K rows and gs V rows
 // (contiguous in a [.., T, D] record) with 16-byte accesses; slots past the count exit.
+// Persistent copy: workgroup w takes staging slots w, w + G, w + 2G, .. of every (b, kv head),
+// four slots in flight per thread.  A small grid (kGatherWG workgroups) leaves the other CUs to
+// the attention that runs beside the copy on another stream.
+constexpr int kGatherWG = 128;
 __global__ __launch_bounds__(kGT) void gather_copy_kernel(GatherArgs A) {
-    const int u = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
-    const int bk = b * A.KVH + kvh;
-    if (u >= A.ucount[bk]) return;
-    const int g = A.ulist[(int64_t)bk * A.U + u];
-    const int64_t p0 = (int64_t)(g / A.M) * A.C + (int64_t)(g % A.M) * A.gs;
-    const int64_t src = ((int64_t)b * A.d_sb + (int64_t)kvh * A.d_sh + p0 * A.d_ss) * A.esz;
-    const int64_t dst = (((int64_t)bk * A.U + u) * A.gs) * (int64_t)A.D * A.esz;
+    const int G = gridDim.x;
     const int vpr = A.D * A.esz / 16;                  // 16-byte pieces per row
-    for (int c = threadIdx.x; c < A.gs * vpr; c += kGT) {
-        const int r = c / vpr, x = (c % vpr) * 16;
-        const int64_t so = src + (int64_t)r * A.d_ss * A.esz + x;
-        const int64_t dO = dst + (int64_t)r * A.D * A.esz + x;
-        *reinterpret_cast<uint4*>(A.stage_k + dO) = *reinterpret_cast<const uint4*>(A.kd + so);
-        *reinterpret_cast<uint4*>(A.stage_v + dO) = *reinterpret_cast<const uint4*>(A.vd + so);
+    const int pieces = A.gs * vpr;                     // of one group's K (or V)
+    for (int bk = 0; bk < A.B * A.KVH; ++bk) {
+        const int cnt = A.ucount[bk];
+        const int b = bk / A.KVH, kvh = bk % A.KVH;
+        const int64_t rec = ((int64_t)b * A.d_sb + (int64_t)kvh * A.d_sh) * A.esz;
+        for (int u0 = blockIdx.x; u0 < cnt; u0 += 4 * G) {
+            int64_t src[4], dst[4];
+            bool ok[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int u = u0 + j * G;
+                ok[j] = u < cnt;
+                const int g = ok[j] ? A.ulist[(int64_t)bk * A.U + u] : 0;
+                const int64_t p0 = (int64_t)(g / A.M) * A.C + (int64_t)(g % A.M) * A.gs;
+                src[j] = rec + p0 * A.d_ss * A.esz;
+                dst[j] = (((int64_t)bk * A.U + u) * A.gs) * (int64_t)A.D * A.esz;
+            }
+            for (int c = threadIdx.x; c < pieces; c += kGT) {
+                const int r = c / vpr, x = (c % vpr) * 16;
+                const int64_t so = (int64_t)r * A.d_ss * A.esz + x;
+                const int64_t dO = (int64_t)r * A.D * A.esz + x;
+                uint4 kq[4], vq[4];
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    if (ok[j]) {
+                        kq[j] = *reinterpret_cast<const uint4*>(A.kd + src[j] + so);
+                        vq[j] = *reinterpret_cast<const uint4*>(A.vd + src[j] + so);
+                    }
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    if (ok[j]) {
+                        *reinterpret_cast<uint4*>(A.stage_k + dst[j] + dO) = kq[j];
+                        *reinterpret_cast<uint4*>(A.stage_v + dst[j] + dO) = vq[j];
+                    }
+            }
+        }
     }
 }
 
@@ -1295,18 +1339,21 @@ __global__ __launch_bounds__(kGT) void gather_copy_kernel(GatherArgs A) {
 }  // namespace hga
 
 namespace {
-// Splits of the split decode attention: the longest key sequence a head of the block can have
-// (every opened slot valid) in kSplitKeys pieces.
+// Splits (kSplitKeys keys each) of the split decode attention: phase 1 the windows and the
+// active chunk, phase 2 the opened groups of the longest list (every slot valid), phase 0 both;
+// the workspace holds the partials of all of them.
 int decode_splits(const hga_config* cfg, int32_t L, int32_t n_closed, int64_t start_pos,
-                  int32_t Kg) {
+                  int32_t Kg, int phase) {
     int f_hi, l_lo;
     hga::windows(n_closed, cfg->keep_first, cfg->keep_last, &f_hi, &l_lo);
     const int64_t C = cfg->chunk_size;
     const int64_t c0 = start_pos - (int64_t)n_closed * C;
-    const int64_t keys = (int64_t)f_hi * C + (int64_t)(n_closed - l_lo) * C +
-                         (int64_t)(Kg > 0 ? Kg : 0) * cfg->group_size + c0 + L;
-    const int64_t n = (keys + hga::kSplitKeys - 1) / hga::kSplitKeys;
-    return (int)(n > 0 ? n : 1);
+    const int64_t win = (int64_t)f_hi * C + (int64_t)(n_closed - l_lo) * C + c0 + L;
+    const int64_t opened = (int64_t)(Kg > 0 ? Kg : 0) * cfg->group_size;
+    auto splits = [](int64_t keys) { return (keys + hga::kSplitKeys - 1) / hga::kSplitKeys; };
+    if (phase == 1) return (int)splits(win);
+    if (phase == 2) return (int)splits(opened);
+    return (int)(splits(win) + splits(opened));
 }
 }  // namespace
 
@@ -1320,7 +1367,7 @@ extern "C" int32_t hga_attend_decode_workspace(const hga_config* cfg, int32_t L,
     const int D = cfg->head_dim;
     *bytes = (D == 64 || D == 128)
                  ? 4 * (int64_t)cfg->batch * cfg->heads * L *
-                       decode_splits(cfg, L, n_closed, start_pos, Kg) * (D + 2)
+                       decode_splits(cfg, L, n_closed, start_pos, Kg, 0) * (D + 2)
                  : 0;
     return HGA_OK;
 }
@@ -1399,7 +1446,7 @@ extern "C" int hga_gather_decode(const hga_config* cfg, int32_t n_closed, const 
     rc = launch_status("hga_gather_decode (plan)");
     if (rc) return rc;
     if (Kg == 0 || n_closed == 0) return HGA_OK;
-    gather_copy_kernel<<<dim3((unsigned)a.U, (unsigned)a.KVH, (unsigned)a.B), dim3(kGT), 0, st>>>(a);
+    gather_copy_kernel<<<dim3((unsigned)kGatherWG), dim3(kGT), 0, st>>>(a);
     return launch_status("hga_gather_decode (copy)");
 }
 
@@ -1593,9 +1640,12 @@ int attend_decode_impl(const hga_config* cfg, int32_t L, int32_t n_closed, int64
                        int64_t d_ss, int32_t record_on_host, const int32_t* open_grp,
                        const int32_t* open_thr, int32_t Kg, void* out, int64_t o_sb,
                        int64_t o_sh, int64_t o_ss, void* workspace, int64_t workspace_bytes,
-                       void* stream) {
+                       void* stream, int32_t phase = 0) {
     int rc = check_config(cfg);
     if (rc) return rc;
+    HGA_REQUIRE(phase >= 0 && phase <= 2, HGA_ERR_ARG, "hga_attend_decode_phase: phase %d", phase);
+    HGA_REQUIRE(phase == 0 || cfg->head_dim == 64 || cfg->head_dim == 128, HGA_ERR_UNSUPPORTED,
+                "hga_attend_decode_phase: phases need head_dim 64 or 128");
     HGA_REQUIRE((q || q_dca) && k_recent && v_recent && out && open_grp && open_thr, HGA_ERR_ARG,
                 "hga_attend_decode: NULL pointer");
     HGA_REQUIRE(L >= 1 && L <= kMaxL && n_closed >= 0 && Kg >= 0 && Kg <= 256 && ring_chunks >= 0,
@@ -1654,19 +1704,28 @@ int attend_decode_impl(const hga_config* cfg, int32_t L, int32_t n_closed, int64
                 HGA_ERR_ARG, "hga_attend_decode: 16-byte aligned key rows required");
     hipStream_t st = (hipStream_t)stream;
     if (D == 64 || D == 128) {
-        const int nsplit = decode_splits(cfg, L, n_closed, start_pos, Kg);
+        // phase 0: one launch over all keys; phases 1 and 2: the windows and active chunk into
+        // partial slots [0, n1), the opened groups into [n1, n1 + n2), then the combine
+        const int n1 = decode_splits(cfg, L, n_closed, start_pos, Kg, 1);
+        const int n2 = decode_splits(cfg, L, n_closed, start_pos, Kg, 2);
+        const int nsplit = n1 + n2;
         const int64_t need = 4 * (int64_t)a.B * a.H * L * nsplit * (D + 2);
         HGA_REQUIRE(workspace && workspace_bytes >= need, HGA_ERR_ARG,
                     "hga_attend_decode: workspace of %lld bytes required (got %lld)",
                     (long long)need, (long long)workspace_bytes);
         float* part = static_cast<float*>(workspace);
-        const dim3 g1((unsigned)nsplit, (unsigned)(a.B * a.H)), g2((unsigned)(a.B * a.H * L));
+        a.phase = phase;
+        a.n1 = n1;
+        const int nlaunch = phase == 0 ? nsplit : (phase == 1 ? n1 : n2);
+        const dim3 g1((unsigned)(nlaunch > 0 ? nlaunch : 1), (unsigned)(a.B * a.H)),
+            g2((unsigned)(a.B * a.H * L));
         // blocks of 8+ rows (bf16, aligned query rows): the MFMA split kernel
         const bool mfma = cfg->dtype == HGA_DTYPE_BF16 && L >= 8 &&
                           (dca || ((uintptr_t)q % 16 == 0 && ((q_sb | q_sh | q_ss) % 8) == 0));
 #define HGA_DS_CASE(DTV, DHV)                                                                    \
         if (cfg->dtype == DTV && D == DHV) {                                                   \
-            if (mfma && DTV == HGA_DTYPE_BF16 && dca) {                                         \
+            if (nlaunch == 0) {                                                                 \
+            } else if (mfma && DTV == HGA_DTYPE_BF16 && dca) {                                  \
                 static bool attr = false;                                                       \
                 if (!attr) {                                                                    \
                     (void)hipFuncSetAttribute((const void*)attend_decode_mfma_kernel<DHV, true>, \
@@ -1682,6 +1741,7 @@ int attend_decode_impl(const hga_config* cfg, int32_t L, int32_t n_closed, int64
             else attend_decode_split_kernel<DTV, DHV, false><<<g1, kDT, 0, st>>>(a, part, nsplit); \
             rc = launch_status("hga_attend_decode (split)");                                    \
             if (rc) return rc;                                                                  \
+            if (phase == 1) return HGA_OK;                                                      \
             decode_combine_kernel<DTV, DHV><<<g2, 128, 0, st>>>(a, part, nsplit);               \
             return launch_status("hga_attend_decode (combine)");                                \
         }
@@ -1730,6 +1790,26 @@ extern "C" int hga_attend_decode(const hga_config* cfg, int32_t L, int32_t n_clo
                                    k_first, v_first, f_sb, f_sh, f_ss, k_record, v_record, d_sb,
                                    d_sh, d_ss, record_on_host, open_grp, open_thr, Kg, out, o_sb,
                                    o_sh, o_ss, workspace, workspace_bytes, stream);
+}
+
+extern "C" int hga_attend_decode_phase(const hga_config* cfg, int32_t L, int32_t n_closed,
+                                       int64_t start_pos, const void* q, int64_t q_sb,
+                                       int64_t q_sh, int64_t q_ss, const void* k_recent,
+                                       const void* v_recent, int64_t r_sb, int64_t r_sh,
+                                       int64_t r_ss, int32_t ring_chunks, const void* k_first,
+                                       const void* v_first, int64_t f_sb, int64_t f_sh,
+                                       int64_t f_ss, const void* k_record, const void* v_record,
+                                       int64_t d_sb, int64_t d_sh, int64_t d_ss,
+                                       int32_t record_on_host, const int32_t* open_grp,
+                                       const int32_t* open_thr, int32_t Kg, void* out,
+                                       int64_t o_sb, int64_t o_sh, int64_t o_ss, int32_t phase,
+                                       void* workspace, int64_t workspace_bytes, void* stream) {
+    HGA_REQUIRE(q, HGA_ERR_ARG, "hga_attend_decode_phase: NULL pointer");
+    return hga::attend_decode_impl(cfg, L, n_closed, start_pos, q, q_sb, q_sh, q_ss, nullptr,
+                                   nullptr, 0, k_recent, v_recent, r_sb, r_sh, r_ss, ring_chunks,
+                                   k_first, v_first, f_sb, f_sh, f_ss, k_record, v_record, d_sb,
+                                   d_sh, d_ss, record_on_host, open_grp, open_thr, Kg, out, o_sb,
+                                   o_sh, o_ss, workspace, workspace_bytes, stream, phase);
 }
 
 extern "C" int hga_attend_decode_dca(const hga_config* cfg, int32_t L, int32_t n_closed,

@@ -421,11 +421,36 @@ def write_tokens(cfg: HgaConfig, L: int, pairs) -> None:
           "hga_write_tokens")
 
 
+def attend_decode_workspace(cfg: HgaConfig, L: int, n_closed: int, start_pos: int, Kg: int,
+                            device) -> torch.Tensor:
+    """A workspace for hga_attend_decode / hga_attend_decode_phase (bytes)."""
+    nb = ctypes.c_int64()
+    check(lib().hga_attend_decode_workspace(ctypes.byref(cfg), L, n_closed, start_pos, Kg,
+                                            ctypes.byref(nb)), "hga_attend_decode_workspace")
+    return torch.empty(max(nb.value, 16), dtype=torch.uint8, device=device)
+
+
+_SIDE = {}
+
+
+def side_stream(device):
+    """(stream, event, event) per device: a second stream (default priority) for copies that
+    overlap compute, and two reusable events to order it against the compute stream."""
+    key = torch.device(device).index if torch.device(device).index is not None else \
+        torch.cuda.current_device()
+    st = _SIDE.get(key)
+    if st is None:
+        st = (torch.cuda.Stream(device=key), torch.cuda.Event(), torch.cuda.Event())
+        _SIDE[key] = st
+    return st
+
+
 def attend_decode(cfg: HgaConfig, q: torch.Tensor, n_closed: int, start_pos: int,
                   recent_k: torch.Tensor, recent_v: torch.Tensor, ring_chunks: int,
                   first_k, first_v, record_k, record_v, record_on_host: bool,
                   open_grp: torch.Tensor, open_thr: torch.Tensor, Kg: int,
-                  out: torch.Tensor | None = None, dca: dict | None = None) -> torch.Tensor:
+                  out: torch.Tensor | None = None, dca: dict | None = None, phase: int = 0,
+                  workspace: torch.Tensor | None = None) -> torch.Tensor:
     """Decode attention of q [B,H,L,Dh] (rows at start_pos..start_pos+L-1).  Token sources are
     [B,KVH,T,Dh] views: ``recent`` (positions >= the last window, optionally a ring of
     ring_chunks chunks), ``first`` (the first window) and ``record`` (the closed-token record
@@ -434,7 +459,11 @@ def attend_decode(cfg: HgaConfig, q: torch.Tensor, n_closed: int, start_pos: int
     ``dca`` selects Dual Chunk Attention: q is then the fp32 intra version and ``dca`` holds
     ``q_succ``/``q_inter`` (fp32, q's shape and strides), ``chunk`` (the DCA chunk length) and
     ``open_pos`` (the opened groups' own ids when open_grp indexes a staging record, else None);
-    the output has the keys' dtype."""
+    the output has the keys' dtype.
+
+    ``phase`` 1 attends the windows and the active chunk into ``workspace`` (the record is not
+    read), phase 2 (same workspace) the opened groups, and writes ``out``
+    (hga_attend_decode_phase); 0 does both in one call."""
     _dev(q, recent_k, recent_v, open_grp, open_thr)
     B, H, L, D = q.shape
     if out is None:
@@ -453,13 +482,19 @@ def attend_decode(cfg: HgaConfig, q: torch.Tensor, n_closed: int, start_pos: int
             raise ValueError("K and V of a source must share strides")
     og = open_grp.contiguous()
     ot = open_thr.contiguous()
-    nb = ctypes.c_int64()
-    check(lib().hga_attend_decode_workspace(ctypes.byref(cfg), L, n_closed, start_pos, Kg,
-                                            ctypes.byref(nb)), "hga_attend_decode_workspace")
-    ws = torch.empty(max(nb.value, 16), dtype=torch.uint8, device=q.device)
+    ws = workspace if workspace is not None else attend_decode_workspace(
+        cfg, L, n_closed, start_pos, Kg, q.device)
     src = (_p(recent_k), _p(recent_v), *_s4(recent_k), ring_chunks, _p(first_k), _p(first_v),
            *_s4(first_k), _p(record_k), _p(record_v), *_s4(record_k),
            1 if record_on_host else 0)
+    if phase:
+        if dca is not None:
+            raise ValueError("phased decode attention is not available for DCA")
+        check(lib().hga_attend_decode_phase(
+            ctypes.byref(cfg), L, n_closed, start_pos, _p(q), *_s4(q), *src, _p(og), _p(ot), Kg,
+            _p(out), *_s4(out), int(phase), _p(ws), ws.numel(), _stream()),
+            "hga_attend_decode_phase")
+        return out
     if dca is None:
         check(lib().hga_attend_decode(
             ctypes.byref(cfg), L, n_closed, start_pos, _p(q), *_s4(q), *src, _p(og), _p(ot), Kg,

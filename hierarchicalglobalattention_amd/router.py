@@ -547,15 +547,38 @@ class RoutedKV:
         staging = src.pop("staging", None)
         resolve = src.pop("resolve", None)
         og = r["open_grp"]
-        if staging is not None:
-            # host record (or its page cache): gather the opened groups into device staging
-            og_rec, n_rec, rk, rv = (resolve(og) if resolve is not None else
-                                     (og, self.n_closed, src["record_k"], src["record_v"]))
-            sk, sv, og = ops.gather_decode(self.hcfg, n_rec, og_rec, r["open_thr"], r["Kg"], rk,
+        if staging is None:
+            return ops.attend_decode(self.hcfg, q, self.n_closed, self.start_pos, open_grp=og,
+                                     open_thr=r["open_thr"], Kg=r["Kg"], **src)
+        # host record (or its page cache): the opened groups are copied into device staging on a
+        # side stream while the windows and the active chunk are attended on this one
+        # (the reference's non-blocking group copy, ram_kv_cache_store.py:578-607)
+        og_rec, n_rec, rk, rv = (resolve(og) if resolve is not None else
+                                 (og, self.n_closed, src["record_k"], src["record_v"]))
+        if self.hcfg.head_dim not in (64, 128):
+            # the split kernels (and their phases) cover head_dim 64 and 128 only
+            sk, sv, sg = ops.gather_decode(self.hcfg, n_rec, og_rec, r["open_thr"], r["Kg"], rk,
                                            rv, src["record_on_host"], staging, q.shape[1])
             src.update(record_k=sk, record_v=sv, record_on_host=False)
-        return ops.attend_decode(self.hcfg, q, self.n_closed, self.start_pos, open_grp=og,
-                                 open_thr=r["open_thr"], Kg=r["Kg"], **src)
+            return ops.attend_decode(self.hcfg, q, self.n_closed, self.start_pos, open_grp=sg,
+                                     open_thr=r["open_thr"], Kg=r["Kg"], **src)
+        main = torch.cuda.current_stream(q.device)
+        side, ready, copied = ops.side_stream(q.device)
+        ready.record(main)                      # routing lists, ring and record writes
+        side.wait_event(ready)
+        with torch.cuda.stream(side):
+            sk, sv, sg = ops.gather_decode(self.hcfg, n_rec, og_rec, r["open_thr"], r["Kg"], rk,
+                                           rv, src["record_on_host"], staging, q.shape[1])
+        copied.record(side)
+        src.update(record_k=sk, record_v=sv, record_on_host=False)
+        ws = ops.attend_decode_workspace(self.hcfg, q.shape[2], self.n_closed, self.start_pos,
+                                         r["Kg"], q.device)
+        out = ops.attend_decode(self.hcfg, q, self.n_closed, self.start_pos, open_grp=og,
+                                open_thr=r["open_thr"], Kg=r["Kg"], phase=1, workspace=ws, **src)
+        main.wait_event(copied)
+        return ops.attend_decode(self.hcfg, q, self.n_closed, self.start_pos, open_grp=sg,
+                                 open_thr=r["open_thr"], Kg=r["Kg"], out=out, phase=2,
+                                 workspace=ws, **src)
 
     def attend_dca(self, q_intra: torch.Tensor, q_succ: torch.Tensor, q_inter: torch.Tensor,
                    dca_chunk: int) -> torch.Tensor:

@@ -247,6 +247,28 @@ int hga_attend_decode(const hga_config* cfg, int32_t L, int32_t n_closed, int64_
                       void* stream);
 
 /*
+ * hga_attend_decode in two launches, so that the opened groups can be copied from the host
+ * record while the windows are attended (the reference starts the non-blocking group copy,
+ * ram_kv_cache_store.py:578-607, before the attention that needs it, chunk_router.py:251-252).
+ * phase 1 attends the first window, the last window and the active chunk into the workspace
+ * (open_grp/open_thr only give each head's opened-list length; the record is not read); phase 2
+ * -- later on the stream, or after an event, with the same arguments and workspace except that
+ * open_grp and the record may be hga_gather_decode's staging -- attends the opened groups and
+ * writes out.  phase 0 is hga_attend_decode.  head_dim 64 or 128.  Same workspace size
+ * (hga_attend_decode_workspace).
+ */
+int hga_attend_decode_phase(const hga_config* cfg, int32_t L, int32_t n_closed, int64_t start_pos,
+                            const void* q, int64_t q_sb, int64_t q_sh, int64_t q_ss,
+                            const void* k_recent, const void* v_recent, int64_t r_sb,
+                            int64_t r_sh, int64_t r_ss, int32_t ring_chunks, const void* k_first,
+                            const void* v_first, int64_t f_sb, int64_t f_sh, int64_t f_ss,
+                            const void* k_record, const void* v_record, int64_t d_sb,
+                            int64_t d_sh, int64_t d_ss, int32_t record_on_host,
+                            const int32_t* open_grp, const int32_t* open_thr, int32_t Kg,
+                            void* out, int64_t o_sb, int64_t o_sh, int64_t o_ss, int32_t phase,
+                            void* workspace, int64_t workspace_bytes, void* stream);
+
+/*
  * Dual Chunk Attention decode (QwenRoutedAttention._dca_attend,
  * Qwen3LongContext/qwen_routed_attention.py:244-283): the same key sequence and visibility as
  * hga_attend_decode over keys stored RoPE'd at pos % dca_chunk.  Key p is scored against

@@ -454,3 +454,46 @@ def test_write_tokens_rejects_mismatches():
         ops.write_tokens(cfg, 3, [(a, a)])
     with pytest.raises(RuntimeError):
         ops.write_tokens(cfg, 4, [(a.cpu(), a)])
+
+
+@pytest.mark.parametrize("case", [c for c in ATTN_CASES if c[3] in (64, 128)],
+                         ids=lambda c: f"B{c[0]}n{c[10]}c{c[11]}L{c[12]}"
+                         f"{'bf16' if c[13] is torch.bfloat16 else 'f32'}")
+def test_attend_decode_phases_equal_one_launch(case):
+    """hga_attend_decode_phase: the windows and active chunk (phase 1) while the opened groups
+    are gathered into device staging, then the opened groups (phase 2) from the staging --
+    bit-identical to the one-launch attention over the host record (same split partition and
+    combine)."""
+    B, H, KVH, Dh, C, gs, tc, tg, kf, kl, n_closed, c0, L, dt = case
+    print(f"[decode] phases {case}", flush=True)
+    M = C // gs
+    gen = torch.Generator().manual_seed(n_closed * 5 + c0 + 1)
+    start = n_closed * C + c0
+    T = start + L
+    k, v = _history(gen, B, KVH, T, Dh, dt)
+    q = torch.randn(B, H, L, Dh, generator=gen).to(dt).to(DEV)
+    cfg = _cfg(B, H, KVH, Dh, C, gs, tc, tg, kf, kl, dt)
+    if n_closed:
+        ck, gk = _summaries(gen, B, KVH, n_closed, M, Dh, dt)
+        r = ops.route_decode(cfg, q, ck.to(DEV), gk.to(DEV), n_closed)
+        og, ot, Kg = r["open_grp"], r["open_thr"], r["Kg"]
+    else:
+        og = ot = torch.full((B, H, 1), -1, dtype=torch.int32, device=DEV)
+        Kg = 0
+    R = kl + 3
+    rk, rv = _ring(k, n_closed, C, kf, kl, R).to(DEV), _ring(v, n_closed, C, kf, kl, R).to(DEV)
+    fk = k[:, :, :max(kf, 1) * C].contiguous().to(DEV)
+    fv = v[:, :, :max(kf, 1) * C].contiguous().to(DEV)
+    hk = torch.zeros(B, KVH, (n_closed + 1) * C, Dh, dtype=dt, pin_memory=True)
+    hv = torch.zeros_like(hk).pin_memory()
+    hk[:, :, :n_closed * C] = k[:, :, :n_closed * C]
+    hv[:, :, :n_closed * C] = v[:, :, :n_closed * C]
+    one = ops.attend_decode(cfg, q, n_closed, start, rk, rv, R, fk, fv, hk, hv, True, og, ot, Kg)
+    staged = ops.gather_decode(cfg, n_closed, og, ot, Kg, hk, hv, True, ops.DecodeStaging(), H)
+    ws = ops.attend_decode_workspace(cfg, L, n_closed, start, Kg, q.device)
+    out = ops.attend_decode(cfg, q, n_closed, start, rk, rv, R, fk, fv, staged[0], staged[1],
+                            False, og, ot, Kg, phase=1, workspace=ws)
+    out = ops.attend_decode(cfg, q, n_closed, start, rk, rv, R, fk, fv, staged[0], staged[1],
+                            False, staged[2], ot, Kg, out=out, phase=2, workspace=ws)
+    torch.cuda.synchronize()
+    assert torch.equal(out, one)
