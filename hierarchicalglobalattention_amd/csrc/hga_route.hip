@@ -51,6 +51,7 @@ struct RouteArgs {
     int32_t *sel_chunk, *sel_thr, *n_sel, *open_grp, *open_thr, *n_open;
     int32_t* stats;
     int B, H, KVH, S, N, C, M, kf, kl, Kc, Kg, Kgr;
+    int n_hi;                // fused launches: query chunks n_hi - 1, n_hi - 2, ... of the grid
     int SP, SP2, SSZ, SPP, BW, SPP2, BW2, VT2, canonical;
     float scale;
 };
@@ -1143,6 +1144,12 @@ void route_stage2_kernel(RouteArgs A) {
 // canonical re-rank of uncertain rows are as in the split kernels, except that an uncertain row
 // is rescored canonically in full.  Pooling, the pooled selection and stage 2 follow the split
 // kernels' rules.
+//
+// Pools of more than 512 chunks (the LONG variant, launched for those query chunks only) take
+// more segments; between segments a row list longer than 32 is cut back to its entries with
+// key >= x, x its 32nd largest key (its (k+1)-th where ties at the 32nd would keep more), so
+// the list still holds every candidate with key >= the largest threshold applied to the row,
+// and at least k + 1 of them.
 // ==========================================================================================
 constexpr int kFThreads = 256;
 constexpr int kFWaves = kFThreads / kWave;
@@ -1150,7 +1157,8 @@ constexpr int kSegTiles = 16;             // 16-candidate tiles per stage-1 segm
 constexpr int kSegCand = 16 * kSegTiles;  // 256
 constexpr int kSurv = 32;                 // survivors per row and segment
 constexpr int kSvStride = 66;             // survivor list slots per row: 2 x 32, padded (bank spread)
-constexpr int kFusedMaxPool = 2 * kSegCand;
+constexpr int kFusedMaxPool = 2 * kSegCand;       // pools of the ordinary variant
+constexpr int kFusedMaxPoolLong = 8 * kSegCand;   // pools of the LONG variant (2048 chunks)
 constexpr int kFusedMaxT2 = 64;
 
 typedef float floatx4 __attribute__((ext_vector_type(4)));
@@ -1421,6 +1429,53 @@ __device__ __forceinline__ void list_rows(int w, int k, float dsc, const float* 
     }
 }
 
+// LONG pools, between segments: the wave's rows t with sRowN[t] > 0 (their list length, more
+// than kSurv) cut their survivor lists back to the entries with key >= x, four rows per pass on
+// the 16-lane DPP rows; x is the row's 32nd largest key, or its (k+1)-th largest where more than
+// 32 entries tie at the 32nd.  sRowN[t] becomes the new length (-2: more than 32 entries even at
+// the (k+1)-th key) and sRowT[t] = x.
+__device__ __forceinline__ void fused_merge(int w, int k, uint2* sSv, int* sRowN, uint32_t* sRowT) {
+    const int l = lane_id(), seg = l & 15;
+    const uint64_t gm = 0xffffull << (l & 48);           // this lane's DPP row
+    const uint64_t below = gm & ((1ull << l) - 1ull);
+    for (int p = 0; p < 4; ++p) {
+        const int t = 16 * w + 4 * p + l / 16;
+        const int ns = sRowN[t];
+        if (__ballot(ns > 0) == 0ull) continue;          // wave-uniform
+        uint2* rowbuf = sSv + t * kSvStride;
+        uint2 e[4];
+        uint32_t R[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int x = 4 * seg + r;
+            e[r] = x < ns ? rowbuf[x] : make_uint2(0u, 0u);
+            R[r] = e[r].x;
+        }
+        sort64_row(R, seg);                               // ascending: position 64 - j = j-th largest
+        const uint32_t x32 = r16_umax(seg == 8 ? R[0] : 0u);
+        const int ek1 = 63 - k;
+        const uint32_t vk1 = (ek1 & 3) == 0 ? R[0] : (ek1 & 3) == 1 ? R[1] : (ek1 & 3) == 2 ? R[2] : R[3];
+        const uint32_t k1th = r16_umax(seg == (ek1 >> 2) ? vk1 : 0u);
+        int c32 = 0;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) c32 += e[r].x >= x32 && e[r].x != 0u ? 1 : 0;
+        c32 = r16_sum(c32);
+        const uint32_t x = c32 <= kSurv ? x32 : k1th;
+        int pos = 0;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const bool in = ns > 0 && e[r].x >= x && e[r].x != 0u;
+            const uint64_t bal = __ballot(in);
+            if (in) rowbuf[pos + __popcll(bal & below)] = e[r];
+            pos += __popcll(bal & gm);
+        }
+        if (seg == 0 && ns > 0) {
+            sRowN[t] = pos > kSurv ? -2 : pos;
+            sRowT[t] = x;
+        }
+    }
+}
+
 // Canonical re-rank of an uncertain stage-1 row t from its survivor list (one wave): every
 // survivor whose MFMA key is >= band (which holds every candidate that can be among the row's
 // canonical top k: those have MFMA scores >= kth - 2 delta) is rescored with the canonical chain;
@@ -1448,7 +1503,7 @@ __device__ __noinline__ void fused_canon_band(int t, int k, uint32_t band, const
 // rescored with the canonical chain, one dot product at a time, and the exact top-k requested.
 // Candidate i is row kb + i*DH (stage 1, sel == nullptr) or group sel[i/M]*M + i%M of kb
 // (stage 2, visible to row t iff thr[i/M] <= t).  Returns the number of rows this wave took.
-template <int DH>
+template <int DH, int JMAX = 8>
 __device__ __noinline__ int fused_canon_rows(int w, int namb, const int* sAmb, int ncand, int k,
                                              const uint16_t* qg, int64_t q_ss, const uint16_t* kb,
                                              const int* sel, int M, const int* thr, float scale,
@@ -1458,7 +1513,7 @@ __device__ __noinline__ int fused_canon_rows(int w, int namb, const int* sAmb, i
     auto row_of = [&](int i) -> const uint16_t* {
         return sel ? kb + ((int64_t)sel[i / M] * M + (i % M)) * DH : kb + (int64_t)i * DH;
     };
-    dispatch_j(ncand, [&](auto jt) {
+    dispatch_j<JMAX>(ncand, [&](auto jt) {
         constexpr int J = decltype(jt)::value;
         for (int a = w; a < namb; a += kFWaves) {
             const int ta = sAmb[a];
@@ -1479,6 +1534,45 @@ __device__ __noinline__ int fused_canon_rows(int w, int namb, const int* sAmb, i
     return taken;
 }
 
+// Canonical top-k of an uncertain stage-1 row t over a LONG pool (one wave): the pool in blocks
+// of 512 candidates (kb + i * DH), each block's exact top-k (canonical score, then lower id)
+// listed at `list` in ascending id order, then the top-k of the listed entries (at most 4 k <=
+// 64: the same order resolves ties to the lower id) requested.  `list` is the row's survivor
+// list, unused once the row is rescored in full.
+template <int DH>
+__device__ __noinline__ void fused_canon_row_long(int t, int ncand, int k, const uint16_t* qr,
+                                                  const uint16_t* kb, float scale, uint2* list,
+                                                  uint32_t* sPk, int* sFirst, uint32_t* sBits, int BW) {
+    const int l = lane_id();
+    int nl = 0;
+    for (int c0 = 0; c0 < ncand; c0 += 512) {
+        float v[8];
+        uint32_t kv[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const int i = c0 + l + 64 * j;
+            v[j] = i < ncand ? canon_dot<HGA_DTYPE_BF16, DH>(qr, kb + (int64_t)i * DH, scale) : -INFINITY;
+            kv[j] = v[j] == -INFINITY ? 0u : okey(v[j]);
+            asm volatile("" ::: "memory");    // one dot product in flight at a time
+        }
+        const uint32_t bits = exact_topk<8>(kv, v, k);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const bool m = (bits >> j) & 1u;
+            const uint64_t bal = __ballot(m);
+            if (m) list[nl + lanes_below(bal)] = make_uint2(kv[j], (uint32_t)(c0 + l + 64 * j));
+            nl += __popcll(bal);
+        }
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    const uint2 e = l < nl ? list[l] : make_uint2(0u, 0u);
+    uint32_t kv1[1] = {e.x};
+    float v1[1] = {l < nl ? okey_inv(e.x) : -INFINITY};
+    if (exact_topk<1>(kv1, v1, k) & 1u) fused_request(t, (int)e.y, e.x, sPk, sFirst, sBits, BW);
+}
+
 // Pooled selection of the fused kernel (wave 0): the certified top-k of the requested
 // candidates (sFirst < kNoRow) by pooled key, the forced candidate ip, written ascending to
 // sSel/sThr with ids base_id + i.  Probes (Gaussian quantile, then secant / Newton steps) find a
@@ -1486,25 +1580,35 @@ __device__ __noinline__ int fused_canon_rows(int w, int namb, const int* sAmb, i
 // lanes 0..15, which gives the exact k-th and (k+1)-th pooled keys.  Returns the count, or -1
 // when no threshold was found, the pooled scores could not be certified or the forced
 // candidate must evict a selected one (the caller then runs the general selection).
+template <int J>
 __device__ __forceinline__ int fused_pool_fast(int P, int k, const uint32_t* sPk, const int* sFirst,
                                                float dpool, int ip, int base_id, int* sSel,
                                                int* sThr, uint2* buf) {
-    constexpr int J = kFusedMaxPool / kWave;
+    constexpr bool REG = J <= 8;            // keys held in registers; wider pools re-read LDS
     const int l = lane_id();
-    uint32_t kv[J];
+    uint32_t kvr[REG ? J : 1];
+    int forced = -1;                        // candidate forced in (its key taken as maximal)
+    auto key = [&](int j) -> uint32_t {
+        const int i = l + 64 * j;
+        uint32_t v;
+        if constexpr (REG) v = kvr[j];
+        else v = (i < P && sFirst[i] < kNoRow) ? sPk[i] : 0u;
+        return i == forced ? 0xffffffffu : v;
+    };
     int nreq = 0;
     float s1 = 0.0f, s2 = 0.0f;
 #pragma unroll
     for (int j = 0; j < J; ++j) {
         const int i = l + 64 * j;
-        kv[j] = 0u;
+        uint32_t v = 0u;
         if (64 * j < P) {                                 // wave-uniform
-            if (i < P && sFirst[i] < kNoRow) kv[j] = sPk[i];
-            nreq += __popcll(__ballot(kv[j] != 0u));
-            const float v = kv[j] != 0u ? okey_inv(kv[j]) : 0.0f;
-            s1 += v;
-            s2 = fmaf(v, v, s2);
+            if (i < P && sFirst[i] < kNoRow) v = sPk[i];
+            nreq += __popcll(__ballot(v != 0u));
+            const float f = v != 0u ? okey_inv(v) : 0.0f;
+            s1 += f;
+            s2 = fmaf(f, f, s2);
         }
+        if constexpr (REG) kvr[j] = v;
     }
     uint32_t x = 1u;                                      // members: keys >= x
     if (nreq > k) {
@@ -1523,7 +1627,7 @@ __device__ __forceinline__ int fused_pool_fast(int P, int k, const uint32_t* sPk
             int c = 0;
 #pragma unroll
             for (int j = 0; j < J; ++j)
-                if (64 * j < P) c += __popcll(__ballot(kv[j] >= tx));
+                if (64 * j < P) c += __popcll(__ballot(key(j) >= tx));
             if (c > k && c <= 32) {
                 ok = true;
                 T = tx;
@@ -1552,9 +1656,10 @@ __device__ __forceinline__ int fused_pool_fast(int P, int k, const uint32_t* sPk
 #pragma unroll
         for (int j = 0; j < J; ++j) {
             if (64 * j < P) {
-                const bool in = kv[j] >= T && kv[j] != 0u;
+                const uint32_t v = key(j);
+                const bool in = v >= T && v != 0u;
                 const uint64_t bal = __ballot(in);
-                if (in) buf[base + lanes_below(bal)] = make_uint2(kv[j], (uint32_t)(l + 64 * j));
+                if (in) buf[base + lanes_below(bal)] = make_uint2(v, (uint32_t)(l + 64 * j));
                 base += __popcll(bal);
             }
         }
@@ -1576,35 +1681,39 @@ __device__ __forceinline__ int fused_pool_fast(int P, int k, const uint32_t* sPk
         bool have = false;
 #pragma unroll
         for (int j = 0; j < J; ++j)
-            if (j == ip / 64) have = kv[j] >= x && kv[j] != 0u;   // meaningful in lane ip % 64
+            if (j == ip / 64) {
+                const uint32_t v = key(j);
+                have = v >= x && v != 0u;                 // meaningful in lane ip % 64
+            }
         const bool have_w = __ballot(l == ip % 64 && have) != 0ull;
         if (!have_w) {
             if (nsel >= k) return -1;                     // eviction: general path
-#pragma unroll
-            for (int j = 0; j < J; ++j)
-                if (j == ip / 64 && l == ip % 64) kv[j] = 0xffffffffu;   // forced in (key >= x)
+            forced = ip;                                  // forced in (key >= x)
             ++nsel;
         }
     }
     int base = 0;
 #pragma unroll
     for (int j = 0; j < J; ++j) {
-        const bool m = kv[j] >= x && kv[j] != 0u;
-        const uint64_t bal = __ballot(m);
-        if (m) {
-            const int i = l + 64 * j;
-            const int pos = base + lanes_below(bal);
-            sSel[pos] = base_id + i;
-            sThr[pos] = i == ip ? 0 : sFirst[i];
+        if (64 * j < P) {
+            const uint32_t v = key(j);
+            const bool m = v >= x && v != 0u;
+            const uint64_t bal = __ballot(m);
+            if (m) {
+                const int i = l + 64 * j;
+                const int pos = base + lanes_below(bal);
+                sSel[pos] = base_id + i;
+                sThr[pos] = i == ip ? 0 : sFirst[i];
+            }
+            base += __popcll(bal);
         }
-        base += __popcll(bal);
     }
     return base;
 }
 
 // General pooled selection (certified with canonical pooled values, forced-candidate
 // eviction): the split kernels' routine, out of line.
-template <int DH>
+template <int DH, int J>
 __device__ __noinline__ int fused_pool_general(int P, int k, int rows, const uint32_t* sBits, int BW,
                                                const uint32_t* sPk, const int* sFirst, float dpool,
                                                const uint16_t* qg, int64_t q_ss, const uint16_t* kb,
@@ -1613,14 +1722,15 @@ __device__ __noinline__ int fused_pool_general(int P, int k, int rows, const uin
     auto canon = [&](int t, int i) {
         return canon_dot<HGA_DTYPE_BF16, DH>(qg + t * q_ss, kb + (int64_t)i * DH, scale);
     };
-    return pooled_select<kFusedMaxPool / kWave>(P, k, rows, sBits, BW, sPk, sFirst, dpool, canon,
+    return pooled_select<J>(P, k, rows, sBits, BW, sPk, sFirst, dpool, canon,
                                                  ip, base_id, sSel, sThr, amb);
 }
 
-template <int DH>
+template <int DH, bool LONG>
 __global__ __launch_bounds__(kFThreads) __attribute__((amdgpu_waves_per_eu(2)))
 void route_fused_kernel(RouteArgs A) {
     constexpr int KS = DH / 32;
+    constexpr int PJ = (LONG ? kFusedMaxPoolLong : kFusedMaxPool) / kWave;   // pool slots per lane
     constexpr int kStageBytes = 64 * DH * 2;                           // 64 candidate rows
     extern __shared__ __align__(16) unsigned char smem_raw[];
     unsigned char* sStage = smem_raw;                                  // [2][64][DH] candidate rows
@@ -1639,7 +1749,7 @@ void route_fused_kernel(RouteArgs A) {
     uint32_t* sBits = reinterpret_cast<uint32_t*>(sFirst + A.SPP);     // [64][BW]
 
     const int N = A.N, C = A.C, M = A.M, BW = A.BW;
-    const int n = N - 1 - (int)(blockIdx.x / (A.B * A.H));            // heavy chunks first
+    const int n = A.n_hi - 1 - (int)(blockIdx.x / (A.B * A.H));       // heavy chunks first
     const int bh = blockIdx.x % (A.B * A.H);
     const int b = bh / A.H, h = bh % A.H, kvh = h / (A.H / A.KVH);
     const int w = threadIdx.x / kWave, l = lane_id(), r16 = l % 16, qd = l / 16;
@@ -1745,16 +1855,36 @@ void route_fused_kernel(RouteArgs A) {
                 for (int i = 0; i < 4; ++i)
                     if (kv[i] != 0u) fused_request(t, 4 * qd + i, kv[i], sPk, sFirst, sBits, BW);
             }
-            continue;
+        } else {
+            s1 = q4_fsum(s1);
+            s2 = q4_fsum(s2);
+            ns = q4_sum(ns);
+            uint32_t T;
+            const bool ok = fused_probe<4 * kSegTiles>(kv, 4 * nt, !hard, ncs, kreq, s1, s2, ns, T);
+            hard = hard || !ok;
+            tmax = max(tmax, T);
+            nsurv = fused_compact<4 * kSegTiles>(kv, 4 * nt, T, c0, sSv + t * kSvStride, nsurv, !hard);
         }
-        s1 = q4_fsum(s1);
-        s2 = q4_fsum(s2);
-        ns = q4_sum(ns);
-        uint32_t T;
-        const bool ok = fused_probe<4 * kSegTiles>(kv, 4 * nt, !hard, ncs, kreq, s1, s2, ns, T);
-        hard = hard || !ok;
-        tmax = max(tmax, T);
-        nsurv = fused_compact<4 * kSegTiles>(kv, 4 * nt, T, c0, sSv + t * kSvStride, nsurv, !hard);
+        if constexpr (LONG) {
+            // lists longer than kSurv are cut back before the next segment appends its survivors
+            const bool big = open && !hard && nsurv > kSurv;
+            if (sg + 1 < nseg && __ballot(big) != 0ull) {             // wave-uniform
+                if (qd == 0) sRowN[t] = big ? nsurv : -1;
+                __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+                __builtin_amdgcn_wave_barrier();
+                __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+                fused_merge(w, kreq, sSv, sRowN, sRowT);
+                __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+                __builtin_amdgcn_wave_barrier();
+                __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+                if (big) {
+                    const int m = sRowN[t];
+                    hard = m < 0;
+                    nsurv = m < 0 ? 0 : m;
+                    tmax = max(tmax, sRowT[t]);
+                }
+            }
+        }
     }
     if (wave_act) {
         if (qd == 0) {
@@ -1782,6 +1912,9 @@ void route_fused_kernel(RouteArgs A) {
             if (sBand[ta] != 0u)
                 fused_canon_band<DH>(ta, kreq, sBand[ta], sSv + ta * kSvStride, sRowN[ta],
                                      qg + ta * A.q_ss, pool, scale, sPk, sFirst, sBits, BW);
+            else if (LONG && P > kFusedMaxPool)
+                fused_canon_row_long<DH>(ta, P, kreq, qg + ta * A.q_ss, pool, scale, sSv + ta * kSvStride,
+                                         sPk, sFirst, sBits, BW);
             else
                 fused_canon_rows<DH>(0, 1, sAmb + a, P, kreq, qg, A.q_ss, pool, nullptr, 0, nullptr,
                                      scale, sPk, sFirst, sBits, BW);
@@ -1799,9 +1932,9 @@ void route_fused_kernel(RouteArgs A) {
         const float dpool = kDeltaRel * knmax * qnmax * scale * 1.01f;
         const int prev = n - 1;
         const int ip = (n > 0 && prev >= f_hi && prev < l_lo) ? prev - f_hi : -1;
-        int cnt = fused_pool_fast(P, A.Kc, sPk, sFirst, dpool, ip, f_hi, sSel, sThr, sSv);
+        int cnt = fused_pool_fast<PJ>(P, A.Kc, sPk, sFirst, dpool, ip, f_hi, sSel, sThr, sSv);
         if (cnt < 0)
-            cnt = fused_pool_general<DH>(P, A.Kc, rows, sBits, BW, sPk, sFirst, dpool, qg, A.q_ss,
+            cnt = fused_pool_general<DH, PJ>(P, A.Kc, rows, sBits, BW, sPk, sFirst, dpool, qg, A.q_ss,
                                          pool, scale, ip, f_hi, sSel, sThr, &amb1p);
         if (l == 0) sScal[0] = cnt;
     }
@@ -1918,9 +2051,9 @@ size_t fused_lds(const RouteArgs& a, int D) {
            2 * sizeof(int) * (size_t)a.SPP + sizeof(uint32_t) * kRows * (size_t)a.BW;
 }
 
-template <int DH>
-int launch_route_fused(const RouteArgs& a, size_t lds, hipStream_t st) {
-    auto k = route_fused_kernel<DH>;
+template <int DH, bool LONG>
+int launch_route_fused(const RouteArgs& a, size_t lds, int nchunks, hipStream_t st) {
+    auto k = route_fused_kernel<DH, LONG>;
     static bool attr_done = false;
     if (!attr_done) {
         if (hipFuncSetAttribute((const void*)k, hipFuncAttributeMaxDynamicSharedMemorySize,
@@ -1930,9 +2063,9 @@ int launch_route_fused(const RouteArgs& a, size_t lds, hipStream_t st) {
         }
         attr_done = true;
     }
-    const unsigned grid = (unsigned)(a.B * a.H * a.N);
+    const unsigned grid = (unsigned)(a.B * a.H * nchunks);
     k<<<dim3(grid), dim3(kFThreads), lds, st>>>(a);
-    return launch_status("hga_route_prefill (fused)");
+    return launch_status(LONG ? "hga_route_prefill (fused, long pools)" : "hga_route_prefill (fused)");
 }
 
 template <int DT, int DH>
@@ -1994,8 +2127,54 @@ extern "C" int hga_route_prefill(const hga_config* cfg, int32_t S, const void* q
     int f_hi, l_lo;
     windows(a.N - 1, a.kf, a.kl, &f_hi, &l_lo);
     const int Pmax = l_lo > f_hi ? l_lo - f_hi : 0;
+    const int D = cfg->head_dim;
     HGA_REQUIRE(a.Kc <= kMaxSel, HGA_ERR_UNSUPPORTED, "hga_route_prefill: top-k chunks %d > %d",
                 a.Kc, kMaxSel);
+    {
+        const int64_t ve = cfg->dtype == HGA_DTYPE_BF16 ? 8 : 4;   // elements per 16 bytes
+        const uintptr_t al = (uintptr_t)chunk_k | (uintptr_t)group_k | (uintptr_t)q;
+        HGA_REQUIRE(al % 16 == 0 && ((ck_sb | ck_sh | gk_sb | gk_sh | q_sb | q_sh | q_ss) % ve) == 0,
+                    HGA_ERR_ARG, "hga_route_prefill: q and summaries need 16-byte aligned rows");
+    }
+    hipStream_t st = (hipStream_t)stream;
+    // bf16 MFMA scoring with a chunk of at most 64 rows, top-k chunks <= 16, pools of at most
+    // 2048 chunks and at most 64 group candidates: the fused kernel (one launch, q read once;
+    // the query chunks whose pools exceed 512 in a launch of the LONG variant of their own)
+    const bool fused = cfg->dtype == HGA_DTYPE_BF16 && !a.canonical && !(flags & HGA_ROUTE_SPLIT) &&
+                       (D == 64 || D == 128) && a.Kc <= kCompactK && Pmax <= kFusedMaxPoolLong &&
+                       T2max <= kFusedMaxT2;
+    if (fused) {
+        // n_long: the first query chunk whose pool exceeds kFusedMaxPool (pools grow with n)
+        int n_long = a.N;
+        while (n_long > 0) {
+            int fh, ll;
+            windows(n_long - 1, a.kf, a.kl, &fh, &ll);
+            if (ll - fh <= kFusedMaxPool) break;
+            --n_long;
+        }
+        auto launch = [&](int n_lo, int n_hi, bool lng) -> int {
+            int fh, ll;
+            windows(n_hi - 1, a.kf, a.kl, &fh, &ll);
+            const int pm = ll > fh ? ll - fh : 0;
+            RouteArgs f = a;
+            f.n_hi = n_hi;
+            f.SPP = (pm > T2max ? pm : T2max) + 1;
+            f.BW = (f.SPP + 31) / 32;
+            f.BW2 = (T2max + 1 + 31) / 32;
+            const size_t lds = fused_lds(f, D);
+            HGA_REQUIRE(lds <= 163840, HGA_ERR_UNSUPPORTED, "hga_route_prefill: %zu bytes of LDS", lds);
+            if (lng)
+                return D == 128 ? launch_route_fused<128, true>(f, lds, n_hi - n_lo, st)
+                                : launch_route_fused<64, true>(f, lds, n_hi - n_lo, st);
+            return D == 128 ? launch_route_fused<128, false>(f, lds, n_hi - n_lo, st)
+                            : launch_route_fused<64, false>(f, lds, n_hi - n_lo, st);
+        };
+        if (n_long < a.N) {
+            rc = launch(n_long, a.N, true);
+            if (rc) return rc;
+        }
+        return n_long > 0 ? launch(0, n_long, false) : HGA_OK;
+    }
     HGA_REQUIRE(Pmax <= kJ * 64 && T2max <= kJ * 64, HGA_ERR_UNSUPPORTED,
                 "hga_route_prefill: routing pool %d / group candidates %d exceed %d", Pmax,
                 T2max, kJ * 64);
@@ -2005,7 +2184,6 @@ extern "C" int hga_route_prefill(const hga_config* cfg, int32_t S, const void* q
     a.SP = row_stride(Pmax);
     a.SP2 = row_stride(T2max);
     a.VT2 = (T2max + 63) / 64 * 64;
-    const int D = cfg->head_dim;
     // stage 1: [32][SP] scores of a row block, row norms, pooled state over the pool
     a.SSZ = kBlk * a.SP;
     a.SPP = Pmax + 1;
@@ -2024,27 +2202,6 @@ extern "C" int hga_route_prefill(const hga_config* cfg, int32_t S, const void* q
     HGA_REQUIRE(lds1 <= 163840 && lds2 <= 163840, HGA_ERR_UNSUPPORTED,
                 "hga_route_prefill: %zu / %zu bytes of LDS needed (pool %d, head_dim %d)", lds1,
                 lds2, Pmax, D);
-    {
-        const int64_t ve = cfg->dtype == HGA_DTYPE_BF16 ? 8 : 4;   // elements per 16 bytes
-        const uintptr_t al = (uintptr_t)chunk_k | (uintptr_t)group_k | (uintptr_t)q;
-        HGA_REQUIRE(al % 16 == 0 && ((ck_sb | ck_sh | gk_sb | gk_sh | q_sb | q_sh | q_ss) % ve) == 0,
-                    HGA_ERR_ARG, "hga_route_prefill: q and summaries need 16-byte aligned rows");
-    }
-    hipStream_t st = (hipStream_t)stream;
-    // bf16 MFMA scoring with a chunk of at most 64 rows, top-k chunks <= 16, pools of at most
-    // 512 chunks and at most 64 group candidates: the fused kernel (one launch, q read once)
-    const bool fused = cfg->dtype == HGA_DTYPE_BF16 && !a.canonical && !(flags & HGA_ROUTE_SPLIT) &&
-                       (D == 64 || D == 128) && a.Kc <= kCompactK && Pmax <= kFusedMaxPool &&
-                       T2max <= kFusedMaxT2;
-    if (fused) {
-        RouteArgs f = a;
-        f.SPP = (Pmax > T2max ? Pmax : T2max) + 1;
-        f.BW = (f.SPP + 31) / 32;
-        f.BW2 = (T2max + 1 + 31) / 32;
-        const size_t lds = fused_lds(f, D);
-        HGA_REQUIRE(lds <= 163840, HGA_ERR_UNSUPPORTED, "hga_route_prefill: %zu bytes of LDS", lds);
-        return D == 128 ? launch_route_fused<128>(f, lds, st) : launch_route_fused<64>(f, lds, st);
-    }
 #define HGA_ROUTE_CASE(DTV, DHV) \
     if (cfg->dtype == DTV && D == DHV) return launch_route<DTV, DHV>(a, lds1, lds2, st);
     HGA_ROUTE_CASE(HGA_DTYPE_BF16, 128)

@@ -82,8 +82,18 @@ def prefill_widths(cfg: HgaConfig, S: int):
 
 ROPE_STEPS_IN_DTYPE = 1
 # Longest routing pool (chunks) of a query chunk that hga_route_prefill takes: its stage-1 rows
-# hold 8 candidates per lane of a wave in registers.
+# hold 8 candidates per lane of a wave in registers.  The fused bf16 router (head_dim 64 or 128,
+# top-k chunks <= 16, at most 64 group candidates) takes pools of up to PREFILL_MAX_POOL_FUSED.
 PREFILL_MAX_POOL = 512
+PREFILL_MAX_POOL_FUSED = 2048
+
+
+def prefill_max_pool(cfg: HgaConfig) -> int:
+    """Longest routing pool (chunks) of a query chunk that ``route_prefill`` takes for cfg."""
+    M = cfg.chunk_size // cfg.group_size
+    fused = (cfg.dtype == _lib.HGA_DTYPE_BF16 and cfg.head_dim in (64, 128) and cfg.topk_chunks <= 16
+             and cfg.topk_chunks * M <= 64)
+    return PREFILL_MAX_POOL_FUSED if fused else PREFILL_MAX_POOL
 
 
 def rope(cfg: HgaConfig, x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor,

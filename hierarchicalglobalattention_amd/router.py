@@ -763,12 +763,13 @@ class ChunkRouter:
         N = (S + C - 1) // C
         pol = self.store.policy
         f_hi, l_lo = pol.hot_first_range(N - 1)[1], pol.hot_last_range(N - 1)[0]
-        if l_lo - f_hi > ops.PREFILL_MAX_POOL:
+        max_pool = ops.prefill_max_pool(hc)
+        if l_lo - f_hi > max_pool:
             raise ValueError(
                 f"a fresh block of {S} tokens routes query chunks over pools of up to "
-                f"{l_lo - f_hi} chunks; the chunk-parallel router takes {ops.PREFILL_MAX_POOL}. "
+                f"{l_lo - f_hi} chunks; the chunk-parallel router takes {max_pool}. "
                 f"Feed the prompt in blocks (the first of at most "
-                f"{(ops.PREFILL_MAX_POOL + 1 + max(pol.keep_first, 0) + max(pol.keep_last, 0)) * C} "
+                f"{(max_pool + 1 + max(pol.keep_first, 0) + max(pol.keep_last, 0)) * C} "
                 f"tokens, later blocks are routed chunk by chunk).")
         if populate_store:
             st = self.store.layer(layer)
