@@ -65,6 +65,10 @@ SIGNATURES = {
                                  _i64, _i64, _i32, _vp, _vp, _i64, _i64, _i64, _vp, _vp, _i64,
                                  _i64, _i64, _i32, _vp, _vp, _i32, _vp, _i64, _i64, _i64, _i32,
                                  _vp, _i64, _vp], ctypes.c_int),
+    "hga_attend_decode_noalloc": ([_CFG, _i32, _i32, _i64, _vp, _i64, _i64, _i64, _vp, _vp,
+                                   _i64, _i64, _i64, _i32, _vp, _vp, _i64, _i64, _i64, _vp, _vp,
+                                   _i64, _i64, _i64, _i32, _vp, _vp, _i32, _vp, _i64, _i64, _i64,
+                                   _vp], ctypes.c_int),
     "hga_attend_decode_dca": ([_CFG, _i32, _i32, _i64, _vp, _vp, _vp, _i64, _i64, _i64, _i32,
                                _vp, _vp, _i64, _i64, _i64, _i32, _vp, _vp, _i64, _i64, _i64,
                                _vp, _vp, _i64, _i64, _i64, _i32, _vp, _vp, _vp, _i32, _vp, _i64,

@@ -21,6 +21,8 @@
 #include "hga_common.h"
 #include "hga_select.h"
 
+#include <mutex>
+
 namespace hga {
 namespace {
 
@@ -1832,4 +1834,78 @@ extern "C" int hga_attend_decode_dca(const hga_config* cfg, int32_t L, int32_t n
                                    ring_chunks, k_first, v_first, f_sb, f_sh, f_ss, k_record,
                                    v_record, d_sb, d_sh, d_ss, record_on_host, open_grp, open_thr,
                                    Kg, out, o_sb, o_sh, o_ss, workspace, workspace_bytes, stream);
+}
+
+// ------------------------------------------------------------------------------------------
+// hga_attend_decode_noalloc: hga_attend_decode with its split partials in a static device
+// array instead of a caller workspace, for callers that cannot allocate device memory
+// ------------------------------------------------------------------------------------------
+// The partials of every call on a device go to that device's copy of `scratch`; a call needs no
+// part of it cleared (each split writes its partial before the combine reads it).  Calls that
+// overlap on one device (two streams, two threads) race on it.  Host code never passes the
+// array's name to a kernel: its device address comes from hipGetSymbolAddress on each device.
+constexpr int64_t kNoAllocScratchBytes = 32ll << 20;     // per device, held until process exit
+static __device__ __align__(256) float scratch[kNoAllocScratchBytes / 4];
+
+namespace {
+constexpr int kNoAllocMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kNoAllocMaxDevices] = {};
+
+// Device address of the current device's scratch array (looked up once per device).
+int scratch_for_current_device(void** ptr) {
+    int dev = -1;
+    const hipError_t e = hipGetDevice(&dev);
+    HGA_REQUIRE(e == hipSuccess && dev >= 0 && dev < kNoAllocMaxDevices, HGA_ERR_LAUNCH,
+                "hga_attend_decode_noalloc: no current device (%s)", hipGetErrorString(e));
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        void* p = nullptr;
+        const hipError_t es = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        HGA_REQUIRE(es == hipSuccess && p, HGA_ERR_LAUNCH,
+                    "hga_attend_decode_noalloc: scratch address on device %d: %s", dev,
+                    hipGetErrorString(es));
+        g_scratch_ptr[dev] = p;
+    }
+    *ptr = g_scratch_ptr[dev];
+    return HGA_OK;
+}
+}  // namespace
+
+extern "C" int hga_attend_decode_noalloc(const hga_config* cfg, int32_t L, int32_t n_closed,
+                                         int64_t start_pos, const void* q, int64_t q_sb,
+                                         int64_t q_sh, int64_t q_ss, const void* k_recent,
+                                         const void* v_recent, int64_t r_sb, int64_t r_sh,
+                                         int64_t r_ss, int32_t ring_chunks, const void* k_first,
+                                         const void* v_first, int64_t f_sb, int64_t f_sh,
+                                         int64_t f_ss, const void* k_record, const void* v_record,
+                                         int64_t d_sb, int64_t d_sh, int64_t d_ss,
+                                         int32_t record_on_host, const int32_t* open_grp,
+                                         const int32_t* open_thr, int32_t Kg, void* out,
+                                         int64_t o_sb, int64_t o_sh, int64_t o_ss, void* stream) {
+    using namespace hga;
+    int rc = check_config(cfg);
+    if (rc) return rc;
+    HGA_REQUIRE(q, HGA_ERR_ARG, "hga_attend_decode_noalloc: NULL pointer");
+    HGA_REQUIRE(L >= 1 && L <= kMaxL && n_closed >= 0 && Kg >= 0 && Kg <= 256, HGA_ERR_ARG,
+                "hga_attend_decode_noalloc: bad L/n_closed/Kg");
+    const int64_t c0 = start_pos - (int64_t)n_closed * cfg->chunk_size;
+    HGA_REQUIRE(c0 >= 0 && c0 + L <= cfg->chunk_size, HGA_ERR_ARG,
+                "hga_attend_decode_noalloc: block [%lld, +%d) is not inside active chunk %d",
+                (long long)start_pos, L, n_closed);
+    int64_t need = 0;
+    rc = hga_attend_decode_workspace(cfg, L, n_closed, start_pos, Kg, &need);
+    if (rc) return rc;
+    HGA_REQUIRE(need <= kNoAllocScratchBytes, HGA_ERR_UNSUPPORTED,
+                "hga_attend_decode_noalloc: %lld bytes of partials exceed the static scratch of "
+                "%lld bytes (call hga_attend_decode with a workspace)",
+                (long long)need, (long long)kNoAllocScratchBytes);
+    void* ws = nullptr;
+    rc = scratch_for_current_device(&ws);
+    if (rc) return rc;
+    return attend_decode_impl(cfg, L, n_closed, start_pos, q, q_sb, q_sh, q_ss, nullptr, nullptr,
+                              0, k_recent, v_recent, r_sb, r_sh, r_ss, ring_chunks, k_first,
+                              v_first, f_sb, f_sh, f_ss, k_record, v_record, d_sb, d_sh, d_ss,
+                              record_on_host, open_grp, open_thr, Kg, out, o_sb, o_sh, o_ss, ws,
+                              kNoAllocScratchBytes, stream);
 }

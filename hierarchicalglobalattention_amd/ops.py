@@ -440,6 +440,38 @@ def attend_decode_workspace(cfg: HgaConfig, L: int, n_closed: int, start_pos: in
     return torch.empty(max(nb.value, 16), dtype=torch.uint8, device=device)
 
 
+def attend_decode_noalloc(cfg: HgaConfig, q: torch.Tensor, n_closed: int, start_pos: int,
+                          recent_k: torch.Tensor, recent_v: torch.Tensor, ring_chunks: int,
+                          first_k, first_v, record_k, record_v, record_on_host: bool,
+                          open_grp: torch.Tensor, open_thr: torch.Tensor, Kg: int,
+                          out: torch.Tensor) -> torch.Tensor:
+    """attend_decode (phase 0, no DCA) through hga_attend_decode_noalloc: the split partials go
+    to the library's static per-device scratch (32 MiB), so neither this call nor the library
+    allocates device memory.  ``out`` is required, the lists must be contiguous; calls that
+    overlap on one device race on the scratch."""
+    _dev(q, recent_k, recent_v, open_grp, open_thr, out)
+    B, H, L, D = q.shape
+    if first_k is None:
+        first_k, first_v = recent_k, recent_v
+    if record_k is None:
+        record_k, record_v = recent_k, recent_v
+    if record_on_host and not record_k.is_pinned():
+        raise ValueError("a host record must be pinned memory")
+    if not record_on_host:
+        _dev(first_k, first_v, record_k, record_v)
+    for a_, b_ in ((recent_k, recent_v), (first_k, first_v), (record_k, record_v)):
+        if a_.stride() != b_.stride():
+            raise ValueError("K and V of a source must share strides")
+    if not (open_grp.is_contiguous() and open_thr.is_contiguous()):
+        raise ValueError("open_grp / open_thr must be contiguous")
+    check(lib().hga_attend_decode_noalloc(
+        ctypes.byref(cfg), L, n_closed, start_pos, _p(q), *_s4(q), _p(recent_k), _p(recent_v),
+        *_s4(recent_k), ring_chunks, _p(first_k), _p(first_v), *_s4(first_k), _p(record_k),
+        _p(record_v), *_s4(record_k), 1 if record_on_host else 0, _p(open_grp), _p(open_thr), Kg,
+        _p(out), *_s4(out), _stream()), "hga_attend_decode_noalloc")
+    return out
+
+
 _SIDE = {}
 
 

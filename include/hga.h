@@ -269,6 +269,26 @@ int hga_attend_decode_phase(const hga_config* cfg, int32_t L, int32_t n_closed, 
                             void* workspace, int64_t workspace_bytes, void* stream);
 
 /*
+ * hga_attend_decode without a workspace: the split partials go to a static device array of the
+ * library (32 MiB on each device the library runs on, held until the process ends; the device
+ * current at the call), so neither the call nor the library allocates device memory.  No
+ * counterpart in the reference: for callers that cannot allocate (code under HIP graph capture,
+ * serving loops that forbid allocation).  Blocks whose partials (hga_attend_decode_workspace)
+ * exceed 32 MiB are refused with HGA_ERR_UNSUPPORTED.  Calls that overlap on one device (two
+ * streams or threads) race on the array; nothing in it needs clearing between calls.
+ */
+int hga_attend_decode_noalloc(const hga_config* cfg, int32_t L, int32_t n_closed,
+                              int64_t start_pos, const void* q, int64_t q_sb, int64_t q_sh,
+                              int64_t q_ss, const void* k_recent, const void* v_recent,
+                              int64_t r_sb, int64_t r_sh, int64_t r_ss, int32_t ring_chunks,
+                              const void* k_first, const void* v_first, int64_t f_sb,
+                              int64_t f_sh, int64_t f_ss, const void* k_record,
+                              const void* v_record, int64_t d_sb, int64_t d_sh, int64_t d_ss,
+                              int32_t record_on_host, const int32_t* open_grp,
+                              const int32_t* open_thr, int32_t Kg, void* out, int64_t o_sb,
+                              int64_t o_sh, int64_t o_ss, void* stream);
+
+/*
  * Dual Chunk Attention decode (QwenRoutedAttention._dca_attend,
  * Qwen3LongContext/qwen_routed_attention.py:244-283): the same key sequence and visibility as
  * hga_attend_decode over keys stored RoPE'd at pos % dca_chunk.  Key p is scored against
