@@ -71,9 +71,7 @@ class QwenRoutedAttention(nn.Module):
         self.head_dim = int(getattr(config, "head_dim", config.hidden_size // self.num_heads))
         self.num_layers = int(getattr(config, "num_hidden_layers", 0))
         self.chunk_size = chunk_size
-        if cache_location not in ("vram", "ram", "fs"):
-            raise ValueError(f"unknown cache_location {cache_location!r}")
-        self.cache_location = cache_location
+        self.cache_location = cache_location     # "vram", "fs", anything else: the RAM tier
         self.vram_cache_chunks = vram_cache_chunks
         self.vram_summary_chunks = vram_summary_chunks
         self.vram_cache_reserve_gb = vram_cache_reserve_gb
@@ -170,7 +168,8 @@ class QwenRoutedAttention(nn.Module):
         return out, None
 
     def _make_store(self, B: int, dtype: torch.dtype, device: torch.device):
-        """VRAM or pinned-RAM token record (qwen_routed_attention.py:286-315)."""
+        """VRAM, on-disk or (any other cache_location) pinned-RAM token record
+        (qwen_routed_attention.py:286-315)."""
         kwargs = dict(compute_device=device, policy=self._policy, kv_heads=self.num_kv_heads,
                       head_dim=self.head_dim, chunk_size=self.chunk_size,
                       groups_per_chunk=self._cfg.groups_per_chunk, batch_size=B, dtype=dtype)

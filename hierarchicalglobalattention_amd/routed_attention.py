@@ -147,11 +147,10 @@ class HierarchicalGlobalAttentionRouted(nn.Module):
         return emb.cos(), emb.sin()
 
     def _make_store(self, B: int, dtype, device):
-        """VRAM, pinned-RAM or on-disk token record (HierarchicalGlobalAttentionRouted.py:223-240)."""
-        cls = {"vram": VramKVCacheStore, "ram": RamKVCacheStore,
-               "fs": FsKVCacheStore}.get(self.cache_location)
-        if cls is None:
-            raise ValueError(f"unknown cache_location {self.cache_location!r}")
+        """VRAM, pinned-RAM or on-disk token record (HierarchicalGlobalAttentionRouted.py:223-240);
+        any other cache_location takes the RAM tier, as in the reference."""
+        cls = {"vram": VramKVCacheStore, "fs": FsKVCacheStore}.get(self.cache_location,
+                                                                   RamKVCacheStore)
         kw = dict(num_layers=self.num_layers) if cls is FsKVCacheStore else {}
         return cls(compute_device=device, policy=self._policy, kv_heads=self.kv_heads,
                    head_dim=self.head_dim, chunk_size=self.chunk_size,

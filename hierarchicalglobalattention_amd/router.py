@@ -13,6 +13,7 @@ import os
 import shutil
 import tempfile
 import weakref
+from abc import ABC, abstractmethod
 from collections import OrderedDict
 from dataclasses import dataclass
 from typing import Dict, List, Optional, Tuple
@@ -111,12 +112,63 @@ class _LayerRecord:
         self.n_closed = 0
 
 
-class _StoreBase:
+class KVCacheStore(ABC):
+    """The tiered KV store interface (kv_cache_store.py:26-82): one instance serves all layers;
+    per layer it holds the closed chunks' summaries (chunk_k [B, KVH, Dh] on the compute device,
+    the routing table), their group summaries and their tokens.  The router of this package
+    reads the summary tables and the token sources directly (``layer``/``sources``); these
+    methods are the reference's seam for callers that drive a store themselves."""
+
+    def __init__(self, *, compute_device, policy: ChunkPlacementPolicy) -> None:
+        self.compute_device = torch.device(compute_device)
+        self.policy = policy
+
+    @abstractmethod
+    def reset(self) -> None: ...
+
+    @abstractmethod
+    def num_closed_chunks(self, layer: int) -> int: ...
+
+    @abstractmethod
+    def chunk_summaries(self, layer: int) -> Optional[torch.Tensor]:
+        """[B, KVH, n_closed, Dh] on the compute device, or None."""
+
+    @abstractmethod
+    def append_closed_chunk(self, layer: int, chunk_k: torch.Tensor, group_k: torch.Tensor,
+                            group_v: torch.Tensor, token_k: torch.Tensor,
+                            token_v: torch.Tensor) -> None:
+        """Store a freshly closed chunk: chunk_k [B, KVH, Dh], group_k/group_v [B, KVH, M, Dh],
+        token_k/token_v [B, KVH, C, Dh]."""
+
+    @abstractmethod
+    def gather_group_summaries(self, layer: int, chunk_idx: torch.Tensor
+                               ) -> Tuple[torch.Tensor, torch.Tensor]:
+        """Group K/V summaries of chunk_idx [B, H, *] -> [B, H, *, M, Dh] on the device."""
+
+    @abstractmethod
+    def gather_tokens(self, layer: int, chunk_idx: torch.Tensor, group_idx: torch.Tensor
+                      ) -> Tuple[torch.Tensor, torch.Tensor]:
+        """Token K/V of the groups (chunk_idx, group_idx) [B, H, *] -> [B, H, *, gs, Dh]."""
+
+    @abstractmethod
+    def hot_group_summaries(self, layer: int, lo: int, hi: int
+                            ) -> Tuple[torch.Tensor, torch.Tensor]:
+        """Group K/V summaries of the window chunks [lo, hi) -> [B, KVH, hi-lo, M, Dh]."""
+
+    @abstractmethod
+    def hot_tokens(self, layer: int, lo: int, hi: int) -> Tuple[torch.Tensor, torch.Tensor]:
+        """Token K/V of the window chunks [lo, hi) -> [B, KVH, hi-lo, C, Dh]."""
+
+    def prefetch(self, layer: int, chunk_idx: torch.Tensor) -> None:  # noqa: B027
+        """Best-effort hint that chunk_idx will be gathered soon (no-op unless a tier reads
+        from disk)."""
+
+
+class _StoreBase(KVCacheStore):
     def __init__(self, *, compute_device, policy: ChunkPlacementPolicy, kv_heads: int,
                  head_dim: int, chunk_size: int, groups_per_chunk: int, batch_size: int,
                  dtype=torch.float32, initial_capacity: int = 64):
-        self.compute_device = torch.device(compute_device)
-        self.policy = policy
+        super().__init__(compute_device=compute_device, policy=policy)
         self.kvh, self.dh, self.C, self.M, self.B = kv_heads, head_dim, chunk_size, \
             groups_per_chunk, batch_size
         self.dtype = dtype
@@ -170,6 +222,136 @@ class _StoreBase:
         if st.act_kraw is None:
             st.act_kraw = self._dev_zeros(B, KVH, C, D)
         return st
+
+    # -- the KVCacheStore seam ---------------------------------------------------------------
+    # Group V summaries are not stored: the exact-token path never reads them, and they are a
+    # function of the tokens the store holds (sum over the group's values x 1/(gs + sqrt(gs)),
+    # chunk_router.py:641-642, 578), so the gathers below recompute them from the tokens.
+    def _group_v(self, v: torch.Tensor) -> torch.Tensor:
+        """[..., C, Dh] token values -> [..., M, Dh] group V summaries."""
+        gs = self.C // self.M
+        return v.reshape(*v.shape[:-2], self.M, gs, self.dh).sum(dim=-2) * \
+            (1.0 / (gs + math.sqrt(gs)))
+
+    def append_closed_chunk(self, layer: int, chunk_k, group_k, group_v, token_k,
+                            token_v) -> None:
+        """Chunk n_closed closes with the given summaries and tokens (its token rows are
+        written as the active chunk's, then handed on as when the router closes a chunk).
+        group_v is not kept (recomputed from token_v)."""
+        st = self.layer(layer)
+        n = st.n_closed
+        B, KVH, C, D, M = self.B, self.kvh, self.C, self.dh, self.M
+        if tuple(chunk_k.shape) != (B, KVH, D) or tuple(group_k.shape) != (B, KVH, M, D) or \
+                tuple(token_k.shape) != (B, KVH, C, D) or token_v.shape != token_k.shape:
+            raise ValueError("append_closed_chunk: chunk_k [B,KVH,Dh], group_k [B,KVH,M,Dh], "
+                             "token_k/token_v [B,KVH,C,Dh] expected")
+        self.prepare_block(layer, n, n + 1)
+        st = self.layer(layer)
+        dev = self.compute_device
+        st.chunk_k[:, :, n] = chunk_k.detach().to(dev)
+        st.group_k[:, :, n] = group_k.detach().to(dev)
+        self.write_tokens(layer, n * C, token_k.detach().to(dev, self.dtype),
+                          token_v.detach().to(dev, self.dtype))
+        self.close_chunk(layer, n)
+        st.n_closed = n + 1
+
+    def seed_closed_chunks(self, layer: int, chunk_k, group_k, group_v, token_k,
+                           token_v) -> None:
+        """N closed chunks at once (ram_kv_cache_store.py:483-527): chunk_k [B,KVH,N,Dh],
+        group_k/group_v [B,KVH,N,M,Dh], token_k/token_v [B,KVH,N,C,Dh]; replaces the layer's
+        contents.  group_v is not kept."""
+        B, KVH, N = token_k.shape[:3]
+        C, D = self.C, self.dh
+        st = self.layer(layer)
+        st.n_closed = 0
+        st = self.ensure_capacity(layer, N + 1)
+        dev = self.compute_device
+        st.chunk_k[:, :, :N] = chunk_k.detach().to(dev)
+        st.group_k[:, :, :N] = group_k.detach().to(dev)
+        self.seed(layer, token_k.detach().to(dev, self.dtype).reshape(B, KVH, N * C, D),
+                  token_v.detach().to(dev, self.dtype).reshape(B, KVH, N * C, D), N)
+        st.n_closed = N
+
+    def _hot_chunk(self, layer: int, c: int):
+        """Device views [B, KVH, C, Dh] of window chunk c's keys and values."""
+        src = self.sources(layer)
+        C = self.C
+        n_closed = self.num_closed_chunks(layer)
+        first = c < self.policy.hot_first_range(n_closed)[1]
+        if not (first or self.policy.hot_last_range(n_closed)[0] <= c <= n_closed):
+            raise ValueError(f"chunk {c} is not in a window of layer {layer} "
+                             f"({n_closed} closed chunks)")
+        if src["ring_chunks"] == 0:                       # record by position (VRAM tier)
+            return src["recent_k"][:, :, c * C:(c + 1) * C], src["recent_v"][:, :, c * C:(c + 1) * C]
+        if first:
+            return src["first_k"][:, :, c * C:(c + 1) * C], src["first_v"][:, :, c * C:(c + 1) * C]
+        s = (c % src["ring_chunks"]) * C
+        return src["recent_k"][:, :, s:s + C], src["recent_v"][:, :, s:s + C]
+
+    def hot_tokens(self, layer: int, lo: int, hi: int):
+        if not 0 <= lo <= hi <= self.num_closed_chunks(layer):
+            raise ValueError(f"window chunks [{lo}, {hi}) outside the closed chunks")
+        if hi == lo:
+            e = torch.empty(self.B, self.kvh, 0, self.C, self.dh, dtype=self.dtype,
+                            device=self.compute_device)
+            return e, e.clone()
+        kv = [self._hot_chunk(layer, c) for c in range(lo, hi)]
+        return (torch.stack([k for k, _ in kv], dim=2), torch.stack([v for _, v in kv], dim=2))
+
+    def hot_group_summaries(self, layer: int, lo: int, hi: int):
+        _, v = self.hot_tokens(layer, lo, hi)
+        return self.layer(layer).group_k[:, :, lo:hi].clone(), self._group_v(v)
+
+    def _gather_groups(self, layer: int, grp: torch.Tensor):
+        """Token K/V [B, H, K, gs, Dh] of the global group ids grp [B, H, K] (chunk*M + group)
+        of closed chunks, through the decode gather (one copy per distinct group and KV head,
+        from whichever record the tier keeps)."""
+        B, H, K = grp.shape
+        gs, D = self.C // self.M, self.dh
+        n_closed = self.num_closed_chunks(layer)
+        cfg = ops.make_config(batch=B, heads=H, kv_heads=self.kvh, head_dim=D, chunk_size=self.C,
+                              group_size=gs, topk_chunks=1, topk_groups=K,
+                              keep_first=self.policy.keep_first, keep_last=self.policy.keep_last,
+                              cutoff_pair=0, dtype=self.dtype)
+        if int(grp.numel()) and (int(grp.min()) < 0 or int(grp.max()) >= n_closed * self.M):
+            raise ValueError("group ids outside the closed chunks")
+        src = self.sources(layer)
+        og = grp.to(self.compute_device, torch.int32).contiguous()
+        ot = torch.zeros_like(og)
+        resolve = src.get("resolve")
+        og_rec, n_rec, rk, rv = (resolve(og) if resolve is not None else
+                                 (og, n_closed, src["record_k"], src["record_v"]))
+        sk, sv, sg = ops.gather_decode(cfg, n_rec, og_rec, ot, K, rk, rv, src["record_on_host"],
+                                       ops.DecodeStaging(), H)
+        U = sk.shape[2] // gs
+        b = torch.arange(B, device=og.device).view(B, 1, 1)
+        kv = (torch.arange(H, device=og.device) // (H // self.kvh)).view(1, H, 1)
+        slot = sg.long()
+        return (sk.view(B, self.kvh, U, gs, D)[b, kv, slot],
+                sv.view(B, self.kvh, U, gs, D)[b, kv, slot])
+
+    def gather_tokens(self, layer: int, chunk_idx: torch.Tensor, group_idx: torch.Tensor):
+        shape = tuple(chunk_idx.shape)
+        B, H = shape[:2]
+        grp = (chunk_idx.long() * self.M + group_idx.long()).reshape(B, H, -1)
+        k, v = self._gather_groups(layer, grp)
+        tail = (self.C // self.M, self.dh)
+        return k.reshape(*shape, *tail), v.reshape(*shape, *tail)
+
+    def gather_group_summaries(self, layer: int, chunk_idx: torch.Tensor):
+        shape = tuple(chunk_idx.shape)
+        B, H = shape[:2]
+        dev = self.compute_device
+        idx = chunk_idx.to(dev).long().reshape(B, H, -1)
+        st = self.layer(layer)
+        b = torch.arange(B, device=dev).view(B, 1, 1)
+        kvh = (torch.arange(H, device=dev) // (H // self.kvh)).view(1, H, 1)
+        gk = st.group_k[b, kvh, idx]                                        # [B, H, n, M, Dh]
+        grp = (idx.unsqueeze(-1) * self.M + torch.arange(self.M, device=dev)).reshape(B, H, -1)
+        _, v = self._gather_groups(layer, grp)                              # [B, H, n*M, gs, Dh]
+        gv = v.sum(dim=-2) * (1.0 / (self.C // self.M + math.sqrt(self.C // self.M)))
+        tail = (self.M, self.dh)
+        return gk.reshape(*shape, *tail), gv.reshape(*shape, *tail)
 
 
 class VramKVCacheStore(_StoreBase):
@@ -488,6 +670,15 @@ class FsKVCacheStore(RamKVCacheStore):
             st.ring_k[:, :, s:s + b - a] = k_rope[:, :, a:b]
             st.ring_v[:, :, s:s + b - a] = v[:, :, a:b]
 
+    def prefetch(self, layer: int, chunk_idx: torch.Tensor) -> None:
+        """Reads the chunks of chunk_idx that are not in the page cache (when they fit in it)."""
+        n_closed = self.num_closed_chunks(layer)
+        chunks = [c for c in np.unique(chunk_idx.detach().cpu().numpy()).tolist()
+                  if 0 <= c < n_closed]
+        f = self.fs_layer(layer)
+        if chunks and len(chunks) <= f.ram_cap:
+            f.ensure_resident(chunks)
+
     def _resolve(self, layer: int, open_grp: torch.Tensor):
         """Makes the opened groups' chunks resident and maps group ids (chunk*M + m) to cache
         ids (slot*M + m); returns the mapped list, the cache size in chunks and the cache's K/V
@@ -520,9 +711,16 @@ class FsKVCacheStore(RamKVCacheStore):
 class RoutedKV:
     """Routing result of one block: the index lists the attention kernel reads -- no
     materialised K/V (compare RoutedKV, chunk_router.py:93-162).  ``attend`` computes the exact
-    softmax attention over real tokens (``use_summaries=False``, the only mode of the exact
-    routed path, HierarchicalGlobalAttentionRouted.py:172-174).  ``chunked`` results come from
-    the vectorized prefill, the others from ``decode_block``."""
+    softmax attention over real tokens.  This router builds no group-summary keys
+    (``summary_k``/``summary_v``/``summary_mask`` are None, as for the reference's exact
+    router), so ``use_summaries`` -- True by default, as in the reference -- selects nothing
+    extra (chunk_router.py:128-136); the exact routed module passes False
+    (HierarchicalGlobalAttentionRouted.py:172-174).  ``chunked`` results come from the
+    vectorized prefill, the others from ``decode_block``."""
+
+    summary_k = None
+    summary_v = None
+    summary_mask = None
 
     def __init__(self, hcfg, routing: dict, scale: float, chunk_size: int, *, chunked: bool,
                  k_rope=None, v=None, sources=None, n_closed: int = 0, start_pos: int = 0):
@@ -535,10 +733,7 @@ class RoutedKV:
         self.sources = sources
         self.n_closed, self.start_pos = n_closed, start_pos
 
-    def attend(self, q: torch.Tensor, use_summaries: bool = False) -> torch.Tensor:
-        if use_summaries:
-            raise NotImplementedError("summary-attending routed attention is not part of the "
-                                      "exact-token path")
+    def attend(self, q: torch.Tensor, use_summaries: bool = True) -> torch.Tensor:
         r = self.routing
         if self.chunked:
             return ops.attend_prefill(self.hcfg, q, self.k_rope, self.v, r["open_grp"],
@@ -611,7 +806,11 @@ class ChunkRouter:
     block runs the vectorized semantics through the HIP kernels; blocks inside one chunk go
     through the decode path."""
 
-    def __init__(self, cfg: RouterConfig, store: VramKVCacheStore) -> None:
+    def __init__(self, cfg: RouterConfig, store: KVCacheStore) -> None:
+        if not store.policy.first_token_level:
+            raise ValueError("ChunkRouter attends the first window at token level "
+                             "(ChunkPlacementPolicy(first_token_level=True)); a summary-level "
+                             "first window belongs to the summary-attending variant")
         self.cfg = cfg
         self.store = store
         self._hcfg_cache: Dict[Tuple[int, torch.dtype], object] = {}
@@ -693,6 +892,25 @@ class ChunkRouter:
         if c0 + L == C:
             self._close_chunk(layer, n, k_rope_chunk=None)
         return routed
+
+    @torch.no_grad()
+    def prefill(self, layer: int, q: torch.Tensor, k_rope: torch.Tensor, k_raw: torch.Tensor,
+                v: torch.Tensor, start_pos: int = 0) -> torch.Tensor:
+        """Stream a prefix chunk by chunk through ``decode_block`` and return the attention
+        output [B, H, S, Dh] (ChunkRouter.prefill, chunk_router.py:410-440): each piece ends at
+        a chunk boundary, is routed against the chunks closed before it and attended."""
+        C = self.cfg.chunk_size
+        S = q.shape[2]
+        outs, p, done = [], start_pos, 0
+        while done < S:
+            take = min(C - (p % C), S - done)
+            sl = slice(done, done + take)
+            routed = self.decode_block(layer, q[:, :, sl], k_rope[:, :, sl], k_raw[:, :, sl],
+                                       v[:, :, sl], p)
+            outs.append(routed.attend(q[:, :, sl]))
+            p += take
+            done += take
+        return torch.cat(outs, dim=2)
 
     def _rotary_rows(self, start: int, length: int, device):
         """Rows [start, start + length) of the fp32 rotary table, sliced from a cached table

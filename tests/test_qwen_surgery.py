@@ -56,8 +56,9 @@ def test_config_and_arguments():
     d = QwenRoutedAttention(model.model.layers[0].self_attn, model.config, chunk_size=8,
                             dca_chunk=40)
     assert (d.dca_local, d.dca_ceil) == (8, 48)
-    with pytest.raises(ValueError):
-        QwenRoutedAttention(model.model.layers[0].self_attn, model.config, cache_location="tape")
+    # any location other than "vram" / "fs" takes the RAM tier (qwen_routed_attention.py:286-315)
+    t = QwenRoutedAttention(model.model.layers[0].self_attn, model.config, cache_location="tape")
+    assert type(t._make_store(1, torch.float32, torch.device("cpu"))).__name__ == "RamKVCacheStore"
     f = QwenRoutedAttention(model.model.layers[0].self_attn, model.config, cache_location="fs",
                             ram_budget_gb=0.5, fs_cache_dir="/tmp")
     assert (f.cache_location, f.ram_budget_gb, f.fs_cache_dir) == ("fs", 0.5, "/tmp")
