@@ -222,9 +222,13 @@ def run_summary_case(name, *, B, KVH, S, Dh, C, gs, theta, dtype, seed):
 
 
 def run_module_case(name, *, B, S, d_model, H, KVH, Dh, C, gs, kf, kl, tc, tg, theta, seed,
-                    gen=0, cache_location="vram", qk_norm=False):
+                    gen=0, cache_location="vram", qk_norm=False, blocks=None):
     """Full ``HierarchicalGlobalAttentionRouted.forward`` (HierarchicalGlobalAttentionRouted.py:137-177):
-    a prefill of ``S`` tokens, then ``gen`` one-token decode steps through a cache object."""
+    a prefill of ``S`` tokens, then ``gen`` one-token decode steps through a cache object, or
+    (``blocks``) blocks of the given token counts, each routed by the reference as decode
+    segments of up to one chunk (chunk_router.py:493-516) -- L > 1 rows per routing decision."""
+    if blocks is not None:
+        gen = int(sum(blocks))
     torch.manual_seed(seed)
     mod = HierarchicalGlobalAttentionRouted(d_model=d_model, nhead=H, kv_heads=KVH, head_dim=Dh,
                                             chunk_size=C, group_size=gs, topk_chunks=tc,
@@ -258,24 +262,26 @@ def run_module_case(name, *, B, S, d_model, H, KVH, Dh, C, gs, kf, kl, tc, tg, t
             cp = torch.arange(S)
             o, _ = mod(hidden_states=x[:, :S], past_key_value=cache, cache_position=cp)
             outs.append(o)
-            for i in range(gen):
-                p = S + i
-                o, _ = mod(hidden_states=x[:, p:p + 1], past_key_value=cache,
-                           cache_position=torch.tensor([p]))
+            p = S
+            for L in (blocks if blocks is not None else [1] * gen):
+                o, _ = mod(hidden_states=x[:, p:p + L], past_key_value=cache,
+                           cache_position=torch.arange(p, p + L))
                 outs.append(o)
+                p += L
     finally:
         ChunkRouter._route_decision = orig
     res = dict(meta=json.dumps(dict(name=name, B=B, S=S, d_model=d_model, H=H, KVH=KVH, Dh=Dh,
                                     C=C, gs=gs, keep_first=kf, keep_last=kl, topk_chunks=tc,
                                     topk_groups=tg, theta=theta, seed=seed, gen=gen,
-                                    cache_location=cache_location, qk_norm=qk_norm)),
+                                    cache_location=cache_location, qk_norm=qk_norm,
+                                    blocks=blocks)),
                x=x.numpy(), out=torch.cat(outs, dim=1).numpy())
     for k_, t in mod.state_dict().items():
         res["w_" + k_] = t.numpy()
     M = C // gs
     # Decode decisions: per step, routed chunks visible at L=1 and opened groups visible.
     dec = [d for d in decisions]
-    if gen > 0:
+    if gen > 0 and blocks is None:
         Kmax = max([d["mid_idx"].shape[-1] for d in dec] + [1])
         Gmax = max([d["open_chunk"].shape[-1] for d in dec] + [1])
         sel = np.full((len(dec), B, H, Kmax), -1, np.int32)
@@ -295,6 +301,41 @@ def run_module_case(name, *, B, S, d_model, H, KVH, Dh, C, gs, kf, kl, tc, tg, t
                 s = np.sort(np.where(ids < 0, 1 << 30, ids), -1)
                 opn[i, ..., :s.shape[-1]] = np.where(s == 1 << 30, -1, s)
         res["dec_n_closed"], res["dec_sel"], res["dec_open"] = ncl, sel, opn
+    if blocks is not None:
+        # L-row decisions: every id visible to some row, ascending, with its first such row
+        # (chunk_router.py:225-276 -- the pool and the group requests span all L rows)
+        def first_rows(ids, vis):
+            """ids [B, H, K], vis [B, H, L, K] -> (sorted ids, first rows) padded with -1."""
+            anyv = vis.any(dim=2)
+            first = torch.argmax(vis.to(torch.int8), dim=2)
+            out_id = np.full(ids.shape, -1, np.int32)
+            out_thr = np.full(ids.shape, -1, np.int32)
+            for b in range(ids.shape[0]):
+                for h in range(ids.shape[1]):
+                    keep = [(int(ids[b, h, j]), int(first[b, h, j])) for j in range(ids.shape[2])
+                            if bool(anyv[b, h, j])]
+                    keep.sort()
+                    for j, (i_, t_) in enumerate(keep):
+                        out_id[b, h, j], out_thr[b, h, j] = i_, t_
+            return out_id, out_thr
+
+        Kmax = max([d["mid_idx"].shape[-1] for d in dec] + [1])
+        Gmax = max([d["open_chunk"].shape[-1] for d in dec] + [1])
+        n = len(dec)
+        bl = dict(L=np.zeros(n, np.int32), sel=np.full((n, B, H, Kmax), -1, np.int32),
+                  sel_thr=np.full((n, B, H, Kmax), -1, np.int32),
+                  open=np.full((n, B, H, Gmax), -1, np.int32),
+                  open_thr=np.full((n, B, H, Gmax), -1, np.int32))
+        for i, d in enumerate(dec):
+            bl["L"][i] = d["mid_vis"].shape[2] if d["mid_idx"].shape[-1] else d["open_vis"].shape[2]
+            if d["mid_idx"].shape[-1]:
+                a, t = first_rows(d["mid_idx"], d["mid_vis"])
+                bl["sel"][i, ..., :a.shape[-1]], bl["sel_thr"][i, ..., :a.shape[-1]] = a, t
+            if d["open_chunk"].shape[-1]:
+                a, t = first_rows(d["open_chunk"] * M + d["open_grp"], d["open_vis"])
+                bl["open"][i, ..., :a.shape[-1]], bl["open_thr"][i, ..., :a.shape[-1]] = a, t
+        for k_, v_ in bl.items():
+            res["blk_" + k_] = v_
     return res
 
 
@@ -345,7 +386,19 @@ def main():
     cases["mod_decode_ram"] = run_module_case(
         "mod_decode_ram", B=2, S=52, d_model=64, H=4, KVH=2, Dh=16, C=8, gs=4, kf=1, kl=2,
         tc=3, tg=6, theta=1e4, seed=11, gen=14, cache_location="ram", qk_norm=True)
+    # multi-row decode blocks (the chat feeds 64-token blocks, chat_qwen30b_fp8.py:67): blocks of
+    # 3, 11 and 64 tokens after a prefill, crossing chunk boundaries (C 16) ...
+    cases["mod_blocks"] = run_module_case(
+        "mod_blocks", B=2, S=75, d_model=64, H=4, KVH=2, Dh=16, C=16, gs=4, kf=1, kl=2, tc=3,
+        tg=6, theta=1e4, seed=12, blocks=[3, 11, 64, 3, 11])
+    # ... and at C 64: the active chunk filled, then a whole 64-row chunk in one decode segment
+    cases["mod_blocks64"] = run_module_case(
+        "mod_blocks64", B=1, S=514, d_model=64, H=4, KVH=2, Dh=16, C=64, gs=16, kf=1, kl=1,
+        tc=3, tg=8, theta=1e4, seed=13, blocks=[62, 64, 11, 3], cache_location="ram")
+    only = sys.argv[1:]
     for name, res in cases.items():
+        if only and name not in only:
+            continue
         path = os.path.join(HERE, f"{name}.npz")
         np.savez_compressed(path, **res)
         print(f"wrote {path} ({os.path.getsize(path) / 1024:.1f} KiB)")

@@ -93,6 +93,58 @@ def test_module_decode_matches_reference(name, monkeypatch):
         _same_lists(og, g["dec_open"][i])
 
 
+def _run_module_blocks(m, x, S, blocks):
+    """Prefill S tokens, then blocks of the given token counts."""
+    cache = _Cache()
+    outs = []
+    with torch.no_grad():
+        o, _ = m(hidden_states=x[:, :S], past_key_value=cache,
+                 cache_position=torch.arange(S, device=DEV))
+        outs.append(o)
+        p = S
+        for L in blocks:
+            o, _ = m(hidden_states=x[:, p:p + L], past_key_value=cache,
+                     cache_position=torch.arange(p, p + L, device=DEV))
+            outs.append(o)
+            p += L
+    torch.cuda.synchronize()
+    return torch.cat(outs, 1).cpu().numpy()
+
+
+@pytest.mark.parametrize("name,loc", [("mod_blocks", "vram"), ("mod_blocks", "ram"),
+                                      ("mod_blocks", "fs"), ("mod_blocks64", "ram"),
+                                      ("mod_blocks64", "vram")])
+def test_module_multi_row_blocks_match_reference(name, loc, monkeypatch):
+    """Blocks of 3, 11 and 64 tokens after a prefill, recorded from the reference module
+    (tests/golden/make_golden.py): every decode segment's routing decision -- L rows pooled
+    for the chunk selection, the groups requested over all rows, each id with its first
+    visible row (chunk_router.py:187-277) -- bit for bit, and the outputs within fp32
+    tolerance.  mod_blocks64 routes a whole 64-row chunk in one segment."""
+    meta, g = load_case(name)
+    print(f"[decode] blocks {name} {loc} {meta['blocks']}", flush=True)
+    seen = []
+    real = ops.route_decode
+
+    def spy(cfg, q, ck, gk, n_closed):
+        r = real(cfg, q, ck, gk, n_closed)
+        seen.append((q.shape[2], {k: r[k].cpu().numpy() for k in
+                                  ("mid", "mid_thr", "open_grp", "open_thr")}))
+        return r
+
+    monkeypatch.setattr(hrouter.ops, "route_decode", spy)
+    m = _module(meta, g, loc)
+    x = torch.from_numpy(g["x"]).to(DEV)
+    out = _run_module_blocks(m, x, meta["S"], meta["blocks"])
+    np.testing.assert_allclose(out, g["out"], atol=F32_TOL, rtol=0)
+    assert len(seen) == len(g["blk_L"])
+    for i, (L, r) in enumerate(seen):
+        assert L == g["blk_L"][i]
+        _same_lists(r["mid"], g["blk_sel"][i])
+        _same_lists(r["mid_thr"], g["blk_sel_thr"][i])
+        _same_lists(r["open_grp"], g["blk_open"][i])
+        _same_lists(r["open_thr"], g["blk_open_thr"][i])
+
+
 @pytest.mark.parametrize("loc", ["ram", "fs"])
 def test_module_host_stores_equal_vram_store(loc):
     meta, g = load_case("mod_decode")

@@ -104,3 +104,34 @@ def test_module_forward_and_decode(name):
             pad = lambda a: np.concatenate(
                 [a, np.full(a.shape[:-1] + (w - a.shape[-1],), -1, np.int32)], -1)
             np.testing.assert_array_equal(pad(r["open_grp"]), pad(ref_open))
+
+
+@pytest.mark.parametrize("name", ["mod_blocks", "mod_blocks64"])
+def test_module_multi_row_blocks(name):
+    """The oracle's L-row decode routing (orc_route_decode with L > 1: chunks pooled over the
+    rows, groups requested over all rows, first visible rows) against the reference module fed
+    blocks of 3, 11 and 64 tokens (make_golden.py:run_module_case with ``blocks``)."""
+    meta, g = load_case(name)
+    om = OracleModule(meta, g)
+    x = torch.from_numpy(g["x"])
+    S = meta["S"]
+    outs, p = [om.forward(x[:, :S], 0)], S
+    for L in meta["blocks"]:
+        outs.append(om.forward(x[:, p:p + L], p))
+        p += L
+    out = torch.cat(outs, dim=1).numpy()
+    np.testing.assert_allclose(out, g["out"], atol=1e-4, rtol=0)
+    assert len(om.decisions) == len(g["blk_L"])
+
+    def same(a, b):
+        w = max(a.shape[-1], b.shape[-1])
+        pad = lambda t: np.concatenate(
+            [t, np.full(t.shape[:-1] + (w - t.shape[-1],), -1, np.int32)], -1)
+        np.testing.assert_array_equal(pad(np.asarray(a)), pad(np.asarray(b)))
+
+    assert max(g["blk_L"]) > 1
+    for i, (ncl, r) in enumerate(om.decisions):
+        same(r["mid"], g["blk_sel"][i])
+        same(r["mid_thr"], g["blk_sel_thr"][i])
+        same(r["open_grp"], g["blk_open"][i])
+        same(r["open_thr"], g["blk_open_thr"][i])
