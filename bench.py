@@ -286,7 +286,9 @@ def run_decode(*, ctx, B, tc, tg, tier, steps, warmup, needles=False, seed=0, bl
     router.seed_store_from_block(0, k_rope[:, :, :ctx], k_raw[:, :, :ctx], v[:, :, :ctx])
     torch.cuda.synchronize()
     ev = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(steps)]
-    stats = dict(open_groups=0, open_groups_union=0, samples=0)
+    stats = dict(open_groups=0, open_groups_union=0, samples=0, gather_ms=0.0, gather_bytes=0)
+    gstage = ops.DecodeStaging()
+    grp_bytes = c["gs"] * Dh * 2 * 2          # K and V of one 16-token group, bf16
 
     def step(i, timed):
         p = ctx + i * block
@@ -321,6 +323,19 @@ def run_decode(*, ctx, B, tc, tg, tier, steps, warmup, needles=False, seed=0, bl
             stats["open_groups"] += n_open
             stats["open_groups_union"] += u
             stats["samples"] += 1
+            if tier == "ram":
+                # the step's gather again, alone on this stream: its deduplicated bytes (one
+                # copy per distinct group and KV head) over its own time
+                src = store.sources(0)
+                g0, g1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                g0.record()
+                ops.gather_decode(hc, routed.n_closed, og, routed.routing["open_thr"],
+                                  routed.routing["Kg"], src["record_k"], src["record_v"], True,
+                                  gstage, H)
+                g1.record()
+                torch.cuda.synchronize()
+                stats["gather_ms"] += g0.elapsed_time(g1)
+                stats["gather_bytes"] += u * grp_bytes
     torch.cuda.synchronize()
     assert torch.isfinite(out.float()).all()
     route_ms = sum(e[0].elapsed_time(e[1]) for e in ev) / steps
@@ -336,7 +351,6 @@ def run_decode(*, ctx, B, tc, tg, tier, steps, warmup, needles=False, seed=0, bl
     torch.cuda.synchronize()
     ms = (time.perf_counter() - t0) * 1e3 / steps
     ns = max(stats["samples"], 1)
-    grp_bytes = c["gs"] * Dh * 2 * 2          # K and V of one 16-token group, bf16
     rd = stats["open_groups"] / ns * grp_bytes
     return dict(ctx=ctx, batch=B, block=block, topk_chunks=tc, topk_groups=tg, tier=tier,
                 steps=steps, ms_per_step=ms, us_per_step_layer=ms * 1e3,
@@ -344,7 +358,21 @@ def run_decode(*, ctx, B, tc, tg, tier, steps, warmup, needles=False, seed=0, bl
                 device_ms=dict(decode_block=route_ms, attention=attn_ms),
                 opened_group_bytes_per_step=rd,
                 opened_group_bytes_per_step_dedup=stats["open_groups_union"] / ns * grp_bytes,
-                h2d_gbs=(rd / (attn_ms * 1e-3) / 1e9) if tier == "ram" else None)
+                gather_ms=stats["gather_ms"] / ns if tier == "ram" else None,
+                h2d_gbs=(stats["gather_bytes"] / (stats["gather_ms"] * 1e-3) / 1e9)
+                if tier == "ram" and stats["gather_ms"] > 0 else None)
+
+
+def _cpu_model():
+    """The host CPU's model name (/proc/cpuinfo), else the platform's processor string."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or platform.machine()
 
 
 def _measured_traffic():
@@ -398,7 +426,7 @@ def main():
     route_gbs = g["route_bytes"] / (t_route * 1e-3) / 1e9
     traffic = _measured_traffic()
     if t_route >= t_attn:
-        roofline = {"kernel": "route_stage1_kernel + route_stage2_kernel <bf16,128>",
+        roofline = {"kernel": "route_fused_kernel<128, false>",
                     "bound": "hbm",
                     "achieved": route_gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                     "frac": route_gbs / HBM_PEAK_GBS, "traffic": traffic,
@@ -458,7 +486,7 @@ def main():
         "backward": g["backward"],
         "c2_40m_8layer_prefill_8k": c2,
         "cpu_baseline": cpu,
-        "host": {"cpu": platform.processor() or platform.machine(), "torch": torch.__version__},
+        "host": {"cpu": _cpu_model(), "torch": torch.__version__},
     }
     print(json.dumps(rec))
 

@@ -611,7 +611,7 @@ bool use_v2(const hga_config* cfg) {
            cfg->group_size % 16 == 0 && cfg->chunk_size % 16 == 0;
 }
 int64_t vt_keys(const hga_config* cfg, int32_t S) {   // Sp: keys per V^T row
-    const int64_t NC = (int64_t)((S + cfg->chunk_size - 1) / cfg->chunk_size) * cfg->chunk_size;
+    const int64_t NC = (int64_t)hga::chunks_of(S, cfg->chunk_size) * cfg->chunk_size;
     return (NC + hga::kVtKeys - 1) / hga::kVtKeys * hga::kVtKeys;
 }
 }  // namespace
@@ -650,7 +650,7 @@ extern "C" int hga_attend_prefill(const hga_config* cfg, int32_t S, const void* 
     a.open_grp = open_grp; a.open_thr = open_thr;
     a.B = cfg->batch; a.H = cfg->heads; a.KVH = cfg->kv_heads; a.S = S;
     a.C = cfg->chunk_size; a.gs = cfg->group_size; a.M = a.C / a.gs;
-    a.N = (S + a.C - 1) / a.C; a.kf = cfg->keep_first; a.kl = cfg->keep_last;
+    a.N = chunks_of(S, a.C); a.kf = cfg->keep_first; a.kl = cfg->keep_last;
     a.Kg = Kg; a.scale = cfg->scale; a.lse = lse;
     int nN, nKc, nKg;
     hga_prefill_widths(cfg, S, &nN, &nKc, &nKg);

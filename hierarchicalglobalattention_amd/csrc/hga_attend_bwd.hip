@@ -553,7 +553,7 @@ extern "C" int hga_attend_prefill_bwd(
     a.open_grp = open_grp; a.open_thr = open_thr;
     a.B = cfg->batch; a.H = cfg->heads; a.KVH = cfg->kv_heads; a.S = S;
     a.C = cfg->chunk_size; a.gs = cfg->group_size; a.M = a.C / a.gs;
-    a.N = (S + a.C - 1) / a.C; a.kf = cfg->keep_first; a.kl = cfg->keep_last;
+    a.N = chunks_of(S, a.C); a.kf = cfg->keep_first; a.kl = cfg->keep_last;
     a.Kg = Kg; a.scale = cfg->scale; a.lse = const_cast<float*>(lse);
     p.dout = dout; p.g_sb = g_sb; p.g_sh = g_sh; p.g_ss = g_ss;
     p.dq = dq; p.dq_sb = dq_sb; p.dq_sh = dq_sh; p.dq_ss = dq_ss;

@@ -102,6 +102,9 @@ __device__ __forceinline__ float okey_inv(uint32_t k) {
 
 // Window ranges for a query chunk / decode step with `n` earlier chunks
 // (vectorized.py:246-253; chunk_placement_policy.py:27-38).
+// Chunks of a block of S tokens (S up to INT32_MAX: computed in 64 bits).
+__host__ __device__ __forceinline__ int chunks_of(int64_t S, int C) { return (int)((S + C - 1) / C); }
+
 __host__ __device__ __forceinline__ void windows(int n, int kf, int kl, int* f_hi, int* l_lo) {
     *f_hi = kf > 0 ? (n < kf ? n : kf) : 0;
     if (kl > 0) {

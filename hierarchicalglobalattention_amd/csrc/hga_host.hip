@@ -57,7 +57,7 @@ extern "C" int32_t hga_prefill_widths(const hga_config* cfg, int32_t S, int32_t*
     int rc = hga::check_config(cfg);
     if (rc) return rc;
     HGA_REQUIRE(S >= 0, HGA_ERR_ARG, "negative S");
-    const int n = (S + cfg->chunk_size - 1) / cfg->chunk_size;
+    const int n = hga::chunks_of(S, cfg->chunk_size);
     const int M = cfg->chunk_size / cfg->group_size;
     const int kc = cfg->topk_chunks > 0 ? (cfg->topk_chunks < n ? cfg->topk_chunks : n) : 0;
     const int kg = cfg->topk_groups > 0 ? (cfg->topk_groups < kc * M ? cfg->topk_groups : kc * M) : 0;

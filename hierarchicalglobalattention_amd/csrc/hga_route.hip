@@ -2116,7 +2116,7 @@ extern "C" int hga_route_prefill(const hga_config* cfg, int32_t S, const void* q
     a.open_grp = open_grp; a.open_thr = open_thr; a.n_open = n_open; a.stats = stats;
     a.B = cfg->batch; a.H = cfg->heads; a.KVH = cfg->kv_heads; a.S = S;
     a.C = cfg->chunk_size; a.M = cfg->chunk_size / cfg->group_size;
-    a.N = (S + a.C - 1) / a.C;
+    a.N = chunks_of(S, a.C);
     a.kf = cfg->keep_first; a.kl = cfg->keep_last;
     a.Kc = cfg->topk_chunks > 0 ? (cfg->topk_chunks < a.N ? cfg->topk_chunks : a.N) : 0;
     const int T2max = a.Kc * a.M;

@@ -135,7 +135,7 @@ extern "C" int hga_summarize(const hga_config* cfg, int32_t S, int64_t pos0, con
                 "hga_summarize: S >= 0 and pos0 a multiple of chunk_size required");
     if (S == 0) return HGA_OK;
     const int C = cfg->chunk_size, gs = cfg->group_size, M = C / gs, Dh = cfg->head_dim;
-    const int N = (S + C - 1) / C;
+    const int N = chunks_of(S, C);
     const size_t lds = sizeof(float) * (size_t)(2 * M * Dh + 2 * (M + 1) * Dh);
     HGA_REQUIRE(lds <= 65536, HGA_ERR_UNSUPPORTED, "hga_summarize: group layout too large");
     dim3 grid(N, cfg->kv_heads, cfg->batch);

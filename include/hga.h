@@ -207,7 +207,9 @@ int32_t hga_decode_widths(const hga_config* cfg, int32_t n_closed, int32_t* Kc, 
  *   mid, mid_thr [B, H, Kc]  routed chunks visible to some row; n_mid [B, H]
  *   open_grp, open_thr [B, H, Kg]  opened groups (chunk*M + group) visible to some row; n_open
  * workspace: hga_route_decode_workspace bytes (the pool's segments' candidate lists), 4-byte
- * aligned, used only by the call's kernels.  Any pool length; L <= 64, topk_chunks <= 64.
+ * aligned, used only by the call's kernels.  Pools of up to (2048 / topk_chunks) * 2048 chunks
+ * (262144 chunks, 16.7M tokens at topk_chunks 16 and chunk_size 64; longer ones are refused with
+ * HGA_ERR_UNSUPPORTED); L <= 64, topk_chunks <= 64.
  */
 int hga_route_decode(const hga_config* cfg, int32_t L, int32_t n_closed, const void* q,
                      int64_t q_sb, int64_t q_sh, int64_t q_ss, const void* chunk_k,

@@ -222,9 +222,10 @@ def prefill(q, k_rope, k_raw, v, cos, sin, *, C, gs, keep_first, keep_last, topk
 
 
 def bench_c3_slab(cfg: dict, budget_s: float = 15.0, seed: int = 0) -> dict:
-    """Times the mirror on the bench workload: summaries for the whole block, then query chunks
-    sampled evenly over the sequence (one at a time) until the budget is used; the layer time is
-    summaries + N * mean per-chunk time."""
+    """Times the mirror on the bench workload: summaries for the whole block, then slabs of 32
+    consecutive query chunks (routed and attended together, as the reference's vectorized path
+    batches chunks) in a strided order over the sequence until the budget is used; the layer
+    time is summaries + the slabs' time scaled to all N chunks (exact when every slab ran)."""
     B, S, H, KVH, Dh = cfg["B"], cfg["S"], cfg["H"], cfg["KVH"], cfg["Dh"]
     C, gs = cfg["C"], cfg["gs"]
     g = torch.Generator().manual_seed(seed)
@@ -248,23 +249,26 @@ def bench_c3_slab(cfg: dict, budget_s: float = 15.0, seed: int = 0) -> dict:
                        1.0 / (gs + math.sqrt(gs)))
     t_sum = time.perf_counter() - t0
     scale = Dh ** -0.5
+    slab = 32
     route_attend_slab(q, kp, vv, ck, gk, geo, cfg["tc"], cfg["tg"], scale, geo.N // 2,
                       geo.N // 2 + 1)   # warm-up
-    times, done = [], []
-    # every chunk, in a strided order so that a budget cut still samples the whole sequence
-    stride = 61 if geo.N % 61 else 59
-    order = [(i * stride) % geo.N for i in range(geo.N)]
+    starts = list(range(0, geo.N, slab))
+    # every slab, in a strided order so that a budget cut still samples the whole sequence
+    stride = next(x for x in (5, 7, 11, 13, 1) if math.gcd(x, len(starts)) == 1)
+    order = [starts[(i * stride) % len(starts)] for i in range(len(starts))]
+    times, done = [], 0
     deadline = time.perf_counter() + budget_s
-    for n in order:
-        if time.perf_counter() > deadline:
+    for n0 in order:
+        if times and time.perf_counter() > deadline:
             break
+        n1 = min(n0 + slab, geo.N)
         a = time.perf_counter()
-        route_attend_slab(q, kp, vv, ck, gk, geo, cfg["tc"], cfg["tg"], scale, n, n + 1)
+        route_attend_slab(q, kp, vv, ck, gk, geo, cfg["tc"], cfg["tg"], scale, n0, n1)
         times.append(time.perf_counter() - a)
-        done.append(n)
-    layer_s = t_sum + geo.N * (sum(times) / len(times))
+        done += n1 - n0
+    layer_s = t_sum + geo.N * (sum(times) / done)
     return dict(tokens_per_s=B * S / layer_s, layer_s=layer_s,
-                sample=(f"RoPE+summaries for all {geo.N} chunks ({t_sum:.2f} s) + {len(done)} of "
-                        f"{geo.N} query chunks spread over the sequence, one at a time, "
-                        f"extrapolated to the full layer; bf16, torch {torch.__version__}, "
+                sample=(f"RoPE+summaries for all {geo.N} chunks ({t_sum:.2f} s) + {done} of "
+                        f"{geo.N} query chunks in {len(times)} slabs of {slab} spread over the "
+                        f"sequence, scaled to the full layer; bf16, torch {torch.__version__}, "
                         f"{torch.get_num_threads()} threads"))

@@ -144,3 +144,24 @@ def test_write_tokens_checks_without_launch():
     assert rc == -1 and b"aligned" in lib.hga_last_error()
     rc = call(4, [(good, [fake, 128 * 64, 64 * 64, 68]), (none, none), (none, none)])
     assert rc == -1 and b"aligned" in lib.hga_last_error()
+
+
+@pytest.mark.skipif(not os.path.exists("/opt/rocm/bin/hipcc"), reason="needs hipcc")
+def test_host_checks_under_address_and_undefined_sanitizers(tmp_path):
+    """The host side of the C ABI (config validation, width / workspace / size queries, every
+    entry point's argument checks, tests/sanitize/capi_checks.cpp) built host-only with
+    -fsanitize=address,undefined and run with boundary and invalid inputs: no report, every
+    status as expected."""
+    import subprocess
+    csrc = os.path.join(ROOT, "hierarchicalglobalattention_amd", "csrc")
+    b = subprocess.run(["make", "-s", "-j8", "-C", csrc, "sanitize"], capture_output=True,
+                       text=True, timeout=600)
+    assert b.returncode == 0, b.stdout[-2000:] + b.stderr[-2000:]
+    exe = os.path.join(ROOT, "hierarchicalglobalattention_amd", "_build", "sanitize",
+                       "capi_checks")
+    env = dict(os.environ, ASAN_OPTIONS="detect_leaks=0:abort_on_error=0",
+               UBSAN_OPTIONS="print_stacktrace=1:halt_on_error=1")
+    r = subprocess.run([exe], capture_output=True, text=True, timeout=300, env=env)
+    assert r.returncode == 0, r.stdout[-2000:] + r.stderr[-4000:]
+    assert "capi_checks: ok" in r.stdout
+    assert "runtime error" not in r.stderr and "AddressSanitizer" not in r.stderr
