@@ -96,6 +96,20 @@ def prefill_max_pool(cfg: HgaConfig) -> int:
     return PREFILL_MAX_POOL_FUSED if fused else PREFILL_MAX_POOL
 
 
+def _rope_tables(cos: torch.Tensor, sin: torch.Tensor, B: int, S: int, D: int):
+    """fp32 contiguous tables and their batch stride (0: one table shared by the batch).
+    Accepted: [S, D] or [Bt, S, D] with Bt 1 or B, sin of cos's shape -- what torch's
+    broadcasting of cos/sin against [B, X, S, D] accepts."""
+    if tuple(sin.shape) != tuple(cos.shape):
+        raise ValueError(f"rotary tables differ in shape: cos {tuple(cos.shape)}, "
+                         f"sin {tuple(sin.shape)}")
+    if cos.dim() not in (2, 3) or tuple(cos.shape[-2:]) != (S, D) or \
+            (cos.dim() == 3 and cos.shape[0] not in (1, B)):
+        raise ValueError(f"rotary table {tuple(cos.shape)} is not [{S}, {D}] or [1|{B}, {S}, {D}]")
+    cb = 0 if cos.dim() == 2 or cos.shape[0] == 1 else S * D
+    return cos.contiguous().float(), sin.contiguous().float(), cb
+
+
 def rope(cfg: HgaConfig, x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor,
          out: torch.Tensor | None = None, steps_in_dtype: bool = False) -> torch.Tensor:
     """Rotate-half RoPE of x [B, X, S, Dh] with tables cos/sin [S, Dh] or [B, S, Dh] (any float
@@ -106,11 +120,7 @@ def rope(cfg: HgaConfig, x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor,
     B, X, S, D = x.shape
     if out is None:
         out = torch.empty((B, X, S, D), dtype=x.dtype, device=x.device)
-    cos = cos.contiguous().float()
-    sin = sin.contiguous().float()
-    if cos.shape[-2:] != (S, D):
-        raise ValueError(f"rotary table {tuple(cos.shape)} does not cover [{S}, {D}]")
-    cb = 0 if cos.dim() == 2 or cos.shape[0] == 1 else S * D
+    cos, sin, cb = _rope_tables(cos, sin, B, S, D)
     check(lib().hga_rope(ctypes.byref(cfg), X, S, _p(x), *_s4(x), _p(out), *_s4(out), _p(cos),
                          _p(sin), cb, ROPE_STEPS_IN_DTYPE if steps_in_dtype else 0, _stream()),
           "hga_rope")
@@ -128,11 +138,7 @@ def rope_qk(cfg: HgaConfig, q: torch.Tensor, k: torch.Tensor, cos: torch.Tensor,
                          f"match the config")
     qo = torch.empty((B, H, S, D), dtype=q.dtype, device=q.device)
     ko = torch.empty(tuple(k.shape), dtype=k.dtype, device=k.device)
-    cos = cos.contiguous().float()
-    sin = sin.contiguous().float()
-    if cos.shape[-2:] != (S, D):
-        raise ValueError(f"rotary table {tuple(cos.shape)} does not cover [{S}, {D}]")
-    cb = 0 if cos.dim() == 2 or cos.shape[0] == 1 else S * D
+    cos, sin, cb = _rope_tables(cos, sin, B, S, D)
     check(lib().hga_rope_qk(ctypes.byref(cfg), S, _p(q), *_s4(q), _p(qo), *_s4(qo), _p(k),
                             *_s4(k), _p(ko), *_s4(ko), _p(cos), _p(sin), cb,
                             ROPE_STEPS_IN_DTYPE if steps_in_dtype else 0, _stream()),

@@ -101,6 +101,12 @@ class HierarchicalGlobalAttentionRouted(nn.Module):
         else:
             q_rope, k_rope = ops.rope_qk(hc, q_raw, k_raw, cos[:, 0], sin[:, 0])
         cos_r, sin_r = cos[:1].to(x.dtype), sin[:1].to(x.dtype)
+        C = self.chunk_size
+        if train and not (start_pos == 0 and (S - 1) // C > 0):
+            # checked before routing, which writes tokens and may close chunks
+            raise NotImplementedError(
+                "backward is supported for a fresh multi-chunk block (start_pos 0, "
+                "S > chunk_size); decode blocks run without gradients")
         with torch.no_grad():
             segments = router.route_query_block(self.layer_idx, q_rope.detach(), k_rope.detach(),
                                                 k_raw.detach(), v.detach(), start_pos,

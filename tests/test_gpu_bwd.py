@@ -235,8 +235,13 @@ def test_module_backward_vs_float64(routed):
 
 
 def test_module_decode_block_backward_raises():
+    """Blocks that are not a fresh multi-chunk block have no backward; the module refuses them
+    before routing, so the router's store is left as it was (a 16-token block would otherwise
+    fill and close chunk 0)."""
     m = hga.HierarchicalGlobalAttentionRouted(d_model=64, nhead=2, kv_heads=1, chunk_size=16,
                                               group_size=4).to(DEV)
-    x = torch.randn(1, 5, 64, device=DEV, requires_grad=True)
-    with pytest.raises(NotImplementedError):
-        m(hidden_states=x)
+    for S in (5, 16):
+        x = torch.randn(1, S, 64, device=DEV, requires_grad=True)
+        with pytest.raises(NotImplementedError):
+            m(hidden_states=x)
+        assert m._kv_router.store.num_closed_chunks(0) == 0

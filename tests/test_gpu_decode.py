@@ -473,23 +473,28 @@ def test_write_tokens_matches_copies(dt, L):
 
 
 def test_write_tokens_past_2g_elements_and_skipped_sets():
-    """Rows beyond element 2^31 of a record are addressed exactly (64-bit offsets), and a row set
-    given as None is left out."""
-    Dh, L = 64, 5
+    """Rows beyond element 2^31 of a record are addressed exactly (64-bit offsets): a record of
+    two sequences whose batch stride exceeds 2^31 elements, rows written near the end of both,
+    so the second sequence's b * d_sb term alone crosses 2^31 (and the whole offset 2^32).  A
+    row set given as None is left out."""
+    Dh, L, B = 64, 5, 2
     rows = (1 << 31) // Dh + 96
-    rec = torch.empty(1, 1, rows, Dh, dtype=torch.bfloat16, device=DEV)
+    rec = torch.empty(B, 1, rows, Dh, dtype=torch.bfloat16, device=DEV)
+    assert rec.stride(0) > (1 << 31)
     try:
         g = torch.Generator(device=DEV).manual_seed(3)
-        k = torch.randn(1, 1, L, Dh, generator=g, device=DEV).to(torch.bfloat16)
-        raw = torch.randn(1, 1, L, Dh, generator=g, device=DEV).to(torch.bfloat16)
-        act = torch.zeros(1, 1, 64, Dh, dtype=torch.bfloat16, device=DEV)
+        k = torch.randn(B, 1, L, Dh, generator=g, device=DEV).to(torch.bfloat16)
+        raw = torch.randn(B, 1, L, Dh, generator=g, device=DEV).to(torch.bfloat16)
+        act = torch.zeros(B, 1, 64, Dh, dtype=torch.bfloat16, device=DEV)
         pos = rows - 40
         before = rec[:, :, pos - 8:pos].clone()
-        ops.write_tokens(_wcfg(1, 1, Dh, torch.bfloat16), L,
+        after = rec[:, :, pos + L:pos + L + 8].clone()
+        ops.write_tokens(_wcfg(B, 1, Dh, torch.bfloat16), L,
                          [(k, rec[:, :, pos:pos + L]), None, (raw, act[:, :, 3:3 + L])])
         torch.cuda.synchronize()
         assert torch.equal(rec[:, :, pos:pos + L], k)
         assert torch.equal(rec[:, :, pos - 8:pos], before)
+        assert torch.equal(rec[:, :, pos + L:pos + L + 8], after)
         assert torch.equal(act[:, :, 3:3 + L], raw)
         assert not act[:, :, :3].any() and not act[:, :, 3 + L:].any()
     finally:
