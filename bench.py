@@ -375,14 +375,15 @@ def _cpu_model():
     return platform.processor() or platform.machine()
 
 
-def _measured_traffic():
-    """HBM bytes per launch of the dominant kernel, from the committed rocprofv3 counter summary
-    (FETCH_SIZE + WRITE_SIZE, scaled by the same counters over a plain copy); None if absent."""
+def _measured_traffic(kernel: str):
+    """HBM bytes per launch of a c3 kernel ("route" or "attention"), from the committed rocprofv3
+    counter summary (FETCH_SIZE + WRITE_SIZE, scaled by the same counters over a plain copy);
+    None if absent."""
     path = os.path.join(HERE, "profiles", "c3_route_prefill_traffic.md")
     try:
         for line in open(path):
-            if line.startswith("traffic_bytes_per_launch:"):
-                return float(line.split(":", 1)[1])
+            if line.startswith(f"traffic_bytes_per_launch_{kernel}:"):
+                return float(line.split(":", 1)[1].split()[0])
     except OSError:
         pass
     return None
@@ -424,8 +425,8 @@ def main():
     t_route, t_attn = g["stage_ms"]["route"], g["stage_ms"]["attention"]
     attn_tflops = g["flops"] / (t_attn * 1e-3) / 1e12
     route_gbs = g["route_bytes"] / (t_route * 1e-3) / 1e9
-    traffic = _measured_traffic()
     if t_route >= t_attn:
+        traffic = _measured_traffic("route")
         roofline = {"kernel": "route_fused_kernel<128, false>",
                     "bound": "hbm",
                     "achieved": route_gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s",
@@ -435,6 +436,7 @@ def main():
                     "score_mfma_frac": g["score_flops"] / (t_route * 1e-3) / 1e12
                                        / MFMA_BF16_PEAK_TFLOPS}
     else:
+        traffic = _measured_traffic("attention")
         roofline = {"kernel": "kv_block_kernel + attend_v2_kernel<128>", "bound": "mfma",
                     "achieved": attn_tflops, "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
                     "frac": attn_tflops / MFMA_BF16_PEAK_TFLOPS, "traffic": traffic}
