@@ -437,7 +437,7 @@ def main():
                                        / MFMA_BF16_PEAK_TFLOPS}
     else:
         traffic = _measured_traffic("attention")
-        roofline = {"kernel": "kv_block_kernel + attend_v2_kernel<128>", "bound": "mfma",
+        roofline = {"kernel": "kv_block_kernel + attend_v3_kernel<128, 2>", "bound": "mfma",
                     "achieved": attn_tflops, "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
                     "frac": attn_tflops / MFMA_BF16_PEAK_TFLOPS, "traffic": traffic}
     dec = None
@@ -479,7 +479,7 @@ def main():
                    "topk_chunks": CFG["tc"], "topk_groups": CFG["tg"], "rope_theta": CFG["theta"]},
         "stages_ms": g["stage_ms"],
         "roofline": roofline,
-        "roofline_attention": {"kernel": "kv_block_kernel + attend_v2_kernel<128>",
+        "roofline_attention": {"kernel": "kv_block_kernel + attend_v3_kernel<128, 2>",
                                "bound": "mfma", "achieved": attn_tflops,
                                "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
                                "frac": attn_tflops / MFMA_BF16_PEAK_TFLOPS,

@@ -9,16 +9,15 @@
 // Masked scores become -inf (the reference's -1e4 fill underflows to exactly 0 in its fp32
 // softmax), the softmax is accumulated online in fp32.
 //
-// bf16 path (head_dim 64/128): one 128-thread workgroup per (batch, head, chunk); wave w owns
-// query rows 32w..32w+31.  64-key tiles are staged in LDS (K row-major, V transposed); scores
-// are computed as S^T = K Q^T with v_mfma_f32_32x32x16_bf16 so each lane holds 32 scores of a
-// single query row, and the output as O^T = V^T P^T so the online-softmax rescale is a per-lane
-// scalar.  Workgroups of the H/KVH heads that share a KV head and chunk are placed on the same
-// XCD (consecutive in that XCD's dispatch order) so their common window/current tiles are L2
-// hits.
+// bf16 path, group and chunk sizes multiples of 16 (head_dim 64/128): kernel v3 below -- the
+// query heads of one KV head share a workgroup and the LDS-staged window / own-chunk K/V tiles,
+// each head's opened groups are staged per head; S^T = K Q^T and O^T = V^T P^T on
+// v_mfma_f32_32x32x16_bf16, software-pipelined.  Other bf16 head_dim 64/128 shapes: a 128-thread
+// workgroup per (batch, head, chunk) with 64-key tiles staged in LDS (K row-major, V transposed).
 // fp32 path (and head_dim 16/32): one wave per query row at a time, VALU dot products, online
 // softmax across the wave.
 #include <algorithm>
+#include <type_traits>
 
 #include "hga_common.h"
 #include "hga_keys.h"
@@ -272,16 +271,8 @@ __global__ __launch_bounds__(kVT) void attend_valu_kernel(AttnArgs A) {
 }
 
 // ------------------------------------------------------------------------------------------
-// bf16 MFMA kernel v2 (group_size and chunk_size multiples of 16): no LDS operands, no barriers
+// bf16 MFMA path (group_size and chunk_size multiples of 16): blocked K/V copies + kernel v3
 // ------------------------------------------------------------------------------------------
-// The key sequence is a list of 16-key blocks (a window or own-chunk block of 16 consecutive
-// tokens, or 16 tokens of an opened group), processed in tiles of two blocks.  One workgroup of
-// two waves owns a (batch, head, chunk), wave w rows 32w..32w+31: S^T = K Q^T, then
-// O^T = V^T P^T, both on v_mfma_f32_32x32x16_bf16.  The two waves share a double-buffered LDS
-// stage per tile: while tile t is computed, tile t+1's K and V blocks are copied into the other
-// stage by direct global->LDS 16-byte loads (global_load_lds_dwordx4), so the copies get a whole
-// tile of cover and hold no registers.
-
 // Blocked operand copies of K and V (one pass per call): a 16-key block is one contiguous run
 // that a stage copy takes verbatim, laid out so that every 16-byte operand read of a wave from
 // LDS is conflict-free (eight consecutive lanes read 128 consecutive bytes):
@@ -362,195 +353,279 @@ __device__ __forceinline__ void lds_copy16_s(const void* sbase, uint32_t voff, u
 #pragma clang diagnostic pop
 
 constexpr float kRescaleLog2 = 8.0f;   // a row's softmax reference may trail its max by 2^8
-constexpr int kV2Threads = 128;        // two waves: rows 0-31 and 32-63 of a query chunk
+// ------------------------------------------------------------------------------------------
+// bf16 MFMA kernel v3: HP query heads of one KV head per workgroup, software-pipelined
+// ------------------------------------------------------------------------------------------
+// The query heads of a KV head see the same windows and own chunk (the reference repeats K/V
+// per head, chunk_router.py:540, vectorized.py:443-472); only their opened groups differ.  A
+// workgroup of 2*HP waves takes HP heads of one (batch, KV head, query chunk), wave w = head
+// slot w/2, rows 32*(w%2)..+31.  Its key sequence is walked in steps of one 32-key tile
+// (two 16-key blocks), in the order
+//   window steps (first window | last window): one tile staged in LDS serves the waves of all
+//     HP heads (copied once, by all threads);
+//   opened steps: each head's two waves compute on that head's own tile of opened groups,
+//     staged in a slot of its own (copied by that head's threads);
+//   own-chunk steps (causal), shared like the windows, last.
+// Software pipeline: step s computes the scores of step s+1 (S = K Q^T, one MFMA chain) in
+// the same straight-line block as the softmax and the O^T += V^T P^T product of step s, so a
+// wave issues its VALU work between its own MFMAs.  K tiles are therefore staged two steps
+// ahead and V tiles one step ahead: the LDS ring holds two K and two V tiles per head slot,
+// and after the barrier that opens step s the slots of K_s and V_{s-1} are refilled with
+// K_{s+2} and V_{s+1}.  Masks: a window or opened block is visible from one row on, so its
+// mask is the exp offset (-inf for a row that does not see the block) and the row maximum
+// is taken over the visible block halves; own-chunk tiles are masked per key.  A row's
+// running sum adds the bf16 P values the PV product uses, two at a time (v_dot2_f32_bf16),
+// except in the variant that stores the log-sum-exp for the backward (fp32 sums).
+// (b, kv head, query chunk, head group) of a v3 workgroup.  Workgroups reach the 8 XCDs
+// round-robin by linear id; each XCD takes a contiguous range of
+// logical = ((b*KVH + kvh)*N + n)*G + hg, so the chunks in flight on one L2 share a KV head.
+__device__ __forceinline__ void group_coords(int nitems, int KVH, int N, int G, int* b, int* kvh,
+                                             int* n, int* hg) {
+    const int bid = blockIdx.x, xcd = bid % 8, slot = bid / 8;
+    const int q = nitems / 8, r = nitems % 8;
+    const int logical = xcd < r ? xcd * (q + 1) + slot : r * (q + 1) + (xcd - r) * q + slot;
+    *hg = logical % G;
+    const int t = logical / G;
+    *n = t % N;
+    const int bk = t / N;
+    *b = bk / KVH;
+    *kvh = bk % KVH;
+}
 
-template <int DH, bool LSE>
-__global__ __launch_bounds__(kV2Threads) void attend_v2_kernel(AttnArgs A,
-                                                               const uint16_t* __restrict__ kbl,
-                                                               const uint16_t* __restrict__ vbl,
-                                                               int Sp, int nb_cap) {
+template <int DH, int HP, bool LSE>
+__global__ __launch_bounds__(128 * HP) void attend_v3_kernel(AttnArgs A,
+                                                             const uint16_t* __restrict__ kbl,
+                                                             const uint16_t* __restrict__ vbl,
+                                                             int Sp, int capS, int capO) {
+    constexpr int NT = 128 * HP;
     constexpr int KS = DH / 16, DB = DH / 32;
-    extern __shared__ __align__(16) int sTab[];   // block table: first position, first row
-    int* sPos = sTab;
-    int* sThr = sTab + nb_cap;
-    int b, h, n;
-    block_coords(A.B * A.H * A.N, A.B, A.H, A.KVH, A.N, &b, &h, &n);
-    const int kvh = h / (A.H / A.KVH);
+    constexpr int BB = 32 * DH;       // bytes of one 16-key block of K or of V
+    constexpr int HT = 2 * BB;        // a half tile: the two K (or V) blocks of one step
+    constexpr int RUNS = HT / 1024;   // 1 KiB runs (64 lanes x 16 bytes) per half tile
+    extern __shared__ __align__(16) int sTab[];
+    int* sPosS = sTab;                     // shared blocks: first position, first visible row
+    int* sThrS = sPosS + capS;
+    int* sPosO = sThrS + capS;             // opened blocks of each head slot: [HP][capO]
+    int* sThrO = sPosO + HP * capO;
+    int* sMeta = sThrO + HP * capO;        // [4]: opened blocks of each head slot
+    unsigned char* sK = reinterpret_cast<unsigned char*>(sMeta + 4);   // [2][HP][HT]
+    unsigned char* sV = sK + 2 * HP * HT;                              // [2][HP][HT]
+
+    const int rep = A.H / A.KVH, G = rep / HP;
+    int b, kvh, n, hg;
+    group_coords(A.B * A.KVH * A.N * G, A.KVH, A.N, G, &b, &kvh, &n, &hg);
     const int C = A.C, gs = A.gs, M = A.M;
     int rows = A.S - n * C;
     if (rows > C) rows = C;
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+    const int j = w >> 1, rh = w & 1;
+    const int h = kvh * rep + hg * HP + j;
     const int l = lane_id(), g = l >> 5, lr = l & 31;
-    const int row = 32 * w + lr;                   // chunk-local query row of this lane
+    const int row = 32 * rh + lr;                  // chunk-local query row of this lane
     const int Kgw = A.Kg > 0 ? A.Kg : 1;
+    const int gpb = gs / 16, bpc = C / 16;
 
-    // opened list length (the router compacts valid entries to the front; an invalid entry
-    // inside the list is never visible)
+    // opened list length of head slot j, in 16-key blocks (the router compacts valid entries
+    // to the front; an invalid entry inside the list is never visible)
     const int32_t* ogp = A.open_grp + (((int64_t)b * A.H + h) * A.N + n) * Kgw;
     const int32_t* otp = A.open_thr + (((int64_t)b * A.H + h) * A.N + n) * Kgw;
-    int last = -1;
-    for (int i = l; i < A.Kg; i += kWave)
-        if (ogp[i] >= 0 && otp[i] >= 0) last = i;
+    if (rh == 0) {
+        int last = -1;
+        for (int i = l; i < A.Kg; i += kWave)
+            if (ogp[i] >= 0 && otp[i] >= 0) last = i;
 #pragma unroll
-    for (int o = 32; o > 0; o >>= 1) last = max(last, __shfl_xor(last, o, kWave));
-    const int nopen = __builtin_amdgcn_readfirstlane(last + 1);   // identical in both waves
+        for (int o = 32; o > 0; o >>= 1) last = max(last, __shfl_xor(last, o, kWave));
+        if (l == 0) sMeta[j] = (last + 1) * gpb;
+    }
     int f_hi, l_lo;
     windows(n, A.kf, A.kl, &f_hi, &l_lo);
-    const int gpb = gs / 16, bpc = C / 16;
-    const int nb1 = f_hi * bpc, nb2 = nb1 + (n - l_lo) * bpc;
-    const int nb3 = nb2 + nopen * gpb, nb4 = nb3 + (rows + 15) / 16;
-    const int ntiles = (nb4 + 1) / 2;              // tiles of two 16-key blocks
-    // block table: first token position and first visible row of every 16-key block
-    for (int gb = threadIdx.x; gb < 2 * ntiles; gb += kV2Threads) {
+    const int nbF = f_hi * bpc, nbW = nbF + (n - l_lo) * bpc;
+    const int nWs = (nbW + 1) / 2;                 // window steps
+    const int nbOwn = (rows + 15) / 16;
+    const int nCs = (nbOwn + 1) / 2;               // own-chunk steps
+    // shared table: window blocks padded to whole tiles, then own-chunk blocks (padding
+    // blocks read block 0 and are never visible)
+    for (int gb = threadIdx.x; gb < 2 * (nWs + nCs); gb += NT) {
         int pos = 0, thr = kNever;
-        if (gb < nb1) {
+        if (gb < nbF) {
             pos = gb * 16;
             thr = 0;
-        } else if (gb < nb2) {
-            pos = l_lo * C + (gb - nb1) * 16;
+        } else if (gb < nbW) {
+            pos = l_lo * C + (gb - nbF) * 16;
             thr = 0;
-        } else if (gb < nb3) {
-            const int gi = (gb - nb2) / gpb, e = (gb - nb2) % gpb;
-            const int grp = ogp[gi], t = otp[gi];
-            if (grp >= 0 && t >= 0) {
-                pos = (grp / M) * C + (grp % M) * gs + 16 * e;
-                thr = t;
-            }
-        } else if (gb < nb4) {
-            pos = n * C + 16 * (gb - nb3);
-            thr = 16 * (gb - nb3);
+        } else if (gb >= 2 * nWs && gb - 2 * nWs < nbOwn) {
+            pos = n * C + 16 * (gb - 2 * nWs);
+            thr = 16 * (gb - 2 * nWs);
         }
-        sPos[gb] = pos;
-        sThr[gb] = thr;
+        sPosS[gb] = pos;
+        sThrS[gb] = thr;
     }
     __syncthreads();
-    // (a wave without rows in a ragged last chunk still takes its share of the stage copies)
-
-    constexpr int BB = 32 * DH;                    // bytes of one 16-key block of K or of V
-    constexpr int STG = 4 * BB;                    // a stage: K blocks a, b, then V blocks a, b
-    unsigned char* sStage = reinterpret_cast<unsigned char*>(sTab + 2 * nb_cap);
-    const uint32_t stage_lds = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) unsigned char*)sStage;
-    const int64_t kvbase = ((int64_t)b * A.KVH + kvh) * (int64_t)Sp * DH;
-    const unsigned char* kblk = reinterpret_cast<const unsigned char*>(kbl + kvbase);
-    const unsigned char* vblk = reinterpret_cast<const unsigned char*>(vbl + kvbase);
-    // Stage copy of tile t: 16-byte piece p = 128 r + thread; a wave's 64 pieces of one r are
-    // consecutive within one block (BB/16 pieces per block), so the LDS side is the wave-uniform
-    // base + 16 * lane that the direct load writes.
-    // per-lane byte offsets within a block of this wave's pieces (p0 % (BB/16) takes two values)
-    const uint32_t voff0 = (uint32_t)(16 * ((64 * w) % (BB / 16)) + 16 * l);
-    const uint32_t voff1 = (uint32_t)(16 * ((128 + 64 * w) % (BB / 16)) + 16 * l);
-    auto copy_tile = [&](int t, int stg) {
-        const int2 p2 = *reinterpret_cast<const int2*>(&sPos[2 * t]);
-        const int64_t ba = (int64_t)(__builtin_amdgcn_readfirstlane(p2.x) >> 4) * BB;
-        const int64_t bbk = (int64_t)(__builtin_amdgcn_readfirstlane(p2.y) >> 4) * BB;
-        const uint32_t dst = __builtin_amdgcn_readfirstlane(stage_lds + (uint32_t)(stg * STG));
+    int nbO = 0;
 #pragma unroll
-        for (int r = 0; r < STG / (16 * kV2Threads); ++r) {
-            const int p0 = 128 * r + 64 * w;
-            const int region = p0 / (BB / 16);
-            const unsigned char* base = (region < 2 ? kblk : vblk) + ((region & 1) ? bbk : ba);
-            lds_copy16_s(base, (p0 % (BB / 16)) < 128 ? voff0 : voff1, dst + (uint32_t)(16 * p0));
+    for (int jj = 0; jj < HP; ++jj) nbO = max(nbO, sMeta[jj]);
+    const int nOs = (nbO + 1) / 2;                 // opened steps (the longest list of the heads)
+    {
+        int* pj = sPosO + j * capO;
+        int* tj = sThrO + j * capO;
+        const int mine = sMeta[j];
+        for (int gb = threadIdx.x - 128 * j; gb < 2 * nOs; gb += 128) {
+            int pos = 0, thr = kNever;
+            if (gb < mine) {
+                const int gi = gb / gpb, e = gb % gpb;
+                const int grp = ogp[gi], t = otp[gi];
+                if (grp >= 0 && t >= 0) {
+                    pos = (grp / M) * C + (grp % M) * gs + 16 * e;
+                    thr = t;
+                }
+            }
+            pj[gb] = pos;
+            tj[gb] = thr;
         }
-    };
+    }
+    const int T = nWs + nOs + nCs;                 // >= 1: rows >= 1
+    const int sC = nWs + nOs;                      // first own-chunk step
+
     const int kcol = 8 * g;                        // this lane's 8 dims per k-step
     bf16x8 qb[KS];
     {
         const uint16_t* qp = reinterpret_cast<const uint16_t*>(A.q) + b * A.q_sb + h * A.q_sh +
                              ((int64_t)n * C + row) * A.q_ss;
 #pragma unroll
-        for (int s = 0; s < KS; ++s) {
+        for (int k = 0; k < KS; ++k) {
             uint4 u = make_uint4(0u, 0u, 0u, 0u);
-            if (row < rows) u = *reinterpret_cast<const uint4*>(qp + 16 * s + kcol);
-            qb[s] = __builtin_bit_cast(bf16x8, u);
+            if (row < rows) u = *reinterpret_cast<const uint4*>(qp + 16 * k + kcol);
+            qb[k] = __builtin_bit_cast(bf16x8, u);
         }
     }
-    __builtin_amdgcn_s_waitcnt(0);   // q is in registers: no compiler wait inside the tile loop
-    // operand reads from a stage: K lane = key lr of the tile (block lr/16), V lane = dim lr of
+    // q is in registers and the list reads are done: the direct LDS copies below are the only
+    // vector memory operations in flight inside the step loop
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();                               // opened tables complete
+
+    const uint32_t k_lds = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) unsigned char*)sK;
+    const uint32_t v_lds = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) unsigned char*)sV;
+    const int64_t kvbase = ((int64_t)b * A.KVH + kvh) * (int64_t)Sp * DH;
+    const unsigned char* kblk = reinterpret_cast<const unsigned char*>(kbl + kvbase);
+    const unsigned char* vblk = reinterpret_cast<const unsigned char*>(vbl + kvbase);
+    // index in sTab of step s's table entries (first positions; the first visible rows follow
+    // at + capS for shared steps, + HP * capO for opened ones), and the head slot its tile is
+    // staged in (0 for shared steps)
+    auto step_tab = [&](int s, int& pi, int& ti, int& hs) __attribute__((always_inline)) {
+        const bool opened = s >= nWs && s < sC;
+        const int i = opened ? 2 * (s - nWs) : 2 * (s < nWs ? s : s - nOs);
+        pi = opened ? 2 * capS + j * capO + i : i;
+        ti = opened ? pi + HP * capO : pi + capS;
+        hs = opened ? j : 0;
+    };
+    // Copy the K (or V) blocks of step s into ring slot s & 1: a shared tile by all waves, an
+    // opened tile by head slot j's two waves.  Run r (1 KiB) of the half tile lies in block
+    // r / (RUNS/2); the direct load writes lane i's 16 bytes at the wave-uniform base + 16 i.
+    auto copy_half = [&](int s, const unsigned char* src, uint32_t lds) __attribute__((always_inline)) {
+        int pi, ti, hs;
+        step_tab(s, pi, ti, hs);
+        const int2 p2 = *reinterpret_cast<const int2*>(&sTab[pi]);
+        const int64_t ba = (int64_t)(__builtin_amdgcn_readfirstlane(p2.x) >> 4) * BB;
+        const int64_t bbk = (int64_t)(__builtin_amdgcn_readfirstlane(p2.y) >> 4) * BB;
+        const uint32_t dst = lds + (uint32_t)(((s & 1) * HP + hs) * HT);
+        auto run = [&](int r) __attribute__((always_inline)) {
+            const int blk = r / (RUNS / 2), off = 1024 * (r % (RUNS / 2));
+            const uint64_t sa = (uint64_t)(uintptr_t)src + (uint64_t)(blk ? bbk : ba);
+            // (readfirstlane returns int: widen through uint32_t, never by sign extension)
+            const uint64_t su =
+                ((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(sa >> 32)) << 32) |
+                (uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)sa);
+            lds_copy16_s(reinterpret_cast<const void*>(su), (uint32_t)(off + 16 * l),
+                         __builtin_amdgcn_readfirstlane(dst + (uint32_t)(blk * BB + off)));
+        };
+        if (s < nWs || s >= sC) {                  // shared: all 2*HP waves
+#pragma unroll
+            for (int rr = 0; rr < (RUNS + 2 * HP - 1) / (2 * HP); ++rr)
+                if (w + 2 * HP * rr < RUNS) run(w + 2 * HP * rr);
+        } else {                                   // opened: head slot j's two waves
+#pragma unroll
+            for (int rr = 0; rr < RUNS / 2; ++rr) run(rh + 2 * rr);
+        }
+    };
+
+    // operand reads from a slot: K lane = key lr of the tile (block lr/16), V lane = dim lr of
     // each 32-dim group; g selects the 8-element half
     const int koff = ((lr >> 4) ? BB : 0) + 256 * g + 16 * (lr & 15);
-    const int voff = 2 * BB + 512 * g + 16 * lr;
+    const int voff = 512 * g + 16 * lr;
     const float c2 = A.scale * 1.4426950408889634f;
-    // raw scores of a tile (S^T: lane = query row, 16 keys per lane)
-    // (two accumulation chains over even and odd k-steps, so consecutive MFMAs do not wait on
-    // each other's results)
-    auto scores_raw = [&](const bf16x8 (&kr)[KS]) {
-        floatx16 s0 = {}, s1 = {};
+    typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+    const bf16x2 ones = {(__bf16)1.0f, (__bf16)1.0f};
+
+    auto read_k = [&](int s, bf16x8 (&kr)[KS]) {
+        int pi, ti, hs;
+        step_tab(s, pi, ti, hs);
+        const unsigned char* base = sK + ((s & 1) * HP + hs) * HT + koff;
 #pragma unroll
-        for (int s = 0; s < KS; s += 2) {
-            s0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kr[s], qb[s], s0, 0, 0, 0);
-            s1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kr[s + 1], qb[s + 1], s1, 0, 0, 0);
-        }
-        return s0 + s1;
+        for (int k = 0; k < KS; ++k)
+            kr[k] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(base + 512 * k));
     };
-    // Mask tile t's scores to the visible keys.  Opened/window blocks have one first-visible
-    // row per block (uniform), so a block is all visible, all hidden, or split at one row for
-    // this wave; own-chunk blocks (index >= nb3) are causal per key.
-    auto mask = [&](int t, floatx16& sc) {
-        const int2 t2 = *reinterpret_cast<const int2*>(&sThr[2 * t]);
-        const int th[2] = {__builtin_amdgcn_readfirstlane(t2.x), __builtin_amdgcn_readfirstlane(t2.y)};
-        const int gb0 = 2 * t;
-        if (gb0 + 1 >= nb3) {
-#pragma unroll
-            for (int i = 0; i < 16; ++i) {
-                const int j = i >> 3;
-                const int within = 8 * ((i >> 2) & 1) + 4 * g + (i & 3);
-                const int thr = th[j] + (gb0 + j >= nb3 ? within : 0);
-                sc[i] = row >= thr ? sc[i] : -INFINITY;
-            }
-        } else {
-#pragma unroll
-            for (int j = 0; j < 2; ++j) {
-                if (th[j] <= 32 * w) continue;          // every row of this wave sees it
-                const bool vis = th[j] <= 32 * w + 31 && row >= th[j];
-#pragma unroll
-                for (int i = 8 * j; i < 8 * j + 8; ++i) sc[i] = vis ? sc[i] : -INFINITY;
-            }
-        }
-    };
-    auto row_max = [&](const floatx16& x) {
-        float m = -INFINITY;
-#pragma unroll
-        for (int i = 0; i < 16; ++i) m = fmaxf(m, x[i]);
-        return fmaxf(m, __shfl_xor(m, 32, kWave));
-    };
-    auto read_k = [&](int t, bf16x8 (&kr)[KS]) {
-        const unsigned char* stg = sStage + (t & 1) * STG + koff;
-#pragma unroll
-        for (int s = 0; s < KS; ++s)
-            kr[s] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(stg + 512 * s));
-    };
-    auto read_v = [&](int t, bf16x8 (&vr)[DB][2]) {
-        const unsigned char* stg = sStage + (t & 1) * STG + voff;
+    auto read_v = [&](int s, bf16x8 (&vr)[DB][2]) {
+        int pi, ti, hs;
+        step_tab(s, pi, ti, hs);
+        const unsigned char* base = sV + ((s & 1) * HP + hs) * HT + voff;
 #pragma unroll
         for (int ks = 0; ks < 2; ++ks)
 #pragma unroll
             for (int d = 0; d < DB; ++d)
                 vr[d][ks] = __builtin_bit_cast(
-                    bf16x8, *reinterpret_cast<const uint4*>(stg + ks * BB + 1024 * d));
+                    bf16x8, *reinterpret_cast<const uint4*>(base + ks * BB + 1024 * d));
+    };
+    auto score = [&](const bf16x8 (&kr)[KS]) {
+        floatx16 x = {};
+#pragma unroll
+        for (int k = 0; k < KS; ++k) x = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kr[k], qb[k], x, 0, 0, 0);
+        return x;
+    };
+    // Mask step s's raw scores: a block visible from row th is masked through the exp offset
+    // (vA/vB: does this row see block a/b); own-chunk tiles per key.  Returns the row maximum
+    // over the visible scores (-inf if none).
+    auto finish = [&](int s, auto causal_tag, floatx16& x, bool& vA, bool& vB) __attribute__((always_inline)) {
+        constexpr bool CAUSAL = decltype(causal_tag)::value;
+        int pi, ti, hs;
+        step_tab(s, pi, ti, hs);
+        const int2 t2 = *reinterpret_cast<const int2*>(&sTab[ti]);
+        const int thA = __builtin_amdgcn_readfirstlane(t2.x);
+        const int thB = __builtin_amdgcn_readfirstlane(t2.y);
+        float m;
+        if constexpr (CAUSAL) {
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const int within = 8 * ((i >> 2) & 1) + 4 * g + (i & 3);
+                x[i] = row >= (i < 8 ? thA : thB) + within ? x[i] : -INFINITY;
+            }
+            vA = vB = true;
+            m = -INFINITY;
+#pragma unroll
+            for (int i = 0; i < 16; ++i) m = fmaxf(m, x[i]);
+        } else {
+            vA = row >= thA;
+            vB = row >= thB;
+            float ma = -INFINITY, mb = -INFINITY;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                ma = fmaxf(ma, x[i]);
+                mb = fmaxf(mb, x[8 + i]);
+            }
+            m = fmaxf(vA ? ma : -INFINITY, vB ? mb : -INFINITY);
+        }
+        return fmaxf(m, __shfl_xor(m, 32, kWave));
     };
 
-    // Softmax reference point per row: the first finite tile max of the row (the accumulators
-    // are still zero then, so adopting it needs no rescale).  Later tiles may exceed it by up
-    // to 2^8 (p <= 256); a row whose tile max goes beyond that rescales its accumulators and
-    // running sum to the new max (rare: a wave-uniform branch skips it otherwise).
     floatx16 acc[DB];
 #pragma unroll
     for (int d = 0; d < DB; ++d) acc[d] = floatx16{};
     float m_ref = -INFINITY, l_run = 0.0f;
-    copy_tile(0, 0);
-    for (int t = 0; t < ntiles; ++t) {
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // this thread's copies of tile t
-        __syncthreads();                                    // everyone's; stage t+1 is free
-        if (t + 1 < ntiles) copy_tile(t + 1, (t + 1) & 1);
-        bf16x8 kr[KS];
-        read_k(t, kr);
-        bf16x8 vr[DB][2];
-        read_v(t, vr);
-        floatx16 sc = scores_raw(kr);
-        mask(t, sc);
-        const float m = row_max(sc);
+    // Adopt a tile's row maximum as the softmax reference: the first finite one (the
+    // accumulators are still zero then), or one beyond the reference by more than 2^8, which
+    // rescales the accumulators and running sum (rare: a wave-uniform branch skips it).
+    auto adopt = [&](float m) __attribute__((always_inline)) {
         bool jump = false;
-        if (m_ref == -INFINITY) m_ref = m;                   // first visible keys (or none yet)
+        if (m_ref == -INFINITY) m_ref = m;
         else jump = (m - m_ref) * c2 > kRescaleLog2;
         if (__builtin_amdgcn_ballot_w64(jump)) {
             if (jump) {
@@ -563,22 +638,88 @@ __global__ __launch_bounds__(kV2Threads) void attend_v2_kernel(AttnArgs A,
                 m_ref = m;
             }
         }
+    };
+    // softmax numerators of the current tile (bf16) and the running sum
+    auto softmax = [&](const floatx16& x, bool vA, bool vB, bf16x8 (&pt)[2]) {
         const float nb = m_ref == -INFINITY ? 0.0f : -m_ref * c2;
-        bf16x8 pt[2];
-        float rs = 0.0f;
+        const float nA = vA ? nb : -INFINITY, nB = vB ? nb : -INFINITY;
+        if constexpr (LSE) {   // the backward's log-sum-exp: fp32 sums of the fp32 values
+            float rs = 0.0f;
 #pragma unroll
-        for (int i = 0; i < 16; ++i) {
-            const float e = __builtin_amdgcn_exp2f(fmaf(sc[i], c2, nb));
-            pt[i >> 3][i & 7] = (__bf16)e;
-            rs += e;
+            for (int i = 0; i < 16; ++i) {
+                const float e = __builtin_amdgcn_exp2f(fmaf(x[i], c2, i < 8 ? nA : nB));
+                pt[i >> 3][i & 7] = (__bf16)e;
+                rs += e;
+            }
+            l_run += rs;
+        } else {
+#pragma unroll
+            for (int i = 0; i < 16; ++i)
+                pt[i >> 3][i & 7] = (__bf16)__builtin_amdgcn_exp2f(fmaf(x[i], c2, i < 8 ? nA : nB));
+#pragma unroll
+            for (int k2 = 0; k2 < 2; ++k2)
+#pragma unroll
+                for (int pr = 0; pr < 4; ++pr) {
+                    const bf16x2 two = {pt[k2][2 * pr], pt[k2][2 * pr + 1]};
+                    l_run = __builtin_amdgcn_fdot2_f32_bf16(two, ones, l_run, false);
+                }
         }
-        l_run += rs;
+    };
+    auto pv = [&](const bf16x8 (&vr)[DB][2], const bf16x8 (&pt)[2]) {
 #pragma unroll
         for (int ks = 0; ks < 2; ++ks)
 #pragma unroll
             for (int d = 0; d < DB; ++d)
                 acc[d] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vr[d][ks], pt[ks], acc[d], 0, 0, 0);
+    };
+
+    // prologue: K_0, V_0 and K_1 staged, scores of step 0
+    copy_half(0, kblk, k_lds);
+    copy_half(0, vblk, v_lds);
+    if (T > 1) copy_half(1, kblk, k_lds);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    floatx16 sc;
+    bool vA, vB;
+    {
+        bf16x8 kr[KS];
+        read_k(0, kr);
+        sc = score(kr);
+        const float m = sC == 0 ? finish(0, std::true_type{}, sc, vA, vB)
+                                : finish(0, std::false_type{}, sc, vA, vB);
+        adopt(m);
     }
+    // step s: stage K_{s+2} and V_{s+1}; scores of step s+1 with the softmax and PV of step s
+    auto step = [&](int s, auto causal_next) __attribute__((always_inline)) {
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // K_{s+1}, V_s copied (this thread)
+        __syncthreads();                                    // by everyone; K_s, V_{s-1} read
+        if (s + 2 < T) copy_half(s + 2, kblk, k_lds);
+        copy_half(s + 1, vblk, v_lds);
+        bf16x8 kr[KS];
+        read_k(s + 1, kr);
+        bf16x8 vr[DB][2];
+        read_v(s, vr);
+        floatx16 sn = score(kr);
+        bf16x8 pt[2];
+        softmax(sc, vA, vB, pt);
+        pv(vr, pt);
+        const float m = finish(s + 1, causal_next, sn, vA, vB);
+        sc = sn;
+        adopt(m);
+    };
+    int s = 0;
+    for (; s + 1 < sC; ++s) step(s, std::false_type{});
+    for (; s + 1 < T; ++s) step(s, std::true_type{});
+    {   // last step: softmax and PV only
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();
+        bf16x8 vr[DB][2];
+        read_v(s, vr);
+        bf16x8 pt[2];
+        softmax(sc, vA, vB, pt);
+        pv(vr, pt);
+    }
+
     const float lt = l_run + __shfl_xor(l_run, 32, kWave);
     if (row >= rows) return;
     if constexpr (LSE)
@@ -605,10 +746,40 @@ __global__ __launch_bounds__(kV2Threads) void attend_v2_kernel(AttnArgs A,
 }  // namespace hga
 
 namespace {
-// v2 applies to bf16, head_dim 64/128, group and chunk sizes that are multiples of 16.
-bool use_v2(const hga_config* cfg) {
+// v3 applies to bf16, head_dim 64/128, group and chunk sizes that are multiples of 16.
+bool use_v3(const hga_config* cfg) {
     return cfg->dtype == HGA_DTYPE_BF16 && (cfg->head_dim == 64 || cfg->head_dim == 128) &&
            cfg->group_size % 16 == 0 && cfg->chunk_size % 16 == 0;
+}
+template <int DH, int HP, bool LSE>
+int launch_v3_t(const hga::AttnArgs& a, const uint16_t* kbl, const uint16_t* vbl, int Sp,
+                int capS, int capO, unsigned grid, size_t lds, hipStream_t st) {
+    auto kern = hga::attend_v3_kernel<DH, HP, LSE>;
+    if (lds > 65536)
+        HGA_REQUIRE(hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                                        hipFuncAttributeMaxDynamicSharedMemorySize,
+                                        (int)lds) == hipSuccess,
+                    HGA_ERR_LAUNCH, "hga_attend_prefill: %zu bytes of LDS refused", lds);
+    kern<<<grid, 128 * HP, lds, st>>>(a, kbl, vbl, Sp, capS, capO);
+    return hga::launch_status("hga_attend_prefill");
+}
+template <int DH, int HP>
+int launch_v3_h(const hga::AttnArgs& a, const uint16_t* kbl, const uint16_t* vbl, int Sp,
+                int capS, int capO, bool lse, unsigned grid, size_t lds, hipStream_t st) {
+    return lse ? launch_v3_t<DH, HP, true>(a, kbl, vbl, Sp, capS, capO, grid, lds, st)
+               : launch_v3_t<DH, HP, false>(a, kbl, vbl, Sp, capS, capO, grid, lds, st);
+}
+template <int DH>
+int launch_v3_d(const hga::AttnArgs& a, const uint16_t* kbl, const uint16_t* vbl, int Sp,
+                int capS, int capO, int HP, bool lse, unsigned grid, size_t lds, hipStream_t st) {
+    if (HP == 2) return launch_v3_h<DH, 2>(a, kbl, vbl, Sp, capS, capO, lse, grid, lds, st);
+    return launch_v3_h<DH, 1>(a, kbl, vbl, Sp, capS, capO, lse, grid, lds, st);
+}
+// v3 launch: head_dim 64/128, HP = query heads of one KV head per workgroup (1 or 2)
+int launch_v3(const hga::AttnArgs& a, const uint16_t* kbl, const uint16_t* vbl, int Sp, int capS,
+              int capO, int D, int HP, bool lse, unsigned grid, size_t lds, hipStream_t st) {
+    return D == 128 ? launch_v3_d<128>(a, kbl, vbl, Sp, capS, capO, HP, lse, grid, lds, st)
+                    : launch_v3_d<64>(a, kbl, vbl, Sp, capS, capO, HP, lse, grid, lds, st);
 }
 int64_t vt_keys(const hga_config* cfg, int32_t S) {   // Sp: keys per V^T row
     const int64_t NC = (int64_t)hga::chunks_of(S, cfg->chunk_size) * cfg->chunk_size;
@@ -622,7 +793,7 @@ extern "C" int hga_attend_prefill_workspace(const hga_config* cfg, int32_t S, in
     if (rc) return rc;
     HGA_REQUIRE(S >= 0 && bytes, HGA_ERR_ARG, "hga_attend_prefill_workspace: bad S/bytes");
     // blocked copies of K and V
-    *bytes = use_v2(cfg) && S > 0
+    *bytes = use_v3(cfg) && S > 0
                  ? 2 * (int64_t)cfg->batch * cfg->kv_heads * cfg->head_dim * vt_keys(cfg, S) * 2
                  : 0;
     return HGA_OK;
@@ -659,7 +830,7 @@ extern "C" int hga_attend_prefill(const hga_config* cfg, int32_t S, const void* 
     const unsigned grid = (unsigned)(a.B * a.H * a.N);
     const size_t lds = sizeof(int) * 2 * (size_t)(Kg > 0 ? Kg : 1);
     hipStream_t st = (hipStream_t)stream;
-    if (use_v2(cfg)) {
+    if (use_v3(cfg)) {
         const uintptr_t al = (uintptr_t)q | (uintptr_t)k | (uintptr_t)v | (uintptr_t)out |
                              (uintptr_t)workspace;
         HGA_REQUIRE(al % 16 == 0 && ((q_sb | q_sh | q_ss | k_sb | k_sh | k_ss | v_sb | v_sh |
@@ -673,30 +844,36 @@ extern "C" int hga_attend_prefill(const hga_config* cfg, int32_t S, const void* 
         const int Sp = (int)vt_keys(cfg, S);
         uint16_t* kbl = (uint16_t*)workspace;
         uint16_t* vbl = kbl + (int64_t)a.B * a.KVH * Sp * D;
-        // 16-key blocks of the longest key sequence, rounded up to whole 2-block tiles; the
-        // windows of chunk n cover min(kf, n) + (n - l_lo) <= min(kf + kl, N - 1) chunks
+        // the windows of chunk n cover min(kf, n) + (n - l_lo) <= min(kf + kl, N - 1) chunks
         const int bpc = a.C / 16;
         const int64_t wch = std::min<int64_t>((int64_t)a.kf + a.kl, a.N - 1);
-        const int nb_cap = (int)(((wch + 1) * bpc + Kg * (a.gs / 16) + 3) / 4 * 4);
-        // block table, then two stages of one tile (K and V of two 16-key blocks)
-        const size_t lds2 = sizeof(int) * 2 * (size_t)nb_cap + 2 * 4 * 32 * (size_t)D;
-        HGA_REQUIRE(lds2 <= 65536, HGA_ERR_UNSUPPORTED,
-                    "hga_attend_prefill: key sequence of %d blocks too long", nb_cap);
+        // query heads of one KV head per workgroup: two (two 2-wave heads share the window and
+        // own-chunk tiles; four heads per workgroup measured slower at the Qwen3 shape: 1.25
+        // against 1.16-1.20 ms, one workgroup per CU by LDS), else one
+        const int rep = a.H / a.KVH;
+        const int HP = rep % 2 == 0 ? 2 : 1;
+        // tables of the shared blocks (windows, own chunk) and of each head's opened blocks,
+        // each padded to whole tiles
+        const int capS = (int)(2 * ((wch * bpc + 1) / 2 + (bpc + 1) / 2));
+        const int capO = std::max(2, (Kg * (a.gs / 16) + 1) / 2 * 2);
+        // tables, then K and V rings of two half tiles per head slot
+        const size_t lds3 = sizeof(int) * (2 * (size_t)capS + 2 * (size_t)HP * capO + 4) +
+                            2 * (size_t)HP * 4 * 32 * D;
+        HGA_REQUIRE(lds3 <= 160 * 1024, HGA_ERR_UNSUPPORTED,
+                    "hga_attend_prefill: key sequence too long for the LDS tables");
+        HGA_REQUIRE((int64_t)Sp * D * 2 < ((int64_t)1 << 32), HGA_ERR_UNSUPPORTED,
+                    "hga_attend_prefill: block of %d tokens too long", S);
         dim3 tg((unsigned)(Sp / kVtKeys), (unsigned)a.KVH, (unsigned)a.B);
-        if (D == 128) {
+        if (D == 128)
             kv_block_kernel<128><<<tg, 256, 0, st>>>((const uint16_t*)k, k_sb, k_sh, k_ss,
                                                      (const uint16_t*)v, v_sb, v_sh, v_ss, kbl,
                                                      vbl, S, Sp, a.KVH);
-            if (lse) attend_v2_kernel<128, true><<<grid, kV2Threads, lds2, st>>>(a, kbl, vbl, Sp, nb_cap);
-            else attend_v2_kernel<128, false><<<grid, kV2Threads, lds2, st>>>(a, kbl, vbl, Sp, nb_cap);
-        } else {
+        else
             kv_block_kernel<64><<<tg, 256, 0, st>>>((const uint16_t*)k, k_sb, k_sh, k_ss,
                                                     (const uint16_t*)v, v_sb, v_sh, v_ss, kbl,
                                                     vbl, S, Sp, a.KVH);
-            if (lse) attend_v2_kernel<64, true><<<grid, kV2Threads, lds2, st>>>(a, kbl, vbl, Sp, nb_cap);
-            else attend_v2_kernel<64, false><<<grid, kV2Threads, lds2, st>>>(a, kbl, vbl, Sp, nb_cap);
-        }
-        return launch_status("hga_attend_prefill");
+        const unsigned grid3 = (unsigned)(a.B * a.KVH * a.N * (rep / HP));
+        return launch_v3(a, kbl, vbl, Sp, capS, capO, D, HP, lse != nullptr, grid3, lds3, st);
     }
     if (cfg->dtype == HGA_DTYPE_BF16 && (D == 64 || D == 128)) {
         const uintptr_t al = (uintptr_t)q | (uintptr_t)k | (uintptr_t)v | (uintptr_t)out;

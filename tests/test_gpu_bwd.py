@@ -89,10 +89,10 @@ def test_attend_prefill_bwd_vs_oracle(case, Kg, keep_lse):
 
 
 @pytest.mark.parametrize("shape", [
-    dict(S=300, Dh=128, C=64, gs=16, dt=torch.bfloat16),   # 16-key-block MFMA kernel
+    dict(S=300, Dh=128, C=64, gs=16, dt=torch.bfloat16),   # pipelined GQA MFMA kernel (v3)
     dict(S=150, Dh=64, C=32, gs=8, dt=torch.bfloat16),     # LDS-tiled MFMA kernel
     dict(S=83, Dh=16, C=8, gs=4, dt=torch.float32),        # VALU kernel
-], ids=["v2", "lds", "valu"])
+], ids=["v3", "lds", "valu"])
 def test_forward_lse_is_logsumexp(shape):
     """The forward's lse output = log2 of the sum over the row's visible keys of
     2^(scale*log2(e)*q.k), float64 under the routing mask."""
