@@ -402,12 +402,13 @@ __global__ __launch_bounds__(128 * HP) void attend_v3_kernel(AttnArgs A,
     constexpr int BB = 32 * DH;       // bytes of one 16-key block of K or of V
     constexpr int HT = 2 * BB;        // a half tile: the two K (or V) blocks of one step
     constexpr int RUNS = HT / 1024;   // 1 KiB runs (64 lanes x 16 bytes) per half tile
+    static_assert(HP == 1 || HP == 2, "sMeta holds one entry per wave, at most four waves");
     extern __shared__ __align__(16) int sTab[];
     int* sPosS = sTab;                     // shared blocks: first position, first visible row
     int* sThrS = sPosS + capS;
     int* sPosO = sThrS + capS;             // opened blocks of each head slot: [HP][capO]
     int* sThrO = sPosO + HP * capO;
-    int* sMeta = sThrO + HP * capO;        // [4]: opened blocks of each head slot
+    int* sMeta = sThrO + HP * capO;        // [4]: last valid list entry seen by each wave
     unsigned char* sK = reinterpret_cast<unsigned char*>(sMeta + 4);   // [2][HP][HT]
     unsigned char* sV = sK + 2 * HP * HT;                              // [2][HP][HT]
 
@@ -425,17 +426,46 @@ __global__ __launch_bounds__(128 * HP) void attend_v3_kernel(AttnArgs A,
     const int Kgw = A.Kg > 0 ? A.Kg : 1;
     const int gpb = gs / 16, bpc = C / 16;
 
-    // opened list length of head slot j, in 16-key blocks (the router compacts valid entries
-    // to the front; an invalid entry inside the list is never visible)
+    // q rows first: their loads overlap the list reads and the table build
+    const int kcol = 8 * g;                        // this lane's 8 dims per k-step
+    bf16x8 qb[KS];
+    {
+        const uint16_t* qp = reinterpret_cast<const uint16_t*>(A.q) + b * A.q_sb + h * A.q_sh +
+                             ((int64_t)n * C + row) * A.q_ss;
+#pragma unroll
+        for (int k = 0; k < KS; ++k) {
+            uint4 u = make_uint4(0u, 0u, 0u, 0u);
+            if (row < rows) u = *reinterpret_cast<const uint4*>(qp + 16 * k + kcol);
+            qb[k] = __builtin_bit_cast(bf16x8, u);
+        }
+    }
+    // Head slot j's opened list, read once by its two waves (entry i by thread i % 128 of the
+    // slot), goes straight into the slot's table: entry i's blocks at i*gpb.., an invalid entry
+    // (group or first row < 0: the router compacts valid entries to the front) and the table's
+    // padding never visible.  The slot's opened steps end after its last valid entry.
     const int32_t* ogp = A.open_grp + (((int64_t)b * A.H + h) * A.N + n) * Kgw;
     const int32_t* otp = A.open_thr + (((int64_t)b * A.H + h) * A.N + n) * Kgw;
-    if (rh == 0) {
+    {
+        const int tl = threadIdx.x - 128 * j;
+        int* pj = sPosO + j * capO;
+        int* tj = sThrO + j * capO;
         int last = -1;
-        for (int i = l; i < A.Kg; i += kWave)
-            if (ogp[i] >= 0 && otp[i] >= 0) last = i;
+        for (int i = tl; i < A.Kg; i += 128) {
+            const int grp = ogp[i], t = otp[i];
+            const bool ok = grp >= 0 && t >= 0;
+            if (ok) last = i;
+            for (int e = 0; e < gpb; ++e) {
+                pj[i * gpb + e] = ok ? (grp / M) * C + (grp % M) * gs + 16 * e : 0;
+                tj[i * gpb + e] = ok ? t : kNever;
+            }
+        }
+        for (int gb = A.Kg * gpb + tl; gb < capO; gb += 128) {
+            pj[gb] = 0;
+            tj[gb] = kNever;
+        }
 #pragma unroll
         for (int o = 32; o > 0; o >>= 1) last = max(last, __shfl_xor(last, o, kWave));
-        if (l == 0) sMeta[j] = (last + 1) * gpb;
+        if (l == 0) sMeta[w] = last;               // per wave (2 * HP <= 4)
     }
     int f_hi, l_lo;
     windows(n, A.kf, A.kl, &f_hi, &l_lo);
@@ -460,48 +490,16 @@ __global__ __launch_bounds__(128 * HP) void attend_v3_kernel(AttnArgs A,
         sPosS[gb] = pos;
         sThrS[gb] = thr;
     }
-    __syncthreads();
-    int nbO = 0;
-#pragma unroll
-    for (int jj = 0; jj < HP; ++jj) nbO = max(nbO, sMeta[jj]);
-    const int nOs = (nbO + 1) / 2;                 // opened steps (the longest list of the heads)
-    {
-        int* pj = sPosO + j * capO;
-        int* tj = sThrO + j * capO;
-        const int mine = sMeta[j];
-        for (int gb = threadIdx.x - 128 * j; gb < 2 * nOs; gb += 128) {
-            int pos = 0, thr = kNever;
-            if (gb < mine) {
-                const int gi = gb / gpb, e = gb % gpb;
-                const int grp = ogp[gi], t = otp[gi];
-                if (grp >= 0 && t >= 0) {
-                    pos = (grp / M) * C + (grp % M) * gs + 16 * e;
-                    thr = t;
-                }
-            }
-            pj[gb] = pos;
-            tj[gb] = thr;
-        }
-    }
-    const int T = nWs + nOs + nCs;                 // >= 1: rows >= 1
-    const int sC = nWs + nOs;                      // first own-chunk step
-
-    const int kcol = 8 * g;                        // this lane's 8 dims per k-step
-    bf16x8 qb[KS];
-    {
-        const uint16_t* qp = reinterpret_cast<const uint16_t*>(A.q) + b * A.q_sb + h * A.q_sh +
-                             ((int64_t)n * C + row) * A.q_ss;
-#pragma unroll
-        for (int k = 0; k < KS; ++k) {
-            uint4 u = make_uint4(0u, 0u, 0u, 0u);
-            if (row < rows) u = *reinterpret_cast<const uint4*>(qp + 16 * k + kcol);
-            qb[k] = __builtin_bit_cast(bf16x8, u);
-        }
-    }
     // q is in registers and the list reads are done: the direct LDS copies below are the only
     // vector memory operations in flight inside the step loop
     __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();                               // opened tables complete
+    __syncthreads();                               // tables complete
+    int nbO = 0;
+#pragma unroll
+    for (int jj = 0; jj < 2 * HP; ++jj) nbO = max(nbO, (sMeta[jj] + 1) * gpb);
+    const int nOs = (nbO + 1) / 2;                 // opened steps (the longest list of the heads)
+    const int T = nWs + nOs + nCs;                 // >= 1: rows >= 1
+    const int sC = nWs + nOs;                      // first own-chunk step
 
     const uint32_t k_lds = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) unsigned char*)sK;
     const uint32_t v_lds = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) unsigned char*)sV;

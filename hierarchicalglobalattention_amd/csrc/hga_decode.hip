@@ -1289,50 +1289,82 @@ __global__ __launch_bounds__(kGT) void gather_plan_kernel(GatherArgs A) {
     }
 }
 
-// One workgroup per (staging slot, kv head, b): copies the group's gs K rows and gs V rows
-// (contiguous in a [.., T, D] record) with 16-byte accesses; slots past the count exit.
-// Persistent copy: workgroup w takes staging slots w, w + G, w + 2G, .. of every (b, kv head),
-// four slots in flight per thread.  A small grid (kGatherWG workgroups) leaves the other CUs to
-// the attention that runs beside the copy on another stream.
+// Persistent copy over the valid staging slots of all (b, kv head) pairs at once: slot v of
+// the flattened list (the (b, kv head) lists one after the other, an exclusive prefix of their
+// counts in LDS locates v's pair) is taken by workgroup v % G, four slots in flight per thread;
+// each copies the group's gs K rows and gs V rows (contiguous in a [.., T, D] record) with
+// 16-byte accesses.  A small grid (kGatherWG workgroups) leaves the other CUs to the attention
+// that runs beside the copy on another stream.
 constexpr int kGatherWG = 128;
 __global__ __launch_bounds__(kGT) void gather_copy_kernel(GatherArgs A) {
-    const int G = gridDim.x;
+    extern __shared__ int sPre[];                      // [nbk + 1] prefix, then [kGT] partials
+    const int G = gridDim.x, nbk = A.B * A.KVH, tid = threadIdx.x;
+    int* sPart = sPre + nbk + 1;
+    const int per = (nbk + kGT - 1) / kGT;
+    const int i0 = tid * per < nbk ? tid * per : nbk, i1 = i0 + per < nbk ? i0 + per : nbk;
+    int part = 0;
+    for (int i = i0; i < i1; ++i) part += A.ucount[i];
+    sPart[tid] = part;
+    __syncthreads();
+    if (tid == 0) {
+        int run = 0;
+        for (int i = 0; i < kGT; ++i) {
+            const int x = sPart[i];
+            sPart[i] = run;
+            run += x;
+        }
+        sPre[nbk] = run;
+    }
+    __syncthreads();
+    {
+        int run = sPart[tid];
+        for (int i = i0; i < i1; ++i) {
+            sPre[i] = run;
+            run += A.ucount[i];
+        }
+    }
+    __syncthreads();
+    const int total = sPre[nbk];
     const int vpr = A.D * A.esz / 16;                  // 16-byte pieces per row
     const int pieces = A.gs * vpr;                     // of one group's K (or V)
-    for (int bk = 0; bk < A.B * A.KVH; ++bk) {
-        const int cnt = A.ucount[bk];
-        const int b = bk / A.KVH, kvh = bk % A.KVH;
-        const int64_t rec = ((int64_t)b * A.d_sb + (int64_t)kvh * A.d_sh) * A.esz;
-        for (int u0 = blockIdx.x; u0 < cnt; u0 += 4 * G) {
-            int64_t src[4], dst[4];
-            bool ok[4];
+    for (int v0 = blockIdx.x; v0 < total; v0 += 4 * G) {
+        int64_t src[4], dst[4];
+        bool ok[4];
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const int u = u0 + j * G;
-                ok[j] = u < cnt;
-                const int g = ok[j] ? A.ulist[(int64_t)bk * A.U + u] : 0;
-                const int64_t p0 = (int64_t)(g / A.M) * A.C + (int64_t)(g % A.M) * A.gs;
-                src[j] = rec + p0 * A.d_ss * A.esz;
-                dst[j] = (((int64_t)bk * A.U + u) * A.gs) * (int64_t)A.D * A.esz;
+        for (int j = 0; j < 4; ++j) {
+            const int v = v0 + j * G;
+            ok[j] = v < total;
+            // the (b, kv head) pair holding v: the last one whose prefix is <= v
+            int lo = 0, hi = nbk - 1;
+            while (lo < hi) {
+                const int mid = (lo + hi + 1) >> 1;
+                if (sPre[mid] <= v) lo = mid;
+                else hi = mid - 1;
             }
-            for (int c = threadIdx.x; c < pieces; c += kGT) {
-                const int r = c / vpr, x = (c % vpr) * 16;
-                const int64_t so = (int64_t)r * A.d_ss * A.esz + x;
-                const int64_t dO = (int64_t)r * A.D * A.esz + x;
-                uint4 kq[4], vq[4];
+            const int bk = lo, u = ok[j] ? v - sPre[bk] : 0;
+            const int b = bk / A.KVH, kvh = bk % A.KVH;
+            const int g = ok[j] ? A.ulist[(int64_t)bk * A.U + u] : 0;
+            const int64_t p0 = (int64_t)(g / A.M) * A.C + (int64_t)(g % A.M) * A.gs;
+            src[j] = ((int64_t)b * A.d_sb + (int64_t)kvh * A.d_sh + p0 * A.d_ss) * A.esz;
+            dst[j] = (((int64_t)bk * A.U + u) * A.gs) * (int64_t)A.D * A.esz;
+        }
+        for (int c = tid; c < pieces; c += kGT) {
+            const int r = c / vpr, x = (c % vpr) * 16;
+            const int64_t so = (int64_t)r * A.d_ss * A.esz + x;
+            const int64_t dO = (int64_t)r * A.D * A.esz + x;
+            uint4 kq[4], vq[4];
 #pragma unroll
-                for (int j = 0; j < 4; ++j)
-                    if (ok[j]) {
-                        kq[j] = *reinterpret_cast<const uint4*>(A.kd + src[j] + so);
-                        vq[j] = *reinterpret_cast<const uint4*>(A.vd + src[j] + so);
-                    }
+            for (int j = 0; j < 4; ++j)
+                if (ok[j]) {
+                    kq[j] = *reinterpret_cast<const uint4*>(A.kd + src[j] + so);
+                    vq[j] = *reinterpret_cast<const uint4*>(A.vd + src[j] + so);
+                }
 #pragma unroll
-                for (int j = 0; j < 4; ++j)
-                    if (ok[j]) {
-                        *reinterpret_cast<uint4*>(A.stage_k + dst[j] + dO) = kq[j];
-                        *reinterpret_cast<uint4*>(A.stage_v + dst[j] + dO) = vq[j];
-                    }
-            }
+            for (int j = 0; j < 4; ++j)
+                if (ok[j]) {
+                    *reinterpret_cast<uint4*>(A.stage_k + dst[j] + dO) = kq[j];
+                    *reinterpret_cast<uint4*>(A.stage_v + dst[j] + dO) = vq[j];
+                }
         }
     }
 }
@@ -1448,7 +1480,9 @@ extern "C" int hga_gather_decode(const hga_config* cfg, int32_t n_closed, const 
     rc = launch_status("hga_gather_decode (plan)");
     if (rc) return rc;
     if (Kg == 0 || n_closed == 0) return HGA_OK;
-    gather_copy_kernel<<<dim3((unsigned)kGatherWG), dim3(kGT), 0, st>>>(a);
+    const size_t lds_c = sizeof(int) * ((size_t)a.B * a.KVH + 1 + kGT);
+    HGA_REQUIRE(lds_c <= 65536, HGA_ERR_UNSUPPORTED, "hga_gather_decode: batch x kv heads too large");
+    gather_copy_kernel<<<dim3((unsigned)kGatherWG), dim3(kGT), lds_c, st>>>(a);
     return launch_status("hga_gather_decode (copy)");
 }
 
