@@ -237,6 +237,23 @@ def copy_calibration(nbytes: int = 1 << 30, reps: int = 3):
     print(json.dumps({"copy_bytes_read": nbytes, "copy_bytes_written": nbytes, "reps": reps}))
 
 
+def h2d_dma_gbs(nbytes: int = 8 << 20, reps: int = 10) -> float:
+    """Host-to-device rate of a contiguous copy from pinned memory (the link's DMA rate), the
+    reference point for the RAM tier's gather of scattered 4 KiB groups."""
+    dev = torch.device("cuda:0")
+    h = torch.empty(nbytes * reps, dtype=torch.uint8, pin_memory=True)
+    d = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+    d.copy_(h[:nbytes], non_blocking=True)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for i in range(reps):
+        d.copy_(h[i * nbytes:(i + 1) * nbytes], non_blocking=True)
+    e1.record()
+    torch.cuda.synchronize()
+    return nbytes * reps / (e0.elapsed_time(e1) * 1e-3) / 1e9
+
+
 DEC_CFG = dict(H=32, KVH=4, Dh=128, C=64, gs=16, kf=2, kl=8, theta=1e6)
 
 
@@ -452,6 +469,7 @@ def main():
                                           steps=max(ds // 8, 4), warmup=4, needles=True),
             "c4_32k_ram_64token_blocks": run_decode(ctx=32768, B=1, tc=16, tg=64, tier="ram",
                                                     steps=max(ds // 8, 4), warmup=4, block=64),
+            "h2d_dma_gbs_contiguous_8mib": h2d_dma_gbs(),
         }
         torch.cuda.empty_cache()
     c2 = None if args.no_c2 else run_c2()

@@ -846,8 +846,7 @@ extern "C" int hga_attend_prefill(const hga_config* cfg, int32_t S, const void* 
         const int bpc = a.C / 16;
         const int64_t wch = std::min<int64_t>((int64_t)a.kf + a.kl, a.N - 1);
         // query heads of one KV head per workgroup: two (two 2-wave heads share the window and
-        // own-chunk tiles; four heads per workgroup measured slower at the Qwen3 shape: 1.25
-        // against 1.16-1.20 ms, one workgroup per CU by LDS), else one
+        // own-chunk tiles; four heads would fit only one workgroup per CU by LDS), else one
         const int rep = a.H / a.KVH;
         const int HP = rep % 2 == 0 ? 2 : 1;
         // tables of the shared blocks (windows, own chunk) and of each head's opened blocks,
