@@ -1358,6 +1358,63 @@ __device__ __forceinline__ int fused_compact(const uint32_t (&kv)[NK], int nk, u
     return base + pair + x32;
 }
 
+// Ascending bitonic sort of the (up to) 64 keys of each query row in the MFMA layout: a row's
+// keys are held by its four lanes l % 16 + 16 qd, element e = 16 qd + i in S[i] (zeros sort
+// first).  In-lane steps for block sizes 2..16, then the size-32 flip against the lane
+// l ^ 16 (element e ^ 31), the size-64 flip against l ^ 48 (element e ^ 63) and its
+// half-cleaner against l ^ 16 (element e ^ 16); the remaining half-cleaners are in-lane.  All 16
+// rows of a wave sort at once, with no LDS round trip.
+__device__ __forceinline__ void q4_ce(uint32_t& a, uint32_t& b) {
+    const uint32_t lo = min(a, b);
+    b = max(a, b);
+    a = lo;
+}
+template <int M>
+__device__ __forceinline__ void q4_inlane(uint32_t (&S)[16]) {
+#pragma unroll
+    for (int i = 0; i < 16; ++i)
+        if ((i ^ M) > i) q4_ce(S[i], S[i ^ M]);
+}
+__device__ __forceinline__ uint32_t q4_x16(uint32_t v) {   // lane ^ 16 (swizzle, xor mask 16)
+    return (uint32_t)__builtin_amdgcn_ds_swizzle((int)v, 0x401f);
+}
+__device__ __forceinline__ void sort64_q4(uint32_t (&S)[16], int qd) {
+    q4_inlane<1>(S);                                                        // size 2
+    q4_inlane<3>(S); q4_inlane<1>(S);                                       // size 4
+    q4_inlane<7>(S); q4_inlane<2>(S); q4_inlane<1>(S);                      // size 8
+    q4_inlane<15>(S); q4_inlane<4>(S); q4_inlane<2>(S); q4_inlane<1>(S);    // size 16
+    uint32_t P[16];
+    {   // size 32: e against e ^ 31 (lane ^ 16, register 15 - i); lanes with even qd keep the minimum
+        const bool lower = (qd & 1) == 0;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) P[i] = q4_x16(S[15 - i]);
+#pragma unroll
+        for (int i = 0; i < 16; ++i) S[i] = lower ? min(S[i], P[i]) : max(S[i], P[i]);
+        q4_inlane<8>(S); q4_inlane<4>(S); q4_inlane<2>(S); q4_inlane<1>(S);
+    }
+    {   // size 64: e against e ^ 63 (lane ^ 48, register 15 - i), then e ^ 16 (lane ^ 16)
+        const bool lower = qd < 2;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) P[i] = (uint32_t)__shfl_xor((int)S[15 - i], 48, kWave);
+#pragma unroll
+        for (int i = 0; i < 16; ++i) S[i] = lower ? min(S[i], P[i]) : max(S[i], P[i]);
+        const bool lower2 = (qd & 1) == 0;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) P[i] = q4_x16(S[i]);
+#pragma unroll
+        for (int i = 0; i < 16; ++i) S[i] = lower2 ? min(S[i], P[i]) : max(S[i], P[i]);
+        q4_inlane<8>(S); q4_inlane<4>(S); q4_inlane<2>(S); q4_inlane<1>(S);
+    }
+}
+// Element pos (0..63, uniform) of each row after sort64_q4, on all four lanes of the row.
+__device__ __forceinline__ uint32_t q4_pick(const uint32_t (&S)[16], int pos, int qd) {
+    uint32_t v = 0u;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) v = (r == (pos & 15) && qd == (pos >> 4)) ? S[r] : v;
+    v = max(v, q4_x16(v));
+    return max(v, (uint32_t)__shfl_xor((int)v, 32, kWave));
+}
+
 __device__ __forceinline__ void fused_request(int t, int id, uint32_t key, uint32_t* sPk,
                                               int* sFirst, uint32_t* sBits, int BW) {
     atomicMax(&sPk[id], key);
@@ -1971,9 +2028,10 @@ void route_fused_kernel(RouteArgs A) {
         return gkb + ((int64_t)sSel[i / M] * M + (i % M)) * DH;
     };
     float knmax2 = 0.0f;
+    uint32_t kv2[16];
+    bool open2 = false;
+    uint32_t kth2 = 0u, k1th2 = 0u;
     if (wave_act) {
-        uint32_t kv2[16];
-        bool open2 = false;
         int nv2 = 0;
         float s1 = 0.0f, s2 = 0.0f;
         int ns = 0;
@@ -1989,29 +2047,66 @@ void route_fused_kernel(RouteArgs A) {
         }
         nv2 = q4_sum(ns);
         open2 = act && nv2 > A.Kgr;
-        if (act && !open2) {
-            // every visible group requested
+        // rows with more visible groups than Kgr: the exact Kgr-th and (Kgr+1)-th largest keys of
+        // the row's T2 <= 64 keys (zeros for the invisible ones), sorted across its four lanes
+        if (__ballot(open2) != 0ull) {                                // wave-uniform
+            uint32_t S[16];
 #pragma unroll
-            for (int i = 0; i < 16; ++i)
-                if (kv2[i] != 0u)
-                    fused_request(t, 16 * (i / 4) + 4 * qd + (i % 4), kv2[i], sPk, sFirst, sBits, BW2);
+            for (int i = 0; i < 16; ++i) S[i] = kv2[i];
+            sort64_q4(S, qd);
+            kth2 = q4_pick(S, 64 - A.Kgr, qd);
+            k1th2 = q4_pick(S, 63 - A.Kgr, qd);
         }
-        if (open2) {
-#pragma unroll
-            for (int i = 0; i < 16; ++i) {
-                const int id = 16 * (i / 4) + 4 * qd + (i % 4);
-                sSv[t * kSvStride + id] = make_uint2(kv2[i], (uint32_t)id);
-            }
-        }
-        if (qd == 0) sRowN[t] = open2 ? kFusedMaxT2 : -1;
         knmax2 = wmax(knmax2);
     }
     if (l == 0) sKn[w] = knmax2;
     __syncthreads();
     knmax2 = fmaxf(fmaxf(sKn[0], sKn[1]), fmaxf(sKn[2], sKn[3]));
     const float ds2 = kDeltaRel * knmax2 * scale * 1.01f;
-    if (wave_act)
-        list_rows<4>(w, A.Kgr, ds2, sQn, sSv, sRowN, nullptr, sPk, sFirst, sBits, BW2, sAmb, &sScal[4], sBand);
+    if (wave_act) {                                                   // wave-uniform
+        // a row whose Kgr-th and (Kgr+1)-th MFMA scores lie within 2*delta (or tie) is rescored
+        // canonically in full
+        bool amb = false;
+        if (open2) {
+            const float delta = ds2 * sQn[t];
+            amb = kth2 == k1th2 || !(okey_inv(kth2) - 2.0f * delta > okey_inv(k1th2));
+            if (amb && qd == 0) {
+                sBand[t] = 0u;
+                sAmb[atomicAdd(&sScal[4], 1)] = t;
+            }
+        }
+        // Requests: every visible group of a row with at most Kgr of them, the certified members
+        // of the others.  A candidate sits in the same register slot of the wave's 16 rows (one
+        // DPP row per lane quarter), so its pooled key (max) and first requesting row (min) over
+        // those rows are 16-lane reductions and cost one atomic pair per candidate and wave;
+        // each row's request bits (T2 <= 64) are stored once.
+        const bool req = act && !amb;
+        const uint32_t lim = open2 ? kth2 : 1u;
+        uint32_t blo = 0u, bhi = 0u;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const int id = 16 * (i / 4) + 4 * qd + (i % 4);
+            const bool mem = req && kv2[i] >= lim && kv2[i] != 0u;
+            const uint32_t mk = r16_umax(mem ? kv2[i] : 0u);
+            const uint32_t fr = r16_umin(mem ? (uint32_t)t : (uint32_t)kNoRow);
+            if (r16 == i && mk != 0u) {
+                atomicMax(&sPk[id], mk);
+                atomicMin(&sFirst[id], (int)fr);
+            }
+            if (mem) {
+                if (id < 32) blo |= 1u << id;
+                else bhi |= 1u << (id - 32);
+            }
+        }
+        blo |= (uint32_t)__shfl_xor((int)blo, 16, kWave);
+        bhi |= (uint32_t)__shfl_xor((int)bhi, 16, kWave);
+        blo |= (uint32_t)__shfl_xor((int)blo, 32, kWave);
+        bhi |= (uint32_t)__shfl_xor((int)bhi, 32, kWave);
+        if (qd == 0 && req) {
+            sBits[t * BW2] = blo;
+            if (BW2 > 1) sBits[t * BW2 + 1] = bhi;
+        }
+    }
     __syncthreads();
     int amb2 = 0, amb2p = 0;
     const int namb2 = sScal[4];
