@@ -1840,6 +1840,10 @@ void route_fused_kernel(RouteArgs A) {
     const uint32_t stage_lds =
         (uint32_t)(uintptr_t)(__attribute__((address_space(3))) unsigned char*)sStage;
 
+    // the first 64 pool candidates go to LDS stage 0 now, so that their copy overlaps the q loads
+    // (vector memory loads complete in order: the compiler's waits for q also cover them)
+    stage_rows<DH>(pool, [&](int r) { return (uint32_t)(r * DH * 2); },
+                   P < kSegCand ? P : kSegCand, stage_lds, w);
     // query rows: B operand (row l % 16, dims 32 ks + 8 qd) and norms
     bf16x8 qb[KS];
     {
@@ -1886,8 +1890,10 @@ void route_fused_kernel(RouteArgs A) {
         uint32_t kv[4 * kSegTiles];
         float s1 = 0.0f, s2 = 0.0f;
         int ns = 0;
-        if (sg > 0) __syncthreads();              // the previous segment's stages are read
-        stage_rows<DH>(pool, [&](int r) { return (uint32_t)((c0 + r) * DH * 2); }, ncs, stage_lds, w);
+        if (sg > 0) {
+            __syncthreads();                      // the previous segment's stages are read
+            stage_rows<DH>(pool, [&](int r) { return (uint32_t)((c0 + r) * DH * 2); }, ncs, stage_lds, w);
+        }
 #pragma unroll
         for (int g = 0; g < kSegTiles / 4; ++g) {
             if (g < ngr) {                                            // workgroup-uniform
