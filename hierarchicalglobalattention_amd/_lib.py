@@ -80,6 +80,11 @@ SIGNATURES = {
     "hga_gather_decode": ([_CFG, _i32, _vp, _vp, _i32, _vp, _vp, _i64, _i64, _i64, _i32, _vp,
                            _vp, _i32, _vp, _vp, _i64, _vp], ctypes.c_int),
     "hga_write_tokens": ([_CFG, _i32] + [_vp, _i64, _i64, _i64] * 6 + [_vp], ctypes.c_int),
+    "hga_attend_decode_overlapped": ([_CFG, _i32, _i32, _i64, _vp, _i64, _i64, _i64, _vp, _vp,
+                                      _i64, _i64, _i64, _i32, _vp, _vp, _i64, _i64, _i64, _vp,
+                                      _vp, _i64, _i64, _i64, _i32, _i32, _vp, _vp, _vp, _i32,
+                                      _vp, _vp, _i32, _vp, _vp, _i64, _vp, _i64, _i64, _i64,
+                                      _vp, _i64, _vp], ctypes.c_int),
 }
 
 _lib = None

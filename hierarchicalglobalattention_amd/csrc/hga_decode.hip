@@ -1943,3 +1943,86 @@ extern "C" int hga_attend_decode_noalloc(const hga_config* cfg, int32_t L, int32
                               record_on_host, open_grp, open_thr, Kg, out, o_sb, o_sh, o_ss, ws,
                               kNoAllocScratchBytes, stream);
 }
+
+// ------------------------------------------------------------------------------------------
+// RAM / disk tier decode attention with the opened groups' copy overlapped (one host call)
+// ------------------------------------------------------------------------------------------
+namespace {
+// Side stream (default priority, non-blocking) and two events per device, for the calling
+// thread: created on first use, kept until the thread ends (a thread's calls are ordered, so
+// its events are never recorded twice before they are waited on).
+struct SideRes {
+    hipStream_t st = nullptr;
+    hipEvent_t ready = nullptr, done = nullptr;   // done: the side stream's work is finished
+};
+constexpr int kMaxDev = 64;
+thread_local SideRes t_side[kMaxDev];
+
+int side_resources(SideRes** out) {
+    int dev = 0;
+    HGA_REQUIRE(hipGetDevice(&dev) == hipSuccess && dev >= 0 && dev < kMaxDev, HGA_ERR_LAUNCH,
+                "hga_attend_decode_overlapped: no current device");
+    SideRes& r = t_side[dev];
+    if (!r.st) {
+        HGA_REQUIRE(hipStreamCreateWithFlags(&r.st, hipStreamNonBlocking) == hipSuccess &&
+                        hipEventCreateWithFlags(&r.ready, hipEventDisableTiming) == hipSuccess &&
+                        hipEventCreateWithFlags(&r.done, hipEventDisableTiming) == hipSuccess,
+                    HGA_ERR_LAUNCH, "hga_attend_decode_overlapped: cannot create the side stream");
+    }
+    *out = &r;
+    return HGA_OK;
+}
+}  // namespace
+
+extern "C" int hga_attend_decode_overlapped(
+    const hga_config* cfg, int32_t L, int32_t n_closed, int64_t start_pos, const void* q,
+    int64_t q_sb, int64_t q_sh, int64_t q_ss, const void* k_recent, const void* v_recent,
+    int64_t r_sb, int64_t r_sh, int64_t r_ss, int32_t ring_chunks, const void* k_first,
+    const void* v_first, int64_t f_sb, int64_t f_sh, int64_t f_ss, const void* k_record,
+    const void* v_record, int64_t d_sb, int64_t d_sh, int64_t d_ss, int32_t record_on_host,
+    int32_t record_chunks, const int32_t* record_grp, const int32_t* open_grp,
+    const int32_t* open_thr, int32_t Kg, void* stage_k, void* stage_v, int32_t stage_groups,
+    int32_t* staged_grp, void* scratch, int64_t scratch_bytes, void* out, int64_t o_sb,
+    int64_t o_sh, int64_t o_ss, void* workspace, int64_t workspace_bytes, void* stream) {
+    using namespace hga;
+    int rc = check_config(cfg);
+    if (rc) return rc;
+    HGA_REQUIRE(q && out && open_grp && open_thr && record_grp && stage_k && stage_v &&
+                    staged_grp,
+                HGA_ERR_ARG, "hga_attend_decode_overlapped: NULL pointer");
+    HGA_REQUIRE(cfg->head_dim == 64 || cfg->head_dim == 128, HGA_ERR_UNSUPPORTED,
+                "hga_attend_decode_overlapped: head_dim 64 or 128");
+    SideRes* sr = nullptr;
+    rc = side_resources(&sr);
+    if (rc) return rc;
+    hipStream_t st = (hipStream_t)stream;
+    const int64_t D = cfg->head_dim, gs = cfg->group_size;
+    const int64_t s_sh = (int64_t)stage_groups * gs * D, s_sb = (int64_t)cfg->kv_heads * s_sh;
+    // The copy is the long pole, so it stays on `stream` right behind the routing; the window and
+    // active-chunk attention (phase 1, partials into the workspace, the record not read) runs on
+    // the side stream, ordered after everything issued on `stream` so far, and `stream` waits for
+    // it only before phase 2, which attends the staged groups and combines all partials.
+    HGA_REQUIRE(hipEventRecord(sr->ready, st) == hipSuccess &&
+                    hipStreamWaitEvent(sr->st, sr->ready, 0) == hipSuccess,
+                HGA_ERR_LAUNCH, "hga_attend_decode_overlapped: cannot order the side stream");
+    rc = hga_attend_decode_phase(cfg, L, n_closed, start_pos, q, q_sb, q_sh, q_ss, k_recent,
+                                 v_recent, r_sb, r_sh, r_ss, ring_chunks, k_first, v_first, f_sb,
+                                 f_sh, f_ss, stage_k, stage_v, s_sb, s_sh, D, 0, open_grp,
+                                 open_thr, Kg, out, o_sb, o_sh, o_ss, 1, workspace,
+                                 workspace_bytes, sr->st);
+    if (rc) return rc;
+    HGA_REQUIRE(hipEventRecord(sr->done, sr->st) == hipSuccess, HGA_ERR_LAUNCH,
+                "hga_attend_decode_overlapped: cannot record the window attention");
+    rc = hga_gather_decode(cfg, record_chunks, record_grp, open_thr, Kg, k_record, v_record, d_sb,
+                           d_sh, d_ss, record_on_host, stage_k, stage_v, stage_groups, staged_grp,
+                           scratch, scratch_bytes, stream);
+    if (rc) return rc;
+    HGA_REQUIRE(hipStreamWaitEvent(st, sr->done, 0) == hipSuccess, HGA_ERR_LAUNCH,
+                "hga_attend_decode_overlapped: cannot wait for the window attention");
+    // phase 2 reads the staging as a record [B, KVH, stage_groups * gs, Dh]
+    return hga_attend_decode_phase(cfg, L, n_closed, start_pos, q, q_sb, q_sh, q_ss, k_recent,
+                                   v_recent, r_sb, r_sh, r_ss, ring_chunks, k_first, v_first, f_sb,
+                                   f_sh, f_ss, stage_k, stage_v, s_sb, s_sh, D, 0, staged_grp,
+                                   open_thr, Kg, out, o_sb, o_sh, o_ss, 2, workspace,
+                                   workspace_bytes, stream);
+}

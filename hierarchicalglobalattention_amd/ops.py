@@ -440,6 +440,40 @@ def write_tokens(cfg: HgaConfig, L: int, pairs) -> None:
           "hga_write_tokens")
 
 
+def attend_decode_overlapped(cfg: HgaConfig, q: torch.Tensor, n_closed: int, start_pos: int,
+                             recent_k: torch.Tensor, recent_v: torch.Tensor, ring_chunks: int,
+                             first_k, first_v, record_k: torch.Tensor, record_v: torch.Tensor,
+                             record_on_host: bool, record_chunks: int, record_grp: torch.Tensor,
+                             open_grp: torch.Tensor, open_thr: torch.Tensor, Kg: int,
+                             staging: "DecodeStaging") -> torch.Tensor:
+    """Decode attention over a host (or page-cache) record in one call
+    (hga_attend_decode_overlapped): the opened groups (record_grp: ids into the record of
+    record_chunks chunks) are copied into ``staging`` on the library's side stream while the
+    windows and the active chunk are attended on the current stream; the staged groups are
+    attended after the copy.  Equals attend_decode over the record.  head_dim 64 or 128."""
+    _dev(q, recent_k, recent_v, open_grp, open_thr, record_grp)
+    B, H, L, D = q.shape
+    if first_k is None:
+        first_k, first_v = recent_k, recent_v
+    if record_on_host and not record_k.is_pinned():
+        raise ValueError("a host record must be pinned memory")
+    for a_, b_ in ((recent_k, recent_v), (first_k, first_v), (record_k, record_v)):
+        if a_.stride() != b_.stride():
+            raise ValueError("K and V of a source must share strides")
+    if not (open_grp.is_contiguous() and open_thr.is_contiguous() and record_grp.is_contiguous()):
+        raise ValueError("the routing lists must be contiguous")
+    U, sk, sv, sg, scr = staging.get(cfg, Kg, H, record_k.dtype, q.device)
+    out = torch.empty((B, H, L, D), dtype=q.dtype, device=q.device)
+    ws = attend_decode_workspace(cfg, L, n_closed, start_pos, Kg, q.device)
+    check(lib().hga_attend_decode_overlapped(
+        ctypes.byref(cfg), L, n_closed, start_pos, _p(q), *_s4(q), _p(recent_k), _p(recent_v),
+        *_s4(recent_k), ring_chunks, _p(first_k), _p(first_v), *_s4(first_k), _p(record_k),
+        _p(record_v), *_s4(record_k), 1 if record_on_host else 0, record_chunks, _p(record_grp),
+        _p(open_grp), _p(open_thr), Kg, _p(sk), _p(sv), U, _p(sg), _p(scr), scr.numel() * 4,
+        _p(out), *_s4(out), _p(ws), ws.numel(), _stream()), "hga_attend_decode_overlapped")
+    return out
+
+
 def attend_decode_workspace(cfg: HgaConfig, L: int, n_closed: int, start_pos: int, Kg: int,
                             device) -> torch.Tensor:
     """A workspace for hga_attend_decode / hga_attend_decode_phase (bytes)."""
@@ -481,19 +515,6 @@ def attend_decode_noalloc(cfg: HgaConfig, q: torch.Tensor, n_closed: int, start_
     return out
 
 
-_SIDE = {}
-
-
-def side_stream(device):
-    """(stream, event, event) per device: a second stream (default priority) for copies that
-    overlap compute, and two reusable events to order it against the compute stream."""
-    key = torch.device(device).index if torch.device(device).index is not None else \
-        torch.cuda.current_device()
-    st = _SIDE.get(key)
-    if st is None:
-        st = (torch.cuda.Stream(device=key), torch.cuda.Event(), torch.cuda.Event())
-        _SIDE[key] = st
-    return st
 
 
 def attend_decode(cfg: HgaConfig, q: torch.Tensor, n_closed: int, start_pos: int,

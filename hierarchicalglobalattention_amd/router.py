@@ -757,23 +757,12 @@ class RoutedKV:
             src.update(record_k=sk, record_v=sv, record_on_host=False)
             return ops.attend_decode(self.hcfg, q, self.n_closed, self.start_pos, open_grp=sg,
                                      open_thr=r["open_thr"], Kg=r["Kg"], **src)
-        main = torch.cuda.current_stream(q.device)
-        side, ready, copied = ops.side_stream(q.device)
-        ready.record(main)                      # routing lists, ring and record writes
-        side.wait_event(ready)
-        with torch.cuda.stream(side):
-            sk, sv, sg = ops.gather_decode(self.hcfg, n_rec, og_rec, r["open_thr"], r["Kg"], rk,
-                                           rv, src["record_on_host"], staging, q.shape[1])
-        copied.record(side)
-        src.update(record_k=sk, record_v=sv, record_on_host=False)
-        ws = ops.attend_decode_workspace(self.hcfg, q.shape[2], self.n_closed, self.start_pos,
-                                         r["Kg"], q.device)
-        out = ops.attend_decode(self.hcfg, q, self.n_closed, self.start_pos, open_grp=og,
-                                open_thr=r["open_thr"], Kg=r["Kg"], phase=1, workspace=ws, **src)
-        main.wait_event(copied)
-        return ops.attend_decode(self.hcfg, q, self.n_closed, self.start_pos, open_grp=sg,
-                                 open_thr=r["open_thr"], Kg=r["Kg"], out=out, phase=2,
-                                 workspace=ws, **src)
+        # one library call: gather on its side stream, windows and active chunk meanwhile
+        return ops.attend_decode_overlapped(
+            self.hcfg, q, self.n_closed, self.start_pos, src["recent_k"], src["recent_v"],
+            src["ring_chunks"], src["first_k"], src["first_v"], rk, rv, src["record_on_host"],
+            n_rec, og_rec.contiguous(), og.contiguous(), r["open_thr"].contiguous(), r["Kg"],
+            staging)
 
     def attend_dca(self, q_intra: torch.Tensor, q_succ: torch.Tensor, q_inter: torch.Tensor,
                    dca_chunk: int) -> torch.Tensor:

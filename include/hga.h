@@ -364,6 +364,30 @@ int hga_gather_decode(const hga_config* cfg, int32_t n_closed, const int32_t* op
                       int32_t record_on_host, void* stage_k, void* stage_v, int32_t stage_groups,
                       int32_t* staged_grp, void* scratch, int64_t scratch_bytes, void* stream);
 
+/*
+ * Decode attention over a host (or page-cache) record with the opened groups' copy overlapped:
+ * RoutedKV.attend for the RAM / disk tiers (chunk_router.py:139-162) with the store's
+ * non-blocking group copy started before the attention that needs it
+ * (ram_kv_cache_store.py:578-607, chunk_router.py:251-252), in one call: hga_gather_decode of
+ * record_grp (the opened groups as ids into the record, record_chunks chunks of it) into the
+ * staging runs on `stream` while hga_attend_decode_phase phase 1 attends the windows and the
+ * active chunk on a side stream of the library (default priority, one per thread and device,
+ * ordered after everything issued on `stream` so far); phase 2 then attends the staged groups
+ * (staged_grp) on `stream` after both.  Arguments as hga_attend_decode_phase (open_grp: the
+ * lists of hga_route_decode, for the list lengths) and hga_gather_decode; the result equals
+ * hga_attend_decode over the record.  head_dim 64 or 128.
+ */
+int hga_attend_decode_overlapped(
+    const hga_config* cfg, int32_t L, int32_t n_closed, int64_t start_pos, const void* q,
+    int64_t q_sb, int64_t q_sh, int64_t q_ss, const void* k_recent, const void* v_recent,
+    int64_t r_sb, int64_t r_sh, int64_t r_ss, int32_t ring_chunks, const void* k_first,
+    const void* v_first, int64_t f_sb, int64_t f_sh, int64_t f_ss, const void* k_record,
+    const void* v_record, int64_t d_sb, int64_t d_sh, int64_t d_ss, int32_t record_on_host,
+    int32_t record_chunks, const int32_t* record_grp, const int32_t* open_grp,
+    const int32_t* open_thr, int32_t Kg, void* stage_k, void* stage_v, int32_t stage_groups,
+    int32_t* staged_grp, void* scratch, int64_t scratch_bytes, void* out, int64_t o_sb,
+    int64_t o_sh, int64_t o_ss, void* workspace, int64_t workspace_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif
