@@ -478,13 +478,17 @@ constexpr int kCap = 32;         // compacted keys per row
 constexpr int kCmpStride = 34;   // per-row buffer: kCap slots, a discard slot, 8-byte aligned
 constexpr int kCompactK = 16;
 
+// (the permutations used here read a lane of the same DPP row, so no lane is out of bounds)
 template <int CTRL>
 __device__ __forceinline__ uint32_t dppu(uint32_t x) {
-    return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, CTRL, 0xf, 0xf, false);
+    return (uint32_t)__builtin_amdgcn_mov_dpp((int)x, CTRL, 0xf, 0xf, true);
 }
-// compare-exchange of this lane's x with partner value p: the lower element keeps the minimum
-__device__ __forceinline__ uint32_t cx(uint32_t x, uint32_t p, bool lower) {
-    return lower ? min(x, p) : max(x, p);
+// Compare-exchange of this lane's x with partner value p: the lower element (hi = 0) keeps the
+// minimum, the upper one (hi = 0xffffffff) the maximum.  max(min(x, p), min(max(x, p), hi)) is
+// the median of {x, p, hi}: one v_med3_u32 instead of a min, a max and a select.
+__device__ __forceinline__ uint32_t cx_mask(bool lower) { return lower ? 0u : 0xffffffffu; }
+__device__ __forceinline__ uint32_t cx(uint32_t x, uint32_t p, uint32_t hi) {
+    return max(min(x, p), min(max(x, p), hi));
 }
 // Ascending bitonic sort of the 32 keys (a = element 2*seg, b = 2*seg + 1) of each 16-lane
 // row: for block sizes 2..32 a flip step (element e against e ^ (size-1), a lane mirror that
@@ -492,13 +496,13 @@ __device__ __forceinline__ uint32_t cx(uint32_t x, uint32_t p, bool lower) {
 __device__ __forceinline__ void sort32_row(uint32_t& a, uint32_t& b, int seg) {
     auto inlane = [&]() { const uint32_t lo = min(a, b); b = max(a, b); a = lo; };
     auto flip = [&](auto pa_fn, int lowbit) {
-        const bool lw = (seg & lowbit) == 0;
+        const uint32_t lw = cx_mask((seg & lowbit) == 0);
         const uint32_t pa = pa_fn(b), pb = pa_fn(a);
         a = cx(a, pa, lw);
         b = cx(b, pb, lw);
     };
     auto half = [&](auto p_fn, int lowbit) {
-        const bool lw = (seg & lowbit) == 0;
+        const uint32_t lw = cx_mask((seg & lowbit) == 0);
         a = cx(a, p_fn(a), lw);
         b = cx(b, p_fn(b), lw);
     };
@@ -533,7 +537,7 @@ __device__ __forceinline__ void sort_inlane4(uint32_t (&R)[4]) {
     }
 }
 template <int ML, class F>
-__device__ __forceinline__ void sort_cross4(uint32_t (&R)[4], F perm, bool lower) {
+__device__ __forceinline__ void sort_cross4(uint32_t (&R)[4], F perm, uint32_t lower) {
     uint32_t P[4];
 #pragma unroll
     for (int r = 0; r < 4; ++r) P[r] = perm(R[r ^ ML]);
@@ -547,7 +551,8 @@ __device__ __forceinline__ void sort64_row(uint32_t (&R)[4], int seg) {
     auto m7 = [](uint32_t v) { return dppu<0x141>(v); };
     auto m15 = [](uint32_t v) { return dppu<0x140>(v); };
     auto x4 = [](uint32_t v) { return (uint32_t)__builtin_amdgcn_ds_swizzle((int)v, 0x101f); };
-    const bool b1 = (seg & 1) == 0, b2 = (seg & 2) == 0, b4 = (seg & 4) == 0, b8 = (seg & 8) == 0;
+    const uint32_t b1 = cx_mask((seg & 1) == 0), b2 = cx_mask((seg & 2) == 0),
+                   b4 = cx_mask((seg & 4) == 0), b8 = cx_mask((seg & 8) == 0);
     sort_inlane4<1>(R);                                                           // size 2
     sort_inlane4<3>(R); sort_inlane4<1>(R);                                       // size 4
     sort_cross4<3>(R, x1, b1); sort_inlane4<2>(R); sort_inlane4<1>(R);            // size 8
@@ -1160,6 +1165,7 @@ constexpr int kSvStride = 66;             // survivor list slots per row: 2 x 32
 constexpr int kFusedMaxPool = 2 * kSegCand;       // pools of the ordinary variant
 constexpr int kFusedMaxPoolLong = 8 * kSegCand;   // pools of the LONG variant (2048 chunks)
 constexpr int kFusedMaxT2 = 64;
+constexpr int kFStageRows = 32;           // candidate rows per stage-1 LDS stage (two stages)
 
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 
@@ -1192,22 +1198,25 @@ __device__ __forceinline__ void route_lds_copy16(const void* sbase, uint32_t vof
 }
 #pragma clang diagnostic pop
 
-// A stage holds 64 candidate rows (DH bf16 each, row-major) with the 16-byte pieces of row r
-// XOR-swizzled: piece j at slot j ^ (r % PPR), so the 16 rows of a tile read the same piece from
-// different banks.  Wave w copies rows 16w..16w+15: row r (< nrows) from sbase + off(r) bytes.
-template <int DH, class Off>
+// A stage holds ROWS (32 or 64) candidate rows (DH bf16 each, row-major) with the 16-byte pieces
+// of row r XOR-swizzled: piece j at slot j ^ (r % PPR), so the 16 rows of a tile read the same
+// piece from different banks.  Wave w copies rows RPW w .. RPW w + RPW - 1 (RPW = ROWS / 4): row
+// r (< nrows) from sbase + off(r) bytes.
+template <int DH, int ROWS, class Off>
 __device__ __forceinline__ void stage_rows(const void* sbase, Off off, int nrows, uint32_t stage,
                                            int w) {
     constexpr int PPR = DH / 8;          // 16-byte pieces per row
     constexpr int RPI = 64 / PPR;        // rows per wave instruction
+    constexpr int RPW = ROWS / 4;        // rows per wave
+    static_assert(RPW % RPI == 0, "a wave copies whole instructions' worth of rows");
     const int l = lane_id();
 #pragma unroll
-    for (int r = 0; r < 16 / RPI; ++r) {
-        const int row = 16 * w + RPI * r + l / PPR;
+    for (int r = 0; r < RPW / RPI; ++r) {
+        const int row = RPW * w + RPI * r + l / PPR;
         const int j = (l % PPR) ^ (row % PPR);
         if (row < nrows)
             route_lds_copy16(sbase, off(row) + 16u * (uint32_t)j,
-                             stage + (uint32_t)((16 * w + RPI * r) * DH * 2));
+                             stage + (uint32_t)((RPW * w + RPI * r) * DH * 2));
     }
 }
 
@@ -1227,12 +1236,12 @@ __device__ __forceinline__ float tile_knorm(const uint4 (&a)[DH / 32]) {
     return __builtin_sqrtf(q4_fsum(x));
 }
 
-// Scores of the wave's rows against the 4 tiles (64 candidates c0 + 16 u + ..) of a stage as
+// Scores of the wave's rows against the NT tiles (16 NT candidates c0 + 16 u + ..) of a stage as
 // order-preserving keys kv[4 tau + i], tau = tau0 + u (0: candidate >= ncand).  A operands from
 // the stage: lane l reads candidate row 16 u + l % 16, dims 32 ks + 8 (l / 16).  Updates knmax
 // with the norms of the tiles with tau % nw == w (the nw active waves see the same candidates:
 // their maximum covers all) and the sample statistics (s1, s2, ns) of tiles 0..3.
-template <int DH, int NK>
+template <int DH, int NK, int NT>
 __device__ __forceinline__ void stage_scores(const unsigned char* stage, int tau0, int c0, int ncand,
                                              int w, int nw, const bf16x8 (&qb)[DH / 32], float scale,
                                              uint32_t (&kv)[NK], float& knmax, float& s1, float& s2,
@@ -1240,7 +1249,7 @@ __device__ __forceinline__ void stage_scores(const unsigned char* stage, int tau
     constexpr int PPR = DH / 8;
     const int l = lane_id(), r16 = l % 16, qd = l / 16;
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
+    for (int u = 0; u < NT; ++u) {
         const int tau = tau0 + u;
         if (tau >= NK / 4) break;
         const int row = 16 * u + r16;
@@ -1385,24 +1394,24 @@ __device__ __forceinline__ void sort64_q4(uint32_t (&S)[16], int qd) {
     q4_inlane<15>(S); q4_inlane<4>(S); q4_inlane<2>(S); q4_inlane<1>(S);    // size 16
     uint32_t P[16];
     {   // size 32: e against e ^ 31 (lane ^ 16, register 15 - i); lanes with even qd keep the minimum
-        const bool lower = (qd & 1) == 0;
+        const uint32_t lower = cx_mask((qd & 1) == 0);
 #pragma unroll
         for (int i = 0; i < 16; ++i) P[i] = q4_x16(S[15 - i]);
 #pragma unroll
-        for (int i = 0; i < 16; ++i) S[i] = lower ? min(S[i], P[i]) : max(S[i], P[i]);
+        for (int i = 0; i < 16; ++i) S[i] = cx(S[i], P[i], lower);
         q4_inlane<8>(S); q4_inlane<4>(S); q4_inlane<2>(S); q4_inlane<1>(S);
     }
     {   // size 64: e against e ^ 63 (lane ^ 48, register 15 - i), then e ^ 16 (lane ^ 16)
-        const bool lower = qd < 2;
+        const uint32_t lower = cx_mask(qd < 2);
 #pragma unroll
         for (int i = 0; i < 16; ++i) P[i] = (uint32_t)__shfl_xor((int)S[15 - i], 48, kWave);
 #pragma unroll
-        for (int i = 0; i < 16; ++i) S[i] = lower ? min(S[i], P[i]) : max(S[i], P[i]);
-        const bool lower2 = (qd & 1) == 0;
+        for (int i = 0; i < 16; ++i) S[i] = cx(S[i], P[i], lower);
+        const uint32_t lower2 = cx_mask((qd & 1) == 0);
 #pragma unroll
         for (int i = 0; i < 16; ++i) P[i] = q4_x16(S[i]);
 #pragma unroll
-        for (int i = 0; i < 16; ++i) S[i] = lower2 ? min(S[i], P[i]) : max(S[i], P[i]);
+        for (int i = 0; i < 16; ++i) S[i] = cx(S[i], P[i], lower2);
         q4_inlane<8>(S); q4_inlane<4>(S); q4_inlane<2>(S); q4_inlane<1>(S);
     }
 }
@@ -1769,29 +1778,54 @@ __device__ __forceinline__ int fused_pool_fast(int P, int k, const uint32_t* sPk
 }
 
 // General pooled selection (certified with canonical pooled values, forced-candidate
-// eviction): the split kernels' routine, out of line.
+// eviction): the split kernels' routine, out of line.  Returns the count in the low 16 bits and
+// the number of canonically rescored pooled candidates above them (a value, not an out-pointer,
+// so that the caller keeps no stack slot).
 template <int DH, int J>
 __device__ __noinline__ int fused_pool_general(int P, int k, int rows, const uint32_t* sBits, int BW,
                                                const uint32_t* sPk, const int* sFirst, float dpool,
                                                const uint16_t* qg, int64_t q_ss, const uint16_t* kb,
                                                float scale, int ip, int base_id, int* sSel,
-                                               int* sThr, int* amb) {
+                                               int* sThr) {
     auto canon = [&](int t, int i) {
         return canon_dot<HGA_DTYPE_BF16, DH>(qg + t * q_ss, kb + (int64_t)i * DH, scale);
     };
-    return pooled_select<J>(P, k, rows, sBits, BW, sPk, sFirst, dpool, canon,
-                                                 ip, base_id, sSel, sThr, amb);
+    int amb = 0;
+    const int cnt = pooled_select<J>(P, k, rows, sBits, BW, sPk, sFirst, dpool, canon,
+                                     ip, base_id, sSel, sThr, &amb);
+    return cnt | (amb << 16);
+}
+
+// LDS: [stage region][survivors][row and selection scalars][pooled state (LONG only)].  The stage
+// region holds the two stage-1 stages; the ordinary variant keeps its pooled state (pooled keys,
+// first requesting rows, request bits) there once stage-1 scoring is over, and stages stage 2's
+// group rows in the survivor area, which is free by then: about 51 KB (Dh 128), three
+// workgroups per CU.
+size_t fused_lds(const RouteArgs& a, int D, bool lng) {
+    const size_t stage = 2 * (size_t)kFStageRows * D * 2;
+    const size_t pooled = 2 * sizeof(int) * (size_t)a.SPP + sizeof(uint32_t) * kRows * (size_t)a.BW;
+    const size_t misc = sizeof(float) * kRows + 3 * sizeof(int) * kRows +
+                        sizeof(int) * (2 * kMaxSel + 8 + kRows) + sizeof(float) * 4;
+    const size_t surv = sizeof(uint2) * kRows * kSvStride;
+    if (lng) return stage + surv + misc + pooled;
+    return (stage > ((pooled + 15) & ~(size_t)15) ? stage : ((pooled + 15) & ~(size_t)15)) + surv + misc;
 }
 
 template <int DH, bool LONG>
-__global__ __launch_bounds__(kFThreads) __attribute__((amdgpu_waves_per_eu(2)))
+__global__ __launch_bounds__(kFThreads) __attribute__((amdgpu_waves_per_eu(LONG ? 2 : 3)))
 void route_fused_kernel(RouteArgs A) {
     constexpr int KS = DH / 32;
     constexpr int PJ = (LONG ? kFusedMaxPoolLong : kFusedMaxPool) / kWave;   // pool slots per lane
-    constexpr int kStageBytes = 64 * DH * 2;                           // 64 candidate rows
+    constexpr int SR = kFStageRows;                                    // candidate rows per stage
+    constexpr int GT = SR / 16;                                        // tiles per stage
+    constexpr int kStageBytes = SR * DH * 2;
     extern __shared__ __align__(16) unsigned char smem_raw[];
-    unsigned char* sStage = smem_raw;                                  // [2][64][DH] candidate rows
-    uint2* sSv = reinterpret_cast<uint2*>(sStage + 2 * kStageBytes);   // [64][kSvStride] survivors
+    unsigned char* sStage = smem_raw;                                  // [2][SR][DH] candidate rows
+    const int pooled_bytes = (8 * A.SPP + 4 * kRows * A.BW + 15) & ~15;
+    const int region = LONG || pooled_bytes < 2 * kStageBytes ? 2 * kStageBytes : pooled_bytes;
+    uint2* sSv = reinterpret_cast<uint2*>(sStage + region);            // [64][kSvStride] survivors
+    // stage 2's group rows: the survivor area (ordinary) or the two stages (LONG)
+    unsigned char* sStage2 = LONG ? sStage : reinterpret_cast<unsigned char*>(sSv);
     float* sQn = reinterpret_cast<float*>(sSv + kRows * kSvStride);    // [64] row norms
     int* sRowN = reinterpret_cast<int*>(sQn + kRows);                  // [64] survivors of a row
     uint32_t* sBand = reinterpret_cast<uint32_t*>(sRowN + kRows);      // [64] re-rank band key
@@ -1801,9 +1835,11 @@ void route_fused_kernel(RouteArgs A) {
     int* sScal = sThr + kMaxSel;                                       // [8]
     int* sAmb = sScal + 8;                                             // [64]
     float* sKn = reinterpret_cast<float*>(sAmb + kRows);               // [4] per-wave norm maxima
-    uint32_t* sPk = reinterpret_cast<uint32_t*>(sKn + 4);              // [SPP] pooled key
-    int* sFirst = reinterpret_cast<int*>(sPk + A.SPP);                 // [SPP]
-    uint32_t* sBits = reinterpret_cast<uint32_t*>(sFirst + A.SPP);     // [64][BW]
+    // pooled state (zeroed once stage-1 scoring is over): [SPP] pooled key, [SPP] first
+    // requesting row, [64][BW] request bits
+    uint32_t* sPk = LONG ? reinterpret_cast<uint32_t*>(sKn + 4) : reinterpret_cast<uint32_t*>(smem_raw);
+    int* sFirst = reinterpret_cast<int*>(sPk + A.SPP);
+    uint32_t* sBits = reinterpret_cast<uint32_t*>(sFirst + A.SPP);
 
     const int N = A.N, C = A.C, M = A.M, BW = A.BW;
     const int n = A.n_hi - 1 - (int)(blockIdx.x / (A.B * A.H));       // heavy chunks first
@@ -1840,35 +1876,37 @@ void route_fused_kernel(RouteArgs A) {
     const uint32_t stage_lds =
         (uint32_t)(uintptr_t)(__attribute__((address_space(3))) unsigned char*)sStage;
 
-    // the first 64 pool candidates go to LDS stage 0 now, so that their copy overlaps the q loads
+    // the first SR pool candidates go to LDS stage 0 now, so that their copy overlaps the q loads
     // (vector memory loads complete in order: the compiler's waits for q also cover them)
-    stage_rows<DH>(pool, [&](int r) { return (uint32_t)(r * DH * 2); },
-                   P < kSegCand ? P : kSegCand, stage_lds, w);
-    // query rows: B operand (row l % 16, dims 32 ks + 8 qd) and norms
+    stage_rows<DH, SR>(pool, [&](int r) { return (uint32_t)(r * DH * 2); }, P < SR ? P : SR,
+                       stage_lds, w);
+    // query rows: B operand (row l % 16, dims 32 ks + 8 qd) and norms.  The ordinary variant
+    // reads q again for stage 2 (from L2: a plain load here allocates it there) rather than keep
+    // it in registers through the stage-1 selection, whose out-of-line calls would have to save
+    // it; the LONG variant streams q once (non-temporal, so its larger summaries stay in L2)
     bf16x8 qb[KS];
-    {
+    auto load_q = [&](const uint16_t* qp, bool nt, float* sumsq) __attribute__((always_inline)) {
         float x = 0.0f;
 #pragma unroll
         for (int ks = 0; ks < KS; ++ks) {
             uint4 u = make_uint4(0u, 0u, 0u, 0u);
-            // q is streamed once (256 MiB at 32K): non-temporal, so the summaries stay in L2
             if (act) {
                 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
-                const u32x4 r = __builtin_nontemporal_load(
-                    reinterpret_cast<const u32x4*>(qg + (int64_t)t * A.q_ss + 32 * ks + 8 * qd));
+                const u32x4* src = reinterpret_cast<const u32x4*>(qp + (int64_t)t * A.q_ss + 32 * ks + 8 * qd);
+                const u32x4 r = nt ? __builtin_nontemporal_load(src) : *src;
                 u = make_uint4(r.x, r.y, r.z, r.w);
             }
-            x += sumsq_bf16x8(u);
+            if (sumsq) x += sumsq_bf16x8(u);
             qb[ks] = as_bf16x8(u);
         }
+        if (sumsq) *sumsq = x;
+    };
+    {
+        float x = 0.0f;
+        load_q(qg, LONG, &x);
         x = q4_fsum(x);
         if (qd == 0) sQn[t] = __builtin_sqrtf(x);
     }
-    for (int i = threadIdx.x; i < A.SPP; i += kFThreads) {
-        sPk[i] = 0u;
-        sFirst[i] = kNoRow;
-    }
-    for (int i = threadIdx.x; i < kRows * BW; i += kFThreads) sBits[i] = 0u;
     if (threadIdx.x < 8) sScal[threadIdx.x] = 0;
     __syncthreads();
 
@@ -1880,45 +1918,39 @@ void route_fused_kernel(RouteArgs A) {
     bool hard = false;
     uint32_t tmax = 1u;                         // largest compaction threshold of the segments
     const int nseg = (P + kSegCand - 1) / kSegCand;
+    uint32_t kv[4 * kSegTiles];
     for (int sg = 0; sg < nseg; ++sg) {
-        // every wave copies a quarter of each 64-candidate group into an LDS stage (double
+        // every wave copies a quarter of each SR-candidate group into an LDS stage (double
         // buffered, one group ahead); the waves with query rows score the stage
         const int c0 = sg * kSegCand;
         const int ncs = P - c0 < kSegCand ? P - c0 : kSegCand;
         const int nt = (ncs + 15) / 16;
-        const int ngr = (nt + 3) / 4;
-        uint32_t kv[4 * kSegTiles];
+        const int ngr = (nt + GT - 1) / GT;
         float s1 = 0.0f, s2 = 0.0f;
         int ns = 0;
         if (sg > 0) {
             __syncthreads();                      // the previous segment's stages are read
-            stage_rows<DH>(pool, [&](int r) { return (uint32_t)((c0 + r) * DH * 2); }, ncs, stage_lds, w);
+            stage_rows<DH, SR>(pool, [&](int r) { return (uint32_t)((c0 + r) * DH * 2); }, ncs,
+                               stage_lds, w);
         }
 #pragma unroll
-        for (int g = 0; g < kSegTiles / 4; ++g) {
+        for (int g = 0; g < kSegTiles / GT; ++g) {
             if (g < ngr) {                                            // workgroup-uniform
                 __builtin_amdgcn_s_waitcnt(0);
                 __syncthreads();          // stage g % 2 complete, stage (g + 1) % 2 no longer read
                 if (g + 1 < ngr)
-                    stage_rows<DH>(pool, [&](int r) { return (uint32_t)((c0 + 64 * (g + 1) + r) * DH * 2); },
-                                   ncs - 64 * (g + 1), stage_lds + (uint32_t)(((g + 1) & 1) * kStageBytes), w);
+                    stage_rows<DH, SR>(pool, [&](int r) { return (uint32_t)((c0 + SR * (g + 1) + r) * DH * 2); },
+                                       ncs - SR * (g + 1), stage_lds + (uint32_t)(((g + 1) & 1) * kStageBytes), w);
                 if (wave_act)
-                    stage_scores<DH, 4 * kSegTiles>(sStage + (g & 1) * kStageBytes, 4 * g, c0 + 64 * g, P,
-                                                    w, nwact, qb, scale, kv, knmax, s1, s2, ns);
+                    stage_scores<DH, 4 * kSegTiles, GT>(sStage + (g & 1) * kStageBytes, GT * g, c0 + SR * g,
+                                                        P, w, nwact, qb, scale, kv, knmax, s1, s2, ns);
             } else {
 #pragma unroll
-                for (int i = 16 * g; i < 16 * g + 16; ++i) kv[i] = 0u;
+                for (int i = 4 * GT * g; i < 4 * GT * (g + 1); ++i) kv[i] = 0u;
             }
         }
         if (!wave_act) continue;
-        if (!open) {
-            // every valid candidate requested (P <= Kc: one tile)
-            if (act) {
-#pragma unroll
-                for (int i = 0; i < 4; ++i)
-                    if (kv[i] != 0u) fused_request(t, 4 * qd + i, kv[i], sPk, sFirst, sBits, BW);
-            }
-        } else {
+        if (open) {
             s1 = q4_fsum(s1);
             s2 = q4_fsum(s2);
             ns = q4_sum(ns);
@@ -1949,6 +1981,13 @@ void route_fused_kernel(RouteArgs A) {
             }
         }
     }
+    // the stages are read: the pooled state (in the stage region of the ordinary variant) is set up
+    __syncthreads();
+    for (int i = threadIdx.x; i < A.SPP; i += kFThreads) {
+        sPk[i] = 0u;
+        sFirst[i] = kNoRow;
+    }
+    for (int i = threadIdx.x; i < kRows * BW; i += kFThreads) sBits[i] = 0u;
     if (wave_act) {
         if (qd == 0) {
             sRowN[t] = !open ? -1 : (hard ? -2 : nsurv);
@@ -1960,6 +1999,12 @@ void route_fused_kernel(RouteArgs A) {
     __syncthreads();
     knmax = fmaxf(fmaxf(sKn[0], sKn[1]), fmaxf(sKn[2], sKn[3]));
     const float ds1 = kDeltaRel * knmax * scale * 1.01f;
+    if (act && !open) {
+        // every valid candidate requested (P <= Kc: one segment, one tile)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            if (kv[i] != 0u) fused_request(t, 4 * qd + i, kv[i], sPk, sFirst, sBits, BW);
+    }
     if (wave_act) {
         if (nseg > 1)
             list_rows<4>(w, kreq, ds1, sQn, sSv, sRowN, sRowT, sPk, sFirst, sBits, BW, sAmb, &sScal[4], sBand);
@@ -1996,9 +2041,12 @@ void route_fused_kernel(RouteArgs A) {
         const int prev = n - 1;
         const int ip = (n > 0 && prev >= f_hi && prev < l_lo) ? prev - f_hi : -1;
         int cnt = fused_pool_fast<PJ>(P, A.Kc, sPk, sFirst, dpool, ip, f_hi, sSel, sThr, sSv);
-        if (cnt < 0)
-            cnt = fused_pool_general<DH, PJ>(P, A.Kc, rows, sBits, BW, sPk, sFirst, dpool, qg, A.q_ss,
-                                         pool, scale, ip, f_hi, sSel, sThr, &amb1p);
+        if (cnt < 0) {
+            const int r = fused_pool_general<DH, PJ>(P, A.Kc, rows, sBits, BW, sPk, sFirst, dpool, qg,
+                                                     A.q_ss, pool, scale, ip, f_hi, sSel, sThr);
+            cnt = r & 0xffff;
+            amb1p = r >> 16;
+        }
         if (l == 0) sScal[0] = cnt;
     }
     __syncthreads();
@@ -2019,9 +2067,11 @@ void route_fused_kernel(RouteArgs A) {
     }
     const int T2 = nsel * M;
     const int BW2 = A.BW2;
-    __syncthreads();                              // the stage-1 stages are read
-    stage_rows<DH>(gkb, [&](int r) { return (uint32_t)(((int64_t)sSel[r / M] * M + (r % M)) * DH * 2); },
-                   T2, stage_lds, w);
+    __syncthreads();                              // the stage-1 stages / survivor lists are read
+    const uint32_t stage2_lds =
+        (uint32_t)(uintptr_t)(__attribute__((address_space(3))) unsigned char*)sStage2;
+    stage_rows<DH, 64>(gkb, [&](int r) { return (uint32_t)(((int64_t)sSel[r / M] * M + (r % M)) * DH * 2); },
+                       T2, stage2_lds, w);
     for (int i = threadIdx.x; i < T2 + 1; i += kFThreads) {
         sPk[i] = 0u;
         sFirst[i] = kNoRow;
@@ -2041,7 +2091,12 @@ void route_fused_kernel(RouteArgs A) {
         int nv2 = 0;
         float s1 = 0.0f, s2 = 0.0f;
         int ns = 0;
-        stage_scores<DH, 16>(sStage, 0, 0, T2, w, nwact, qb, scale, kv2, knmax2, s1, s2, ns);
+        if constexpr (!LONG) {
+            const uint16_t* qg2 = qg;
+            asm volatile("" : "+s"(qg2));        // a fresh read: q is not kept from stage 1
+            load_q(qg2, false, nullptr);
+        }
+        stage_scores<DH, 16, 4>(sStage2, 0, 0, T2, w, nwact, qb, scale, kv2, knmax2, s1, s2, ns);
         // candidate c is visible to row t from its parent's first row on
         ns = 0;
 #pragma unroll
@@ -2144,12 +2199,6 @@ void route_fused_kernel(RouteArgs A) {
         if (A.stats && l == 0 && amb2p) atomicAdd(&A.stats[3], amb2p);
     }
     if (A.stats && l == 0 && amb2) atomicAdd(&A.stats[2], amb2);
-}
-
-size_t fused_lds(const RouteArgs& a, int D) {
-    return 2 * 64 * (size_t)D * 2 + sizeof(uint2) * kRows * kSvStride + sizeof(float) * kRows + 3 * sizeof(int) * kRows +
-           sizeof(int) * (2 * kMaxSel + 8 + kRows) + sizeof(float) * 4 +
-           2 * sizeof(int) * (size_t)a.SPP + sizeof(uint32_t) * kRows * (size_t)a.BW;
 }
 
 template <int DH, bool LONG>
@@ -2262,7 +2311,7 @@ extern "C" int hga_route_prefill(const hga_config* cfg, int32_t S, const void* q
             f.SPP = (pm > T2max ? pm : T2max) + 1;
             f.BW = (f.SPP + 31) / 32;
             f.BW2 = (T2max + 1 + 31) / 32;
-            const size_t lds = fused_lds(f, D);
+            const size_t lds = fused_lds(f, D, lng);
             HGA_REQUIRE(lds <= 163840, HGA_ERR_UNSUPPORTED, "hga_route_prefill: %zu bytes of LDS", lds);
             if (lng)
                 return D == 128 ? launch_route_fused<128, true>(f, lds, n_hi - n_lo, st)
