@@ -1415,6 +1415,43 @@ __device__ __forceinline__ void sort64_q4(uint32_t (&S)[16], int qd) {
         q4_inlane<8>(S); q4_inlane<4>(S); q4_inlane<2>(S); q4_inlane<1>(S);
     }
 }
+// The 32nd and 33rd largest of the 64 keys of each row (the split at the middle, on all four
+// lanes of the row), without the rest of the sort: the two 32-key halves are sorted (as in
+// sort64_q4), and the first size-64 step leaves the 32 largest keys on lanes qd >= 2 and the 32
+// smallest on lanes qd < 2, so the 32nd largest is the minimum of the upper lanes and the 33rd the
+// maximum of the lower ones.
+__device__ __forceinline__ void split64_q4(uint32_t (&S)[16], int qd, uint32_t& k32, uint32_t& k33) {
+    q4_inlane<1>(S);
+    q4_inlane<3>(S); q4_inlane<1>(S);
+    q4_inlane<7>(S); q4_inlane<2>(S); q4_inlane<1>(S);
+    q4_inlane<15>(S); q4_inlane<4>(S); q4_inlane<2>(S); q4_inlane<1>(S);
+    uint32_t P[16];
+    {
+        const uint32_t lower = cx_mask((qd & 1) == 0);
+#pragma unroll
+        for (int i = 0; i < 16; ++i) P[i] = q4_x16(S[15 - i]);
+#pragma unroll
+        for (int i = 0; i < 16; ++i) S[i] = cx(S[i], P[i], lower);
+        q4_inlane<8>(S); q4_inlane<4>(S); q4_inlane<2>(S); q4_inlane<1>(S);
+    }
+    const uint32_t lower = cx_mask(qd < 2);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) P[i] = (uint32_t)__shfl_xor((int)S[15 - i], 48, kWave);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) S[i] = cx(S[i], P[i], lower);
+    uint32_t mn = S[0], mx = S[0];
+#pragma unroll
+    for (int i = 1; i < 16; ++i) {
+        mn = min(mn, S[i]);
+        mx = max(mx, S[i]);
+    }
+    mn = min(mn, q4_x16(mn));                       // lanes qd >= 2: the 32nd largest
+    mx = max(mx, q4_x16(mx));                       // lanes qd < 2: the 33rd largest
+    const uint32_t mn_o = (uint32_t)__shfl_xor((int)mn, 32, kWave);
+    const uint32_t mx_o = (uint32_t)__shfl_xor((int)mx, 32, kWave);
+    k32 = qd >= 2 ? mn : mn_o;
+    k33 = qd < 2 ? mx : mx_o;
+}
 // Element pos (0..63, uniform) of each row after sort64_q4, on all four lanes of the row.
 __device__ __forceinline__ uint32_t q4_pick(const uint32_t (&S)[16], int pos, int qd) {
     uint32_t v = 0u;
@@ -1679,17 +1716,21 @@ __device__ __forceinline__ int fused_pool_fast(int P, int k, const uint32_t* sPk
     uint32_t x = 1u;                                      // members: keys >= x
     if (nreq > k) {
         // a threshold T leaving k < count(key >= T) <= 32 requested candidates
+        // (the probe positions are a search seed only: approximate instructions are fine, the
+        // threshold found is exact by its count)
         s1 = wsum(s1);
         s2 = wsum(s2);
-        const float mu = s1 / (float)nreq;
-        const float sd = sqrtf(fmaxf(s2 / (float)nreq - mu * mu, 0.0f));
+        const float rn = __builtin_amdgcn_rcpf((float)nreq);
+        const float mu = s1 * rn;
+        const float sd = __builtin_amdgcn_sqrtf(fmaxf(s2 * rn - mu * mu, 0.0f));
+        const float rsd = __builtin_amdgcn_rcpf(sd > 0.0f ? sd : 1.0f);
         const float target = 0.5f * (float)(k + 1 + 32);
         uint32_t T = 1u;
         bool ok = nreq <= 32;
-        float xf = mu + z_upper((target + 0.5f) / (float)nreq) * sd, lf = 0.0f, hf = 0.0f;
+        float xf = mu + z_upper_fast((target + 0.5f) * rn) * sd, lf = 0.0f, hf = 0.0f;
         int clo = -1, chi = -1;
         for (int it = 0; it < 8 && !ok; ++it) {
-            const uint32_t tx = min(max(okey(xf), 1u), 0xfffffffeu);
+            const uint32_t tx = min(max(okey_fast(xf), 1u), 0xfffffffeu);
             int c = 0;
 #pragma unroll
             for (int j = 0; j < J; ++j)
@@ -1706,12 +1747,11 @@ __device__ __forceinline__ int fused_pool_fast(int P, int k, const uint32_t* sPk
                     chi = c;
                 }
                 if (clo >= 0 && chi >= 0) {
-                    xf = lf + (hf - lf) * ((float)clo - target) / (float)(clo - chi);
+                    xf = lf + (hf - lf) * ((float)clo - target) * __builtin_amdgcn_rcpf((float)(clo - chi));
                 } else {
-                    const float z = (xf - mu) / (sd > 0.0f ? sd : 1.0f);
-                    const float dens = (float)nreq * 0.39894228f * expf(-0.5f * z * z) /
-                                       (sd > 0.0f ? sd : 1.0f);
-                    const float step = ((float)c - target) / fmaxf(dens, 1e-30f);
+                    const float z = (xf - mu) * rsd;
+                    const float dens = (float)nreq * 0.39894228f * __expf(-0.5f * z * z) * rsd;
+                    const float step = ((float)c - target) * __builtin_amdgcn_rcpf(fmaxf(dens, 1e-30f));
                     xf += fminf(fmaxf(step, -2.0f * sd), 2.0f * sd);
                 }
             }
@@ -1884,8 +1924,7 @@ void route_fused_kernel(RouteArgs A) {
     // reads q again for stage 2 (from L2: a plain load here allocates it there) rather than keep
     // it in registers through the stage-1 selection, whose out-of-line calls would have to save
     // it; the LONG variant streams q once (non-temporal, so its larger summaries stay in L2)
-    bf16x8 qb[KS];
-    auto load_q = [&](const uint16_t* qp, bool nt, float* sumsq) __attribute__((always_inline)) {
+    auto load_q = [&](bf16x8 (&qb)[KS], const uint16_t* qp, bool nt, float* sumsq) __attribute__((always_inline)) {
         float x = 0.0f;
 #pragma unroll
         for (int ks = 0; ks < KS; ++ks) {
@@ -1902,8 +1941,9 @@ void route_fused_kernel(RouteArgs A) {
         if (sumsq) *sumsq = x;
     };
     {
+        bf16x8 qn[KS];
         float x = 0.0f;
-        load_q(qg, LONG, &x);
+        load_q(qn, qg, LONG, &x);
         x = q4_fsum(x);
         if (qd == 0) sQn[t] = __builtin_sqrtf(x);
     }
@@ -1932,6 +1972,14 @@ void route_fused_kernel(RouteArgs A) {
             __syncthreads();                      // the previous segment's stages are read
             stage_rows<DH, SR>(pool, [&](int r) { return (uint32_t)((c0 + r) * DH * 2); }, ncs,
                                stage_lds, w);
+        }
+        // q as the B operand, read per segment (L2 hits after the first): held through the
+        // scoring only, not through the selection of the segment's rows
+        bf16x8 qb[KS];
+        {
+            const uint16_t* qs = qg;
+            asm volatile("" : "+s"(qs));
+            load_q(qb, qs, LONG, nullptr);
         }
 #pragma unroll
         for (int g = 0; g < kSegTiles / GT; ++g) {
@@ -2072,6 +2120,13 @@ void route_fused_kernel(RouteArgs A) {
         (uint32_t)(uintptr_t)(__attribute__((address_space(3))) unsigned char*)sStage2;
     stage_rows<DH, 64>(gkb, [&](int r) { return (uint32_t)(((int64_t)sSel[r / M] * M + (r % M)) * DH * 2); },
                        T2, stage2_lds, w);
+    bf16x8 qb2[KS];
+    {
+        // q again, in flight with the group rows (the wait below covers both)
+        const uint16_t* qg2 = qg;
+        asm volatile("" : "+s"(qg2));            // a fresh read: q is not kept from stage 1
+        if (wave_act) load_q(qb2, qg2, LONG, nullptr);
+    }
     for (int i = threadIdx.x; i < T2 + 1; i += kFThreads) {
         sPk[i] = 0u;
         sFirst[i] = kNoRow;
@@ -2091,12 +2146,7 @@ void route_fused_kernel(RouteArgs A) {
         int nv2 = 0;
         float s1 = 0.0f, s2 = 0.0f;
         int ns = 0;
-        if constexpr (!LONG) {
-            const uint16_t* qg2 = qg;
-            asm volatile("" : "+s"(qg2));        // a fresh read: q is not kept from stage 1
-            load_q(qg2, false, nullptr);
-        }
-        stage_scores<DH, 16, 4>(sStage2, 0, 0, T2, w, nwact, qb, scale, kv2, knmax2, s1, s2, ns);
+        stage_scores<DH, 16, 4>(sStage2, 0, 0, T2, w, nwact, qb2, scale, kv2, knmax2, s1, s2, ns);
         // candidate c is visible to row t from its parent's first row on
         ns = 0;
 #pragma unroll
@@ -2114,9 +2164,13 @@ void route_fused_kernel(RouteArgs A) {
             uint32_t S[16];
 #pragma unroll
             for (int i = 0; i < 16; ++i) S[i] = kv2[i];
-            sort64_q4(S, qd);
-            kth2 = q4_pick(S, 64 - A.Kgr, qd);
-            k1th2 = q4_pick(S, 63 - A.Kgr, qd);
+            if (A.Kgr == 32) {
+                split64_q4(S, qd, kth2, k1th2);
+            } else {
+                sort64_q4(S, qd);
+                kth2 = q4_pick(S, 64 - A.Kgr, qd);
+                k1th2 = q4_pick(S, 63 - A.Kgr, qd);
+            }
         }
         knmax2 = wmax(knmax2);
     }
