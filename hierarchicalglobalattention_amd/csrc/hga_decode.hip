@@ -822,6 +822,35 @@ __device__ __forceinline__ void load_slice(const typename Elem<DT>::T* p, float 
     }
 }
 
+// A lane's DPL elements of a key or value row as loaded (bf16 pairs or fp32 words), widened to
+// fp32 on use exactly as load_slice does.
+template <int DT, int DPL>
+struct RawSlice {
+    static constexpr int NW = DT == HGA_DTYPE_BF16 ? DPL / 2 : DPL;
+    uint32_t w[NW];
+    __device__ __forceinline__ void load(const typename Elem<DT>::T* p) {
+        if constexpr (DT == HGA_DTYPE_BF16 && DPL == 8) {
+            const uint4 u = *reinterpret_cast<const uint4*>(p);
+            w[0] = u.x; w[1] = u.y; w[2] = u.z; w[3] = u.w;
+        } else if constexpr (DT == HGA_DTYPE_BF16) {
+            const uint2 u = *reinterpret_cast<const uint2*>(p);
+            w[0] = u.x; w[1] = u.y;
+        } else {
+#pragma unroll
+            for (int e = 0; e < DPL; e += 4) {
+                const uint4 u = *reinterpret_cast<const uint4*>(p + e);
+                w[e] = u.x; w[e + 1] = u.y; w[e + 2] = u.z; w[e + 3] = u.w;
+            }
+        }
+    }
+    __device__ __forceinline__ float at(int e) const {
+        if constexpr (DT == HGA_DTYPE_BF16)
+            return __uint_as_float((e & 1) ? (w[e >> 1] & 0xffff0000u) : (w[e >> 1] << 16));
+        else
+            return __uint_as_float(w[e]);
+    }
+};
+
 template <int DT, int DH, bool DCA>
 __global__ __launch_bounds__(kDT) void attend_decode_split_kernel(DecAttnArgs A, float* part,
                                                                   int nsplit) {
@@ -892,21 +921,30 @@ __global__ __launch_bounds__(kDT) void attend_decode_split_kernel(DecAttnArgs A,
 #pragma unroll
         for (int e = 0; e < DPL; ++e) acc[e] = 0.0f;
         for (int i0 = 0; i0 < KPG; i0 += U) {
-            const T* vp[U];
-            float s[U];
+            // the U keys' K and V slices are loaded together: one memory round trip per U keys
+            RawSlice<DT, DPL> kxs[U], vxs[U];
+            bool visu[U];
 #pragma unroll
             for (int u = 0; u < U; ++u) {
                 const int k = gk0 + i0 + u, kl = G * KPG + i0 + u;   // kl: key within the split
-                const T* kp = reinterpret_cast<const T*>(sKP[kl]);
-                vp[u] = reinterpret_cast<const T*>(sVP[kl]);
-                const int thr = sKT[kl];
+                visu[u] = k < keys.n && row >= sKT[kl];
+                if (visu[u]) {
+                    kxs[u].load(reinterpret_cast<const T*>(sKP[kl]) + j * DPL);
+                    vxs[u].load(reinterpret_cast<const T*>(sVP[kl]) + j * DPL);
+                }
+            }
+            float s[U];
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const int kl = G * KPG + i0 + u;
                 int64_t kpos = 0;
                 if constexpr (DCA) kpos = sKX[kl];
                 float d = 0.0f;
-                const bool vis = k < keys.n && row >= thr;
+                const bool vis = visu[u];
                 if (vis) {
                     float kx[DPL];
-                    load_slice<DT, DPL>(kp + j * DPL, kx);
+#pragma unroll
+                    for (int e = 0; e < DPL; ++e) kx[e] = kxs[u].at(e);
                     if constexpr (DCA) {
                         const int r = dca_regime(kpos, A.start_pos + row, A.dca_chunk);
 #pragma unroll
@@ -921,7 +959,6 @@ __global__ __launch_bounds__(kDT) void attend_decode_split_kernel(DecAttnArgs A,
                 }
                 d = r16_sum_f(d);                    // whole group: uniform control flow
                 s[u] = vis ? d * A.scale : -INFINITY;
-                if (!vis) vp[u] = nullptr;
             }
             float mx = m_run;
 #pragma unroll
@@ -935,11 +972,9 @@ __global__ __launch_bounds__(kDT) void attend_decode_split_kernel(DecAttnArgs A,
             for (int u = 0; u < U; ++u) {
                 const float p = expf(s[u] - m_use);
                 l_run += p;
-                if (vp[u]) {
-                    float vx[DPL];
-                    load_slice<DT, DPL>(vp[u] + j * DPL, vx);
+                if (visu[u]) {
 #pragma unroll
-                    for (int e = 0; e < DPL; ++e) acc[e] = fmaf(p, vx[e], acc[e]);
+                    for (int e = 0; e < DPL; ++e) acc[e] = fmaf(p, vxs[u].at(e), acc[e]);
                 }
             }
             m_run = mx;
