@@ -1841,6 +1841,14 @@ __device__ __noinline__ int fused_pool_general(int P, int k, int rows, const uin
 // first requesting rows, request bits) there once stage-1 scoring is over, and stages stage 2's
 // group rows in the survivor area, which is free by then: about 51 KB (Dh 128), three
 // workgroups per CU.
+// The ordinary variant's layout is fixed at its largest pool (kFusedMaxPool chunks), so that every
+// LDS array sits at a compile-time offset.
+constexpr int kSPPo = kFusedMaxPool + 1;                       // pooled slots (ordinary variant)
+constexpr int kBWo = (kSPPo + 31) / 32;                        // request-bit words per row
+constexpr int kPooledO = (8 * kSPPo + 4 * kRows * kBWo + 15) & ~15;
+constexpr int fused_region(int D) {
+    return kPooledO > 2 * kFStageRows * D * 2 ? kPooledO : 2 * kFStageRows * D * 2;
+}
 size_t fused_lds(const RouteArgs& a, int D, bool lng) {
     const size_t stage = 2 * (size_t)kFStageRows * D * 2;
     const size_t pooled = 2 * sizeof(int) * (size_t)a.SPP + sizeof(uint32_t) * kRows * (size_t)a.BW;
@@ -1848,7 +1856,7 @@ size_t fused_lds(const RouteArgs& a, int D, bool lng) {
                         sizeof(int) * (2 * kMaxSel + 8 + kRows) + sizeof(float) * 4;
     const size_t surv = sizeof(uint2) * kRows * kSvStride;
     if (lng) return stage + surv + misc + pooled;
-    return (stage > ((pooled + 15) & ~(size_t)15) ? stage : ((pooled + 15) & ~(size_t)15)) + surv + misc;
+    return (size_t)fused_region(D) + surv + misc;
 }
 
 template <int DH, bool LONG>
@@ -1861,8 +1869,7 @@ void route_fused_kernel(RouteArgs A) {
     constexpr int kStageBytes = SR * DH * 2;
     extern __shared__ __align__(16) unsigned char smem_raw[];
     unsigned char* sStage = smem_raw;                                  // [2][SR][DH] candidate rows
-    const int pooled_bytes = (8 * A.SPP + 4 * kRows * A.BW + 15) & ~15;
-    const int region = LONG || pooled_bytes < 2 * kStageBytes ? 2 * kStageBytes : pooled_bytes;
+    constexpr int region = LONG ? 2 * kStageBytes : fused_region(DH);
     uint2* sSv = reinterpret_cast<uint2*>(sStage + region);            // [64][kSvStride] survivors
     // stage 2's group rows: the survivor area (ordinary) or the two stages (LONG)
     unsigned char* sStage2 = LONG ? sStage : reinterpret_cast<unsigned char*>(sSv);
@@ -1878,8 +1885,8 @@ void route_fused_kernel(RouteArgs A) {
     // pooled state (zeroed once stage-1 scoring is over): [SPP] pooled key, [SPP] first
     // requesting row, [64][BW] request bits
     uint32_t* sPk = LONG ? reinterpret_cast<uint32_t*>(sKn + 4) : reinterpret_cast<uint32_t*>(smem_raw);
-    int* sFirst = reinterpret_cast<int*>(sPk + A.SPP);
-    uint32_t* sBits = reinterpret_cast<uint32_t*>(sFirst + A.SPP);
+    int* sFirst = reinterpret_cast<int*>(sPk + (LONG ? A.SPP : kSPPo));
+    uint32_t* sBits = reinterpret_cast<uint32_t*>(sFirst + (LONG ? A.SPP : kSPPo));
 
     const int N = A.N, C = A.C, M = A.M, BW = A.BW;
     const int n = A.n_hi - 1 - (int)(blockIdx.x / (A.B * A.H));       // heavy chunks first
@@ -2365,6 +2372,8 @@ extern "C" int hga_route_prefill(const hga_config* cfg, int32_t S, const void* q
             f.SPP = (pm > T2max ? pm : T2max) + 1;
             f.BW = (f.SPP + 31) / 32;
             f.BW2 = (T2max + 1 + 31) / 32;
+            HGA_REQUIRE(lng || (f.SPP <= kSPPo && f.BW <= kBWo), HGA_ERR_UNSUPPORTED,
+                        "hga_route_prefill: pooled state of %d slots exceeds the fused layout", f.SPP);
             const size_t lds = fused_lds(f, D, lng);
             HGA_REQUIRE(lds <= 163840, HGA_ERR_UNSUPPORTED, "hga_route_prefill: %zu bytes of LDS", lds);
             if (lng)
