@@ -442,16 +442,16 @@ def main():
     t_route, t_attn = g["stage_ms"]["route"], g["stage_ms"]["attention"]
     attn_tflops = g["flops"] / (t_attn * 1e-3) / 1e12
     route_gbs = g["route_bytes"] / (t_route * 1e-3) / 1e9
+    roofline_route = {"kernel": "route_fused_kernel<128, false>",
+                      "bound": "hbm",
+                      "achieved": route_gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                      "frac": route_gbs / HBM_PEAK_GBS, "traffic": _measured_traffic("route"),
+                      "algorithmic_bytes": g["route_bytes"],
+                      "score_mfma_tflops": g["score_flops"] / (t_route * 1e-3) / 1e12,
+                      "score_mfma_frac": g["score_flops"] / (t_route * 1e-3) / 1e12
+                                         / MFMA_BF16_PEAK_TFLOPS}
     if t_route >= t_attn:
-        traffic = _measured_traffic("route")
-        roofline = {"kernel": "route_fused_kernel<128, false>",
-                    "bound": "hbm",
-                    "achieved": route_gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                    "frac": route_gbs / HBM_PEAK_GBS, "traffic": traffic,
-                    "algorithmic_bytes": g["route_bytes"],
-                    "score_mfma_tflops": g["score_flops"] / (t_route * 1e-3) / 1e12,
-                    "score_mfma_frac": g["score_flops"] / (t_route * 1e-3) / 1e12
-                                       / MFMA_BF16_PEAK_TFLOPS}
+        roofline = roofline_route
     else:
         traffic = _measured_traffic("attention")
         roofline = {"kernel": "kv_block_kernel + attend_v3_kernel<128, 2>", "bound": "mfma",
@@ -497,6 +497,7 @@ def main():
                    "topk_chunks": CFG["tc"], "topk_groups": CFG["tg"], "rope_theta": CFG["theta"]},
         "stages_ms": g["stage_ms"],
         "roofline": roofline,
+        "roofline_route": roofline_route,
         "roofline_attention": {"kernel": "kv_block_kernel + attend_v3_kernel<128, 2>",
                                "bound": "mfma", "achieved": attn_tflops,
                                "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
