@@ -1404,6 +1404,118 @@ __global__ __launch_bounds__(kGT) void gather_copy_kernel(GatherArgs A) {
     }
 }
 
+// Exclusive prefix sum over the kGT threads of a workgroup (wave scans, then the wave totals).
+__device__ __forceinline__ int block_excl_scan(int x, int* sWave) {
+    const int l = lane_id(), w = (int)threadIdx.x / kWave;
+    int inc = x;
+#pragma unroll
+    for (int d = 1; d < kWave; d <<= 1) {
+        const int y = __shfl_up(inc, d, kWave);
+        if (l >= d) inc += y;
+    }
+    if (l == kWave - 1) sWave[w] = inc;
+    __syncthreads();
+    int base = 0;
+    for (int i = 0; i < w; ++i) base += sWave[i];
+    return base + inc - x;
+}
+
+// Plan and copy in one launch, for B * KVH * ceil(NG / 32) <= kFusedPlanWords: every workgroup
+// marks the valid opened groups of all (b, kv head) pairs in an LDS bitmap (words of pair bk at
+// bk * NW ..), takes an exclusive prefix of the words' popcounts -- a group's staging slot in its
+// pair is its rank among the pair's marked ids, as in gather_plan_kernel -- and copies its share
+// of the flattened slots; workgroup 0 also writes every opened group's slot.
+constexpr int kFusedPlanWords = 4096;
+__global__ __launch_bounds__(kGT) void gather_fused_kernel(GatherArgs A) {
+    extern __shared__ uint32_t sBmF[];                 // [nw] bitmap, [nw + 1] prefix, [4] waves
+    const int G = gridDim.x, nbk = A.B * A.KVH, tid = threadIdx.x;
+    const int NW = (A.NG + 31) / 32, nw = nbk * NW;
+    int* sPre = reinterpret_cast<int*>(sBmF + nw);
+    int* sWave = sPre + nw + 1;
+    for (int i = tid; i < nw; i += kGT) sBmF[i] = 0u;
+    __syncthreads();
+    const int Kgw = A.Kg > 0 ? A.Kg : 1, n_ent = A.B * A.H * A.Kg;
+    for (int e = tid; e < n_ent; e += kGT) {
+        const int bh = e / A.Kg, b = bh / A.H, h = bh % A.H;
+        const int64_t idx = (int64_t)bh * Kgw + e % A.Kg;
+        const int g = A.open_grp[idx];
+        if (g >= 0 && g < A.NG && A.open_thr[idx] >= 0)
+            atomicOr(&sBmF[(b * A.KVH + h / A.rep) * NW + (g >> 5)], 1u << (g & 31));
+    }
+    __syncthreads();
+    const int per = (nw + kGT - 1) / kGT;
+    const int w0 = tid * per < nw ? tid * per : nw, w1 = w0 + per < nw ? w0 + per : nw;
+    int part = 0;
+    for (int i = w0; i < w1; ++i) part += __popc(sBmF[i]);
+    int run = block_excl_scan(part, sWave);
+    for (int i = w0; i < w1; ++i) {
+        sPre[i] = run;
+        run += __popc(sBmF[i]);
+    }
+    if (tid == kGT - 1) sPre[nw] = run;
+    __syncthreads();
+    const int total = sPre[nw];
+    if (blockIdx.x == 0) {
+        for (int e = tid; e < n_ent; e += kGT) {
+            const int bh = e / A.Kg, b = bh / A.H, h = bh % A.H;
+            const int64_t idx = (int64_t)bh * Kgw + e % A.Kg;
+            const int g = A.open_grp[idx];
+            int slot = -1;
+            if (g >= 0 && g < A.NG && A.open_thr[idx] >= 0) {
+                const int bk = b * A.KVH + h / A.rep, wi = bk * NW + (g >> 5);
+                slot = sPre[wi] - sPre[bk * NW] + __popc(sBmF[wi] & ((1u << (g & 31)) - 1u));
+            }
+            A.staged_grp[idx] = slot;
+        }
+    }
+    const int vpr = A.D * A.esz / 16;                  // 16-byte pieces per row
+    const int pieces = A.gs * vpr;                     // of one group's K (or V)
+    for (int v0 = blockIdx.x; v0 < total; v0 += 4 * G) {
+        int64_t src[4], dst[4];
+        bool ok[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int v = v0 + j * G;
+            ok[j] = v < total;
+            // the bitmap word holding slot v: the last one whose prefix is <= v (a word with
+            // marked groups, since the prefix rises past v there)
+            int lo = 0, hi = nw - 1;
+            while (lo < hi) {
+                const int mid = (lo + hi + 1) >> 1;
+                if (sPre[mid] <= v) lo = mid;
+                else hi = mid - 1;
+            }
+            const int bk = lo / NW;
+            uint32_t bits = ok[j] ? sBmF[lo] : 0u;
+            for (int r = ok[j] ? v - sPre[lo] : 0; r > 0; --r) bits &= bits - 1u;   // r-th set bit
+            const int g = (lo % NW) * 32 + (bits ? __builtin_ctz(bits) : 0);
+            const int u = ok[j] ? v - sPre[bk * NW] : 0;
+            const int b = bk / A.KVH, kvh = bk % A.KVH;
+            const int64_t p0 = (int64_t)(g / A.M) * A.C + (int64_t)(g % A.M) * A.gs;
+            src[j] = ((int64_t)b * A.d_sb + (int64_t)kvh * A.d_sh + p0 * A.d_ss) * A.esz;
+            dst[j] = (((int64_t)bk * A.U + u) * A.gs) * (int64_t)A.D * A.esz;
+        }
+        for (int c = tid; c < pieces; c += kGT) {
+            const int r = c / vpr, x = (c % vpr) * 16;
+            const int64_t so = (int64_t)r * A.d_ss * A.esz + x;
+            const int64_t dO = (int64_t)r * A.D * A.esz + x;
+            uint4 kq[4], vq[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                if (ok[j]) {
+                    kq[j] = *reinterpret_cast<const uint4*>(A.kd + src[j] + so);
+                    vq[j] = *reinterpret_cast<const uint4*>(A.vd + src[j] + so);
+                }
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                if (ok[j]) {
+                    *reinterpret_cast<uint4*>(A.stage_k + dst[j] + dO) = kq[j];
+                    *reinterpret_cast<uint4*>(A.stage_v + dst[j] + dO) = vq[j];
+                }
+        }
+    }
+}
+
 }  // namespace
 }  // namespace hga
 
@@ -1511,6 +1623,13 @@ extern "C" int hga_gather_decode(const hga_config* cfg, int32_t n_closed, const 
     HGA_REQUIRE(lds <= 65536, HGA_ERR_UNSUPPORTED, "hga_gather_decode: %d closed chunks too many",
                 n_closed);
     hipStream_t st = (hipStream_t)stream;
+    const int64_t nwf = (int64_t)a.B * a.KVH * NW;
+    if (Kg > 0 && n_closed > 0 && nwf <= kFusedPlanWords) {
+        // plan and copy in one launch
+        const size_t lds_f = sizeof(uint32_t) * (2 * (size_t)nwf + 1 + kGT / kWave);
+        gather_fused_kernel<<<dim3((unsigned)kGatherWG), dim3(kGT), lds_f, st>>>(a);
+        return launch_status("hga_gather_decode (plan + copy)");
+    }
     gather_plan_kernel<<<dim3((unsigned)(a.B * a.KVH)), dim3(kGT), lds, st>>>(a);
     rc = launch_status("hga_gather_decode (plan)");
     if (rc) return rc;

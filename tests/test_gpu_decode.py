@@ -386,12 +386,16 @@ def test_attend_decode_vs_oracle(case, tier):
         assert d.max() <= F32_TOL, d.max()
 
 
-@pytest.mark.parametrize("on_host", [True, False])
-def test_gather_decode_contents(on_host):
+@pytest.mark.parametrize("on_host,n_closed", [(True, 40), (False, 40), (False, 8200)])
+def test_gather_decode_contents(on_host, n_closed):
     """Staged groups are the record's groups, one slot per distinct (b, kv head, group) in
-    ascending group order; every opened entry maps to its group's slot, padding to -1."""
+    ascending group order; every opened entry maps to its group's slot, padding to -1.  At 40
+    closed chunks the plan and the copy run in one launch; at 8200 (a group bitmap of more than
+    4096 words over the (b, kv head) pairs) they run as two."""
     B, H, KVH, Dh, C, gs, tc, tg, kf, kl = 2, 8, 2, 128, 64, 16, 8, 16, 1, 2
-    n_closed, dt = 40, torch.bfloat16
+    dt = torch.bfloat16
+    if n_closed > 1000:
+        Dh = 64
     M = C // gs
     gen = torch.Generator().manual_seed(17)
     cfg = _cfg(B, H, KVH, Dh, C, gs, tc, tg, kf, kl, dt)
