@@ -779,11 +779,15 @@ __global__ __launch_bounds__(kDT) void attend_decode_kernel(DecAttnArgs A) {
 
 // ------------------------------------------------------------------------------------------
 // split decode attention (head_dim 64 / 128): the key sequence of each (b, head) in splits of
-// kSplitKeys keys, one workgroup per split; 16 lanes per key (a lane holds head_dim/16
-// consecutive dims, so a key row is one contiguous read), 16 keys per 16-lane group, four in
-// flight.  Each split writes its (max, sum, accumulator) partial; decode_combine_kernel merges.
+// SK keys (kSplitKeys or kWideSplitKeys), one workgroup per split; 16 lanes per key (a lane
+// holds head_dim/16 consecutive dims, so a key row is one contiguous read), SK / 16 keys per
+// 16-lane group, four in flight.  Each split writes its (max, sum, accumulator) partial; decode_combine_kernel merges.
 // ------------------------------------------------------------------------------------------
 constexpr int kSplitKeys = 256;
+// One-token steps of large batches (B * H >= kWideSplitHeads) take splits of twice as many keys:
+// half the workgroups, each locating its keys and merging its groups once for twice the work.
+constexpr int kWideSplitKeys = 512;
+constexpr int kWideSplitHeads = 512;
 
 // Sum over the 16 lanes of a DPP row, bit-identical in all of them (butterfly: xor 1, xor 2,
 // half-row mirror, row mirror).
@@ -851,22 +855,22 @@ struct RawSlice {
     }
 };
 
-template <int DT, int DH, bool DCA>
+template <int DT, int DH, bool DCA, int SK>
 __global__ __launch_bounds__(kDT) void attend_decode_split_kernel(DecAttnArgs A, float* part,
                                                                   int nsplit) {
     typedef typename Elem<DT>::T T;
     constexpr int DPL = DH / 16;
     constexpr int NG = kDT / 16;                     // 16-lane groups per workgroup
-    constexpr int KPG = kSplitKeys / NG;             // keys per group
+    constexpr int KPG = SK / NG;                     // keys per group
     constexpr int U = 4;                             // keys in flight per group
     constexpr int NQ = DCA ? 3 : 1;                  // query versions
-    static_assert(kDT == kSplitKeys, "one thread locates each key of a split");
+    static_assert(SK % kDT == 0, "every thread locates SK / kDT keys of a split");
     __shared__ int sOG[256], sOT[256], sOP[DCA ? 256 : 1];
     __shared__ float sM[NG], sL[NG];
     __shared__ float sAcc[NG][DH];
     // the split's keys, located once: K and V row addresses, first visible row, position
-    __shared__ unsigned long long sKP[kSplitKeys], sVP[kSplitKeys];
-    __shared__ int sKT[kSplitKeys], sKX[DCA ? kSplitKeys : 1];
+    __shared__ unsigned long long sKP[SK], sVP[SK];
+    __shared__ int sKT[SK], sKX[DCA ? SK : 1];
     __shared__ int sNopen;
     int split, bh;
     xcd_item(split, bh);
@@ -890,20 +894,21 @@ __global__ __launch_bounds__(kDT) void attend_decode_split_kernel(DecAttnArgs A,
     DecKeys<T> keys;
     keys.init(A, b, kvh, sOG, sOT, sNopen, ph);
     if constexpr (DCA) keys.sOP = sOP;
-    {
-        const int k = split * kSplitKeys + (int)threadIdx.x;
+#pragma unroll
+    for (int t = (int)threadIdx.x; t < SK; t += kDT) {
+        const int k = split * SK + t;
         const T* kp = nullptr;
         const T* vp = nullptr;
         int thr = kNoRow;
         int64_t kpos = 0;
         if (k < keys.n) keys.locate(k, kp, vp, thr, kpos);
-        sKP[threadIdx.x] = (unsigned long long)kp;
-        sVP[threadIdx.x] = (unsigned long long)vp;
-        sKT[threadIdx.x] = k < keys.n ? thr : kNoRow;
-        if constexpr (DCA) sKX[threadIdx.x] = (int)kpos;
+        sKP[t] = (unsigned long long)kp;
+        sVP[t] = (unsigned long long)vp;
+        sKT[t] = k < keys.n ? thr : kNoRow;
+        if constexpr (DCA) sKX[t] = (int)kpos;
     }
     __syncthreads();
-    const int gk0 = split * kSplitKeys + G * KPG;
+    const int gk0 = split * SK + G * KPG;
     const T* qg = reinterpret_cast<const T*>(A.q) + b * A.q_sb + h * A.q_sh;
     for (int row = 0; row < A.L; ++row) {
         float qvs[NQ][DPL];
@@ -1520,18 +1525,25 @@ __global__ __launch_bounds__(kGT) void gather_fused_kernel(GatherArgs A) {
 }  // namespace hga
 
 namespace {
-// Splits (kSplitKeys keys each) of the split decode attention: phase 1 the windows and the
-// active chunk, phase 2 the opened groups of the longest list (every slot valid), phase 0 both;
-// the workspace holds the partials of all of them.
+// Keys per split: kWideSplitKeys for one-token steps of B * H >= kWideSplitHeads (these take
+// the VALU split kernel), else kSplitKeys.
+int split_keys(const hga_config* cfg, int32_t L) {
+    return L == 1 && (int64_t)cfg->batch * cfg->heads >= hga::kWideSplitHeads ? hga::kWideSplitKeys
+                                                                               : hga::kSplitKeys;
+}
+// Splits of the split decode attention: phase 1 the windows and the active chunk, phase 2 the
+// opened groups of the longest list (every slot valid), phase 0 both; the workspace holds the
+// partials of all of them.
 int decode_splits(const hga_config* cfg, int32_t L, int32_t n_closed, int64_t start_pos,
                   int32_t Kg, int phase) {
+    const int sk = split_keys(cfg, L);
     int f_hi, l_lo;
     hga::windows(n_closed, cfg->keep_first, cfg->keep_last, &f_hi, &l_lo);
     const int64_t C = cfg->chunk_size;
     const int64_t c0 = start_pos - (int64_t)n_closed * C;
     const int64_t win = (int64_t)f_hi * C + (int64_t)(n_closed - l_lo) * C + c0 + L;
     const int64_t opened = (int64_t)(Kg > 0 ? Kg : 0) * cfg->group_size;
-    auto splits = [](int64_t keys) { return (keys + hga::kSplitKeys - 1) / hga::kSplitKeys; };
+    auto splits = [sk](int64_t keys) { return (keys + sk - 1) / sk; };
     if (phase == 1) return (int)splits(win);
     if (phase == 2) return (int)splits(opened);
     return (int)(splits(win) + splits(opened));
@@ -1912,6 +1924,7 @@ int attend_decode_impl(const hga_config* cfg, int32_t L, int32_t n_closed, int64
         // blocks of 8+ rows (bf16, aligned query rows): the MFMA split kernel
         const bool mfma = cfg->dtype == HGA_DTYPE_BF16 && L >= 8 &&
                           (dca || ((uintptr_t)q % 16 == 0 && ((q_sb | q_sh | q_ss) % 8) == 0));
+        const bool wide = split_keys(cfg, L) == kWideSplitKeys;   // never with the MFMA kernel (L 1)
 #define HGA_DS_CASE(DTV, DHV)                                                                    \
         if (cfg->dtype == DTV && D == DHV) {                                                   \
             if (nlaunch == 0) {                                                                 \
@@ -1927,8 +1940,13 @@ int attend_decode_impl(const hga_config* cfg, int32_t L, int32_t n_closed, int64
                     a, part, nsplit);                                                           \
             } else if (mfma && DTV == HGA_DTYPE_BF16)                                           \
                 attend_decode_mfma_kernel<DHV, false><<<g1, kDMT, 0, st>>>(a, part, nsplit);    \
-            else if (dca) attend_decode_split_kernel<DTV, DHV, true><<<g1, kDT, 0, st>>>(a, part, nsplit); \
-            else attend_decode_split_kernel<DTV, DHV, false><<<g1, kDT, 0, st>>>(a, part, nsplit); \
+            else if (wide && dca)                                                               \
+                attend_decode_split_kernel<DTV, DHV, true, kWideSplitKeys><<<g1, kDT, 0, st>>>(a, part, nsplit); \
+            else if (wide)                                                                      \
+                attend_decode_split_kernel<DTV, DHV, false, kWideSplitKeys><<<g1, kDT, 0, st>>>(a, part, nsplit); \
+            else if (dca)                                                                       \
+                attend_decode_split_kernel<DTV, DHV, true, kSplitKeys><<<g1, kDT, 0, st>>>(a, part, nsplit); \
+            else attend_decode_split_kernel<DTV, DHV, false, kSplitKeys><<<g1, kDT, 0, st>>>(a, part, nsplit); \
             rc = launch_status("hga_attend_decode (split)");                                    \
             if (rc) return rc;                                                                  \
             if (phase == 1) return HGA_OK;                                                      \
